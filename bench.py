@@ -1,0 +1,293 @@
+"""Benchmark of the gfx950 hot path on one MI355X.
+
+Headline workload: masked-tail bf16 row reductions
+on x[8191, 3000] -- one step = one LayerNorm pass + one softmax pass over one
+batch; value = algorithmic HBM bytes per step / step time (GB/s).  Inputs are
+resident in HBM before the timed region; the timed region rotates 4 buffer
+sets (~590 MB > the 256 MB Infinity Cache) so that successive steps cannot be
+served from MALL.
+
+The same line carries
+  * roofline: the dominant kernel's achieved GB/s (algorithmic bytes per launch
+    / its average launch time, HIP events on the launch stream) against the
+    8 TB/s HBM peak;
+  * cpu_baseline: the OpenMP fp32 CPU path (oracle/cpu_baseline.c, the a100c
+    worker-pool restatement) on the same workload, on this host's cores;
+  * suite: every other BASELINE config (fp32 RMSNorm/softmax GB/s, bf16 GEMM,
+    causal GQA attention and int8 GEMM TFLOP/s) with its own roofline fraction.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GEMM/attn TFLOP/s + norm/softmax HBM GB/s vs roofline, 1×MI355X"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFS = 2516.6   # dense, 256 CU x 2.4 GHz x 4096 FLOP/clk
+INT8_PEAK_TOPS = 5033.2  # dense, 8192 OP/clk/CU
+ROTATE = 4
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def event_time(torch, launch, iters, warmup):
+    """Average ms per call of ``launch(i)``, HIP events on the current stream."""
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(iters):
+        launch(i)
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def headline(torch, ops, args):
+    """Config 2: LayerNorm + softmax, bf16 [8191, 3000]."""
+    from oracle import inputs
+    rows, cols = 8191, 3000
+    dev = "cuda:0"
+    sets = []
+    for s in range(ROTATE):
+        c = inputs.config2(rows, cols, seed=inputs.SEEDS["c2"] + s)
+        bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
+        sets.append({
+            "x": bf(c["x"]), "g": bf(c["gamma"]), "b": bf(c["beta"]),
+            "y": torch.empty((rows, cols), dtype=torch.bfloat16, device=dev),
+            "s": torch.empty((rows, cols), dtype=torch.bfloat16, device=dev),
+            "mean": torch.empty(rows, dtype=torch.float32, device=dev),
+            "rstd": torch.empty(rows, dtype=torch.float32, device=dev),
+        })
+    eps = 1e-5
+    ln_bytes = 2 * rows * cols * 2 + 2 * cols * 2 + 2 * rows * 4
+    sm_bytes = 2 * rows * cols * 2
+
+    def ln(i):
+        d = sets[i % ROTATE]
+        ops.layernorm_kernel(d["x"], d["y"], d["g"], d["b"], d["mean"], d["rstd"], cols, cols, eps)
+
+    def sm(i):
+        d = sets[i % ROTATE]
+        ops.softmax_kernel(d["x"], d["s"], cols)
+
+    def step(i):
+        ln(i)
+        sm(i)
+
+    # per-kernel launch times (events around many launches of one kernel)
+    ln_ms = event_time(torch, ln, 200, 10)
+    ln_kernel = ops.rt.module().last_kernel
+    sm_ms = event_time(torch, sm, 200, 10)
+    sm_kernel = ops.rt.module().last_kernel
+
+    # the timed steps: barrier-free single process, synchronize on both sides
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        step(i)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(end) / args.steps
+    value = (ln_bytes + sm_bytes) / (ms_step * 1e-3) / 1e9
+    dom = ("layernorm", ln_kernel, ln_bytes, ln_ms) if ln_ms >= sm_ms else ("softmax", sm_kernel, sm_bytes, sm_ms)
+    achieved = dom[2] / (dom[3] * 1e-3) / 1e9
+    roof = {"bound": "hbm", "kernel": dom[1], "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "algorithmic_bytes": dom[2], "avg_launch_us": round(dom[3] * 1e3, 2)}
+    per_kernel = {
+        "layernorm": {"kernel": ln_kernel, "us": round(ln_ms * 1e3, 2),
+                      "GB/s": round(ln_bytes / (ln_ms * 1e-3) / 1e9, 1), "bytes": ln_bytes},
+        "softmax": {"kernel": sm_kernel, "us": round(sm_ms * 1e3, 2),
+                    "GB/s": round(sm_bytes / (sm_ms * 1e-3) / 1e9, 1), "bytes": sm_bytes},
+    }
+    del sets
+    return value, ms_step, wall, roof, per_kernel, ln_bytes + sm_bytes
+
+
+def cpu_baseline(seconds=10.0):
+    """OpenMP fp32 CPU path on config 2 (full workload, repeated ~`seconds`)."""
+    from oracle import build as obuild
+    from oracle import inputs
+    from oracle.reference import bf16_bits
+    lib = obuild.load()
+    rows, cols = 8191, 3000
+    c = inputs.config2(rows, cols)
+    x = bf16_bits(c["x"])
+    g, b = bf16_bits(c["gamma"]), bf16_bits(c["beta"])
+    y = np.empty_like(x)
+    s = np.empty_like(x)
+    mean = np.empty(rows, np.float32)
+    rstd = np.empty(rows, np.float32)
+    p = lambda a: a.ctypes.data  # noqa: E731
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        lib.g950o_layernorm_bf16(p(x), p(g), p(b), p(y), p(mean), p(rstd), rows, cols, 1e-5)
+        lib.g950o_softmax_bf16(p(x), p(s), rows, cols)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 1000:
+            break
+    nbytes = (2 * rows * cols * 2 + 2 * cols * 2 + 2 * rows * 4) + 2 * rows * cols * 2
+    return {"value": round(nbytes * reps / el / 1e9, 2), "unit": "GB/s", "cores": int(lib.g950o_threads()),
+            "kind": "port",
+            "sample": f"full config-2 workload (LayerNorm + softmax, bf16 [8191,3000]) x {reps} passes, "
+                      f"{el:.1f} s, oracle/cpu_baseline.c OpenMP fp32",
+            "cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def suite(torch, ops):
+    """Every other BASELINE config, timed per kernel with HIP events."""
+    from oracle import inputs
+    dev = "cuda:0"
+    out = []
+
+    # C1: fp32 RMSNorm + softmax [4096, 4096], 4 rotating sets (512 MiB)
+    sets = []
+    for s in range(ROTATE):
+        c = inputs.config1(seed=inputs.SEEDS["c1"] + s)
+        sets.append({"x": torch.from_numpy(c["x"]).to(dev), "w": torch.from_numpy(c["w"]).to(dev),
+                     "y": torch.empty((4096, 4096), device=dev), "r": torch.empty(4096, device=dev)})
+    rb = 2 * 4096 * 4096 * 4 + 2 * 4096 * 4
+    sb = 2 * 4096 * 4096 * 4
+
+    def rms(i):
+        d = sets[i % ROTATE]
+        ops.rms_layernorm_forward_kernel(d["y"], 4096, d["x"], 4096, d["w"], 1, d["r"], 1, 4096, 1e-6)
+
+    def smx(i):
+        d = sets[i % ROTATE]
+        ops.softmax_kernel(d["x"], d["y"], 4096)
+
+    for name, fn, nbytes in (("C1a rmsnorm fp32 [4096,4096]", rms, rb), ("C1b softmax fp32 [4096,4096]", smx, sb)):
+        ms = event_time(torch, fn, 200, 10)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"config": name, "kernel": ops.rt.module().last_kernel, "us": round(ms * 1e3, 2),
+                    "value": round(gbs, 1), "unit": "GB/s", "bound": "hbm",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    del sets
+    torch.cuda.empty_cache()
+
+    # C3: bf16 GEMM, A row-major, B column-major
+    for m, n, k in ((8192, 8192, 8192), (4097, 11008, 4096)):
+        c = inputs.config3(m, n, k)
+        a = torch.from_numpy(c["a"]).to(dev).to(torch.bfloat16)
+        bt = torch.from_numpy(c["bt"]).to(dev).to(torch.bfloat16)
+        del c
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        ms = event_time(torch, lambda i: ops.matmul_kernel(a, bt.t(), y, m, n, k), 20, 3)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out.append({"config": f"C3 gemm bf16 {m}x{n}x{k}", "kernel": ops.rt.module().last_kernel,
+                    "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
+                    "frac": round(tf / BF16_PEAK_TFS, 4)})
+        del a, bt, y
+        torch.cuda.empty_cache()
+
+    # C4: causal GQA attention bf16 (4, 32/8, 4096, 128) with LSE
+    c = inputs.config4()
+    bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
+    q, k, v = bf(c["q"]), bf(c["k"]), bf(c["v"])
+    del c
+    o = torch.empty_like(q)
+    lse = torch.empty((4, 32, 4096), dtype=torch.float32, device=dev)
+    ms = event_time(torch, lambda i: ops.attention(q, k, v, causal=True, out=o, lse=lse), 10, 2)
+    flops = 4.0 * 4 * 32 * 128 * 4096 * 4096 / 2
+    tf = flops / (ms * 1e-3) / 1e12
+    out.append({"config": "C4 causal GQA attention bf16 (4,32/8,4096,128)", "kernel": ops.rt.module().last_kernel,
+                "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
+                "frac": round(tf / BF16_PEAK_TFS, 4)})
+    del q, k, v, o, lse
+    torch.cuda.empty_cache()
+
+    # C5: int8 GEMM 4096x8192x8192 + dequant
+    c = inputs.config5()
+    a = torch.from_numpy(c["a"]).to(dev)
+    bt = torch.from_numpy(c["bt"]).to(dev)
+    sa = torch.from_numpy(c["sa"]).to(dev)
+    sbv = torch.from_numpy(c["sb"]).to(dev)
+    del c
+    y = torch.empty((4096, 8192), dtype=torch.bfloat16, device=dev)
+    ms = event_time(torch, lambda i: ops.matmul_i8_dequant_kernel(a, bt.t(), sa, sbv, y, 4096, 8192, 8192), 20, 3)
+    tops = 2.0 * 4096 * 8192 * 8192 / (ms * 1e-3) / 1e12
+    out.append({"config": "C5 int8 gemm 4096x8192x8192 + dequant", "kernel": ops.rt.module().last_kernel,
+                "us": round(ms * 1e3, 1), "value": round(tops, 1), "unit": "TOP/s", "bound": "mfma",
+                "frac": round(tops / INT8_PEAK_TOPS, 4)})
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-suite", action="store_true", help="headline workload only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the multi-GPU "
+              "sharding plan is design-only", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from compiler_amd import operators as ops
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs the MI355X")
+    log("bench: headline (config 2) ...")
+    value, ms_step, wall, roof, per_kernel, step_bytes = headline(torch, ops, args)
+    log(f"bench: headline {value:.1f} GB/s, {ms_step * 1e3:.1f} us/step")
+    suite_rows = []
+    if not args.no_suite:
+        log("bench: suite ...")
+        suite_rows = suite(torch, ops)
+        for r in suite_rows:
+            log(f"bench:   {r['config']}: {r['value']} {r['unit']} ({r['frac'] * 100:.1f}% of peak)")
+    cpu = None
+    if not args.no_cpu:
+        log("bench: cpu baseline ...")
+        cpu = cpu_baseline(args.cpu_seconds)
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded numpy draws of the BASELINE distributions, oracle/inputs.py)",
+        "config": {"workload": "C2 masked-tail bf16 LayerNorm + softmax, x[8191,3000] (1% +-60), "
+                               "fp32 statistics, 4 rotating buffer sets",
+                   "rows": 8191, "cols": 3000, "bytes_per_step": step_bytes},
+        "roofline": roof, "kernels": per_kernel, "cpu_baseline": cpu, "suite": suite_rows,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

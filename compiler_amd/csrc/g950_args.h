@@ -1,0 +1,64 @@
+// Kernel argument blocks shared by the gfx950 kernels and the host launcher.
+// Each kernel takes exactly one of these structs by value; the launcher fills
+// it after validating the operator contract.  Plain C layout only.
+#pragma once
+
+namespace g950 {
+
+struct RowArgs {
+  const void* x;
+  void* y;
+  const void* w;      // RMSNorm / LayerNorm weight (same dtype as x)
+  const void* b;      // LayerNorm bias
+  void* stat0;        // RMSNorm r / LayerNorm Mean
+  void* stat1;        // LayerNorm Rstd
+  long long x_row;    // row strides in elements
+  long long y_row;
+  long long stat0_stride;
+  long long stat1_stride;
+  int rows;
+  int cols;
+  float eps;
+  int stat_dtype;     // dtype code of stat0/stat1
+};
+
+struct GemmArgs {
+  const void* a;      // fast: [M,K] K-contiguous; general: element strides below
+  const void* b;      // fast: Bt[N,K] K-contiguous
+  void* c;            // output [M,N]
+  const float* sa;    // int8 dequant: per-row A scale (may be null -> no dequant output)
+  const float* sb;    // per-column B scale
+  int* acc_out;       // int8: optional int32 accumulator output [M,N]
+  long long a_s0, a_s1;   // element strides of A along (m, k)
+  long long b_s0, b_s1;   // element strides of B along (k, n)
+  long long c_s0, c_s1;   // element strides of C along (m, n)
+  long long acc_s0;       // row stride of acc_out
+  int M, N, K;
+  int tiles_m, tiles_n;
+  int a_dtype, b_dtype, c_dtype;
+};
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;  // may be null
+  long long q_sz, q_sh, q_ss;  // element strides (z, h, s); d stride is 1
+  long long k_sz, k_sh, k_ss;
+  long long v_sz, v_sh, v_ss;
+  long long o_sz, o_sh, o_ss;
+  long long lse_sz, lse_sh, lse_ss;
+  int Z, Hq, Hkv, Sq, Sk;
+  float scale_log2;  // scale * log2(e)
+  int causal;
+  int nqb;           // query blocks of 128
+};
+
+struct AttnGenArgs {
+  AttnArgs a;
+  int D;
+  int dtype;
+};
+
+}  // namespace g950

@@ -1,0 +1,619 @@
+// g950rt -- the single gfx950 module loader and launcher (C ABI in
+// include/g950rt.h).
+//
+// It takes the place of the reference's native runtime for the hot-path
+// operators: the bundle/pool/operator_entry machinery of
+// a100c/runtime/{main.c,pool.c,bundle.c} and the per-operator assembly that
+// a100c/backend emits.  One code object holds every kernel; an operator call
+// is (op contract, views, scalars) in the reference's sorted-argument-name
+// order (a100_support/native_io.py:74,81).  The launcher
+//   1. validates every view against its allocation (reach inside storage,
+//      dtype, rank, contiguity the kernel assumes) and every scalar against
+//      the views (the reference passes redundant shape/stride scalars; a
+//      mismatch is a refusal, never a silent reinterpretation),
+//   2. picks the kernel variant from dtypes, extents, strides and alignment,
+//   3. fills the kernel's argument block and launches it on the caller's
+//      stream.
+// Nothing is launched unless every check passed.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/g950rt.h"
+#include "g950_args.h"
+
+using namespace g950;
+
+struct g950_module {
+  hipModule_t mod = nullptr;
+  int device = -1;
+  std::mutex mu;
+  std::unordered_map<std::string, hipFunction_t> fns;
+};
+
+namespace {
+
+thread_local std::string t_error;
+thread_local std::string t_kernel;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  t_error = buf;
+  return code;
+}
+
+int itemsize(uint32_t dt) {
+  static const int sizes[] = {0, 1, 1, 1, 2, 2, 4, 4, 8, 8, 2, 2, 4, 8};
+  return dt < 14 ? sizes[dt] : 0;
+}
+
+const char* dtname(uint32_t dt) {
+  static const char* names[] = {"?", "bool", "int8", "uint8", "int16", "uint16", "int32",
+                                "uint32", "int64", "uint64", "float16", "bfloat16",
+                                "float32", "float64"};
+  return dt < 14 ? names[dt] : "?";
+}
+
+bool is_float16ish(uint32_t dt) { return dt == G950_DTYPE_BFLOAT16 || dt == G950_DTYPE_FLOAT16; }
+bool is_float(uint32_t dt) { return is_float16ish(dt) || dt == G950_DTYPE_FLOAT32; }
+
+// A checked view: extents and ELEMENT strides.
+struct View {
+  const char* name = "";
+  const g950_view* v = nullptr;
+  int nd = 0;
+  int64_t shape[8] = {};
+  int64_t stride[8] = {};  // elements
+  int isz = 0;
+  uintptr_t addr() const { return (uintptr_t)v->data; }
+};
+
+int check_view(const g950_view* views, uint32_t idx, const char* name, int ndim, View& out,
+               bool output) {
+  const g950_view& v = views[idx];
+  out.name = name;
+  out.v = &v;
+  if ((int)v.ndim != ndim)
+    return fail(G950_REJECTED, "view %s: rank %u, contract needs %d", name, v.ndim, ndim);
+  if (!v.shape || !v.strides) return fail(G950_REJECTED, "view %s: null shape/strides", name);
+  out.isz = itemsize(v.dtype);
+  if (!out.isz) return fail(G950_REJECTED, "view %s: unknown dtype code %u", name, v.dtype);
+  if (v.flags & ~1u) return fail(G950_REJECTED, "view %s: reserved flag bits set", name);
+  if (output && !(v.flags & G950_VIEW_OUTPUT))
+    return fail(G950_REJECTED, "view %s: output argument lacks the output flag", name);
+  if (!v.data || !v.storage) return fail(G950_REJECTED, "view %s: null device pointer", name);
+  out.nd = ndim;
+  int64_t lo = 0, hi = 0;
+  bool empty = false;
+  for (int i = 0; i < ndim; ++i) {
+    out.shape[i] = v.shape[i];
+    if (v.shape[i] < 0) return fail(G950_REJECTED, "view %s: negative extent", name);
+    if (v.shape[i] == 0) empty = true;
+    if (v.strides[i] % out.isz)
+      return fail(G950_REJECTED, "view %s: byte stride %lld not a multiple of the item size",
+                  name, (long long)v.strides[i]);
+    out.stride[i] = v.strides[i] / out.isz;
+    if (v.strides[i] < 0) lo += v.strides[i] * (v.shape[i] - 1);
+    else hi += v.strides[i] * (v.shape[i] - 1);
+  }
+  if (!empty) {
+    const intptr_t base = (intptr_t)v.data - (intptr_t)v.storage;
+    if (base + lo < 0 || (uint64_t)(base + hi + out.isz) > v.storage_size)
+      return fail(G950_REJECTED, "view %s: reach [%lld, %lld) outside its %llu-byte storage", name,
+                  (long long)(base + lo), (long long)(base + hi + out.isz),
+                  (unsigned long long)v.storage_size);
+  }
+  return G950_OK;
+}
+
+int scalar_int(const g950_scalar* s, const char* name, long long& out) {
+  switch (s->dtype) {
+    case G950_DTYPE_BOOL: case G950_DTYPE_UINT8: out = (long long)(s->bits & 0xFF); break;
+    case G950_DTYPE_INT8: out = (int8_t)(s->bits & 0xFF); break;
+    case G950_DTYPE_INT16: out = (int16_t)(s->bits & 0xFFFF); break;
+    case G950_DTYPE_UINT16: out = (long long)(s->bits & 0xFFFF); break;
+    case G950_DTYPE_INT32: out = (int32_t)(s->bits & 0xFFFFFFFFu); break;
+    case G950_DTYPE_UINT32: out = (long long)(s->bits & 0xFFFFFFFFu); break;
+    case G950_DTYPE_INT64: case G950_DTYPE_UINT64: out = (long long)s->bits; break;
+    default: return fail(G950_USAGE, "scalar %s: dtype %s is not an integer", name, dtname(s->dtype));
+  }
+  return G950_OK;
+}
+
+int scalar_float(const g950_scalar* s, const char* name, double& out) {
+  if (s->dtype == G950_DTYPE_FLOAT32) {
+    float f;
+    uint32_t b = (uint32_t)s->bits;
+    memcpy(&f, &b, 4);
+    out = f;
+  } else if (s->dtype == G950_DTYPE_FLOAT64) {
+    memcpy(&out, &s->bits, 8);
+  } else {
+    long long i;
+    if (scalar_int(s, name, i)) return fail(G950_USAGE, "scalar %s: not a number", name);
+    out = (double)i;
+  }
+  return G950_OK;
+}
+
+int expect_int(const g950_scalar* scalars, uint32_t idx, const char* name, long long want) {
+  long long got;
+  if (int rc = scalar_int(&scalars[idx], name, got)) return rc;
+  if (got != want)
+    return fail(G950_USAGE, "scalar %s = %lld disagrees with the views (%lld)", name, got, want);
+  return G950_OK;
+}
+
+hipFunction_t function(g950_module* m, const std::string& name) {
+  std::lock_guard<std::mutex> lock(m->mu);
+  auto it = m->fns.find(name);
+  if (it != m->fns.end()) return it->second;
+  hipFunction_t f = nullptr;
+  if (hipModuleGetFunction(&f, m->mod, name.c_str()) != hipSuccess) return nullptr;
+  m->fns.emplace(name, f);
+  return f;
+}
+
+template <class Args>
+int launch(g950_module* m, const std::string& name, unsigned grid, unsigned block, Args& args,
+           void* stream) {
+  if (!m) {  // validation only (g950_validate): report the choice, launch nothing
+    t_kernel = name;
+    return G950_OK;
+  }
+  hipFunction_t f = function(m, name);
+  if (!f) return fail(G950_RESOURCE, "kernel %s not found in the code object", name.c_str());
+  if (grid == 0) {  // nothing to do (empty extent)
+    t_kernel = name;
+    return G950_OK;
+  }
+  void* params[] = {&args};
+  hipError_t e = hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, (hipStream_t)stream, params,
+                                       nullptr);
+  if (e != hipSuccess)
+    return fail(G950_RESOURCE, "launch of %s failed: %s", name.c_str(), hipGetErrorString(e));
+  t_kernel = name;
+  return G950_OK;
+}
+
+bool aligned16(uintptr_t p) { return (p & 15) == 0; }
+
+// ------------------------------------------------------------ row reductions
+struct RowCfg { int items, block; };
+const RowCfg kRowCfgs[] = {{1, 64}, {2, 64}, {4, 64}, {3, 128}, {8, 64}, {4, 128},
+                           {4, 256}, {8, 256}, {16, 256}};
+
+const char* rr_dtype(uint32_t dt) {
+  return dt == G950_DTYPE_FLOAT32 ? "f32" : dt == G950_DTYPE_BFLOAT16 ? "bf16" : "f16";
+}
+
+// Pick and launch the row kernel.  `params` are the per-column parameter
+// views (W, B) whose alignment the vector form also needs.
+int launch_rows(g950_module* m, const char* op, RowArgs& a, uint32_t dt, const View& x,
+                const View& y, const View* p0, const View* p1, void* stream) {
+  const int isz = itemsize(dt);
+  const int vmax = 16 / isz;
+  bool vec = (a.cols % vmax == 0) && aligned16(x.addr()) && aligned16(y.addr()) &&
+             ((a.x_row * isz) % 16 == 0) && ((a.y_row * isz) % 16 == 0);
+  if (p0) vec = vec && aligned16(p0->addr());
+  if (p1) vec = vec && aligned16(p1->addr());
+  const int v = vec ? vmax : 1;
+  const int nvec = a.cols / v;
+  char name[128];
+  const RowCfg* pick = nullptr;
+  for (const RowCfg& c : kRowCfgs)
+    if (c.items * c.block >= nvec) { pick = &c; break; }
+  if (pick) {
+    snprintf(name, sizeof name, "g950_rr_%s_%s_v%d_i%d_b%d", op, rr_dtype(dt), v, pick->items,
+             pick->block);
+    return launch(m, name, (unsigned)a.rows, (unsigned)pick->block, a, stream);
+  }
+  snprintf(name, sizeof name, "g950_rr_loop_%s_%s", op, rr_dtype(dt));
+  return launch(m, name, (unsigned)a.rows, 256u, a, stream);
+}
+
+int row_common(const View& x, const View& y) {
+  if (!is_float(x.v->dtype) || x.v->dtype != y.v->dtype)
+    return fail(G950_USAGE, "row op: x/y dtypes %s/%s unsupported (float32, bfloat16, float16, same)",
+                dtname(x.v->dtype), dtname(y.v->dtype));
+  if (x.shape[0] != y.shape[0] || x.shape[1] != y.shape[1])
+    return fail(G950_USAGE, "row op: x and y shapes differ");
+  if (x.shape[1] > 1 && (x.stride[1] != 1 || y.stride[1] != 1))
+    return fail(G950_USAGE, "row op: the reduced (last) axis must be contiguous");
+  if (x.shape[0] > 0x7FFFFFFF || x.shape[1] > 0x7FFFFFFF)
+    return fail(G950_USAGE, "row op: extent too large");
+  return G950_OK;
+}
+
+int op_softmax(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+               uint32_t nsc, void* stream) {
+  if (nviews != 2 || nsc != 1) return fail(G950_USAGE, "softmax: needs views (x_ptr, y_ptr), scalars (n_cols)");
+  View x, y;
+  if (int rc = check_view(views, 0, "x_ptr", 2, x, false)) return rc;
+  if (int rc = check_view(views, 1, "y_ptr", 2, y, true)) return rc;
+  if (int rc = row_common(x, y)) return rc;
+  if (int rc = expect_int(sc, 0, "n_cols", x.shape[1])) return rc;
+  RowArgs a{};
+  a.x = x.v->data; a.y = y.v->data;
+  a.x_row = x.stride[0]; a.y_row = y.stride[0];
+  a.rows = (int)x.shape[0]; a.cols = (int)x.shape[1];
+  if (a.cols == 0) return fail(G950_USAGE, "softmax: empty row");
+  return launch_rows(m, "softmax", a, x.v->dtype, x, y, nullptr, nullptr, stream);
+}
+
+int stat_view(const View& s, const View& x, const char* what) {
+  if (!is_float(s.v->dtype)) return fail(G950_USAGE, "%s: dtype %s unsupported", what, dtname(s.v->dtype));
+  if (s.shape[0] != x.shape[0]) return fail(G950_USAGE, "%s: needs one entry per row", what);
+  return G950_OK;
+}
+
+int param_view(const View& p, const View& x, const char* what) {
+  if (p.v->dtype != x.v->dtype) return fail(G950_USAGE, "%s: dtype must match X", what);
+  if (p.shape[0] != x.shape[1]) return fail(G950_USAGE, "%s: needs one entry per column", what);
+  if (p.shape[0] > 1 && p.stride[0] != 1) return fail(G950_USAGE, "%s: must be contiguous", what);
+  return G950_OK;
+}
+
+int op_rms(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+           uint32_t nsc, void* stream) {
+  if (nviews != 4 || nsc != 6)
+    return fail(G950_USAGE, "rms_layernorm: needs views (W, X, Y, r) and 6 scalars");
+  View w, x, y, r;
+  if (int rc = check_view(views, 0, "W", 1, w, false)) return rc;
+  if (int rc = check_view(views, 1, "X", 2, x, false)) return rc;
+  if (int rc = check_view(views, 2, "Y", 2, y, true)) return rc;
+  if (int rc = check_view(views, 3, "r", 1, r, true)) return rc;
+  if (int rc = row_common(x, y)) return rc;
+  if (int rc = param_view(w, x, "W")) return rc;
+  if (int rc = stat_view(r, x, "r")) return rc;
+  long long wrs;
+  if (int rc = scalar_int(&sc[0], "W_row_stride", wrs)) return rc;
+  if (int rc = expect_int(sc, 1, "X_row_stride", x.stride[0])) return rc;
+  if (int rc = expect_int(sc, 2, "Y_row_stride", y.stride[0])) return rc;
+  double eps;
+  if (int rc = scalar_float(&sc[3], "eps", eps)) return rc;
+  if (int rc = expect_int(sc, 4, "n_cols", x.shape[1])) return rc;
+  if (int rc = expect_int(sc, 5, "r_row_stride", r.stride[0])) return rc;
+  RowArgs a{};
+  a.x = x.v->data; a.y = y.v->data; a.w = w.v->data; a.stat0 = r.v->data;
+  a.x_row = x.stride[0]; a.y_row = y.stride[0]; a.stat0_stride = r.stride[0];
+  a.rows = (int)x.shape[0]; a.cols = (int)x.shape[1];
+  a.eps = (float)eps; a.stat_dtype = (int)r.v->dtype;
+  if (a.cols == 0) return fail(G950_USAGE, "rms_layernorm: empty row");
+  return launch_rows(m, "rmsnorm", a, x.v->dtype, x, y, &w, nullptr, stream);
+}
+
+int op_layernorm(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+                 uint32_t nsc, void* stream) {
+  if (nviews != 6 || nsc != 3)
+    return fail(G950_USAGE, "layernorm: needs views (B, Mean, Rstd, W, X, Y), scalars (N, eps, stride)");
+  View b, mean, rstd, w, x, y;
+  if (int rc = check_view(views, 0, "B", 1, b, false)) return rc;
+  if (int rc = check_view(views, 1, "Mean", 1, mean, true)) return rc;
+  if (int rc = check_view(views, 2, "Rstd", 1, rstd, true)) return rc;
+  if (int rc = check_view(views, 3, "W", 1, w, false)) return rc;
+  if (int rc = check_view(views, 4, "X", 2, x, false)) return rc;
+  if (int rc = check_view(views, 5, "Y", 2, y, true)) return rc;
+  if (int rc = row_common(x, y)) return rc;
+  if (int rc = param_view(w, x, "W")) return rc;
+  if (int rc = param_view(b, x, "B")) return rc;
+  if (int rc = stat_view(mean, x, "Mean")) return rc;
+  if (int rc = stat_view(rstd, x, "Rstd")) return rc;
+  if (mean.v->dtype != rstd.v->dtype) return fail(G950_USAGE, "layernorm: Mean/Rstd dtypes differ");
+  if (int rc = expect_int(sc, 0, "N", x.shape[1])) return rc;
+  double eps;
+  if (int rc = scalar_float(&sc[1], "eps", eps)) return rc;
+  if (x.stride[0] != y.stride[0]) return fail(G950_USAGE, "layernorm: X and Y share one row stride");
+  if (int rc = expect_int(sc, 2, "stride", x.stride[0])) return rc;
+  RowArgs a{};
+  a.x = x.v->data; a.y = y.v->data; a.w = w.v->data; a.b = b.v->data;
+  a.stat0 = mean.v->data; a.stat1 = rstd.v->data;
+  a.x_row = x.stride[0]; a.y_row = y.stride[0];
+  a.stat0_stride = mean.stride[0]; a.stat1_stride = rstd.stride[0];
+  a.rows = (int)x.shape[0]; a.cols = (int)x.shape[1];
+  a.eps = (float)eps; a.stat_dtype = (int)mean.v->dtype;
+  if (a.cols == 0) return fail(G950_USAGE, "layernorm: empty row");
+  return launch_rows(m, "layernorm", a, x.v->dtype, x, y, &w, &b, stream);
+}
+
+// --------------------------------------------------------------------- GEMM
+int gemm_tiles(GemmArgs& g) {
+  const long long tm = (g.M + 255) / 256, tn = (g.N + 255) / 256;
+  if (tm * tn > 0x7FFFFFFF) return -1;
+  g.tiles_m = (int)tm;
+  g.tiles_n = (int)tn;
+  return (int)(tm * tn);
+}
+
+// A[M,K] and B[K,N] both K-contiguous, 16-byte rows, K a whole number of
+// 128-byte slabs: the MFMA kernel applies.
+bool gemm_fast_ok(const View& a, const View& b, int K, int esz) {
+  return a.stride[1] == 1 && b.stride[0] == 1 && (K * esz) % 128 == 0 && K > 0 &&
+         aligned16(a.addr()) && aligned16(b.addr()) && (a.stride[0] * esz) % 16 == 0 &&
+         (b.stride[1] * esz) % 16 == 0 && a.shape[0] > 0 && b.shape[1] > 0;
+}
+
+int gemm_views(const View& a, const View& b, const View& y, const g950_scalar* sc, long long& M,
+               long long& N, long long& K) {
+  M = a.shape[0]; K = a.shape[1]; N = b.shape[1];
+  if (b.shape[0] != K) return fail(G950_USAGE, "matmul: a is [%lld,%lld] but b has %lld rows", M, K, (long long)b.shape[0]);
+  if (y.shape[0] != M || y.shape[1] != N) return fail(G950_USAGE, "matmul: output must be [M,N]");
+  if (M > 0x7FFFFFFF || N > 0x7FFFFFFF || K > 0x7FFFFFFF) return fail(G950_USAGE, "matmul: extent too large");
+  if (int rc = expect_int(sc, 0, "K", K)) return rc;
+  if (int rc = expect_int(sc, 1, "M", M)) return rc;
+  if (int rc = expect_int(sc, 2, "N", N)) return rc;
+  return G950_OK;
+}
+
+int op_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+              uint32_t nsc, void* stream) {
+  if (nviews != 3 || nsc != 3) return fail(G950_USAGE, "matmul: needs views (a_ptr, b_ptr, y_ptr), scalars (K, M, N)");
+  View a, b, y;
+  if (int rc = check_view(views, 0, "a_ptr", 2, a, false)) return rc;
+  if (int rc = check_view(views, 1, "b_ptr", 2, b, false)) return rc;
+  if (int rc = check_view(views, 2, "y_ptr", 2, y, true)) return rc;
+  long long M, N, K;
+  if (int rc = gemm_views(a, b, y, sc, M, N, K)) return rc;
+  if (!is_float(a.v->dtype) || !is_float(b.v->dtype) || !is_float(y.v->dtype))
+    return fail(G950_USAGE, "matmul: float32/bfloat16/float16 operands only");
+  GemmArgs g{};
+  g.a = a.v->data; g.b = b.v->data; g.c = y.v->data;
+  g.M = (int)M; g.N = (int)N; g.K = (int)K;
+  g.a_dtype = (int)a.v->dtype; g.b_dtype = (int)b.v->dtype; g.c_dtype = (int)y.v->dtype;
+  g.c_s0 = y.stride[0]; g.c_s1 = y.stride[1];
+  if (M == 0 || N == 0) return launch(m, "g950_gemm_general", 0, 256, g, stream);
+  const bool same16 = a.v->dtype == b.v->dtype && is_float16ish(a.v->dtype);
+  if (same16 && gemm_fast_ok(a, b, (int)K, 2) && y.stride[1] == 1 && aligned16(y.addr())) {
+    g.a_s0 = a.stride[0];
+    g.b_s0 = b.stride[1];  // Bt row (n) stride
+    const int tiles = gemm_tiles(g);
+    if (tiles < 0) return fail(G950_USAGE, "matmul: too many tiles");
+    return launch(m, a.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_gemm_bf16_256x256" : "g950_gemm_f16_256x256",
+                  (unsigned)tiles, 512u, g, stream);
+  }
+  g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
+  g.b_s0 = b.stride[0]; g.b_s1 = b.stride[1];
+  g.tiles_n = (int)((N + 63) / 64);
+  const long long blocks = ((M + 63) / 64) * g.tiles_n;
+  if (blocks > 0x7FFFFFFF) return fail(G950_USAGE, "matmul: too many tiles");
+  return launch(m, "g950_gemm_general", (unsigned)blocks, 256u, g, stream);
+}
+
+int op_matmul_i8(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+                 uint32_t nsc, bool dequant, void* stream) {
+  const uint32_t want = dequant ? 5 : 3;
+  if (nviews != want || nsc != 3)
+    return fail(G950_USAGE, dequant ? "matmul_i8_dequant: needs views (a_ptr, b_ptr, sa_ptr, sb_ptr, y_ptr), scalars (K, M, N)"
+                                    : "matmul_i8: needs views (a_ptr, b_ptr, c_ptr), scalars (K, M, N)");
+  View a, b, y, sa, sb;
+  if (int rc = check_view(views, 0, "a_ptr", 2, a, false)) return rc;
+  if (int rc = check_view(views, 1, "b_ptr", 2, b, false)) return rc;
+  if (dequant) {
+    if (int rc = check_view(views, 2, "sa_ptr", 1, sa, false)) return rc;
+    if (int rc = check_view(views, 3, "sb_ptr", 1, sb, false)) return rc;
+    if (int rc = check_view(views, 4, "y_ptr", 2, y, true)) return rc;
+  } else {
+    if (int rc = check_view(views, 2, "c_ptr", 2, y, true)) return rc;
+  }
+  if (a.v->dtype != G950_DTYPE_INT8 || b.v->dtype != G950_DTYPE_INT8)
+    return fail(G950_USAGE, "matmul_i8: operands must be int8");
+  long long M, N, K;
+  if (int rc = gemm_views(a, b, y, sc, M, N, K)) return rc;
+  GemmArgs g{};
+  g.a = a.v->data; g.b = b.v->data;
+  g.M = (int)M; g.N = (int)N; g.K = (int)K;
+  g.a_dtype = g.b_dtype = G950_DTYPE_INT8;
+  if (dequant) {
+    if (sa.v->dtype != G950_DTYPE_FLOAT32 || sb.v->dtype != G950_DTYPE_FLOAT32)
+      return fail(G950_USAGE, "matmul_i8_dequant: scales must be float32");
+    if (sa.shape[0] != M || sb.shape[0] != N) return fail(G950_USAGE, "matmul_i8_dequant: scale extents");
+    if ((M > 1 && sa.stride[0] != 1) || (N > 1 && sb.stride[0] != 1))
+      return fail(G950_USAGE, "matmul_i8_dequant: scales must be contiguous");
+    if (!is_float(y.v->dtype)) return fail(G950_USAGE, "matmul_i8_dequant: float output only");
+    g.sa = (const float*)sa.v->data; g.sb = (const float*)sb.v->data;
+    g.c = y.v->data; g.c_dtype = (int)y.v->dtype;
+    g.c_s0 = y.stride[0]; g.c_s1 = y.stride[1];
+  } else {
+    if (y.v->dtype != G950_DTYPE_INT32) return fail(G950_USAGE, "matmul_i8: c_ptr must be int32");
+    if (N > 1 && y.stride[1] != 1) return fail(G950_USAGE, "matmul_i8: c_ptr rows must be contiguous");
+    g.acc_out = (int*)y.v->data; g.acc_s0 = y.stride[0];
+  }
+  if (M == 0 || N == 0) return launch(m, "g950_gemm_general_i8", 0, 256, g, stream);
+  const bool out_ok = dequant ? (y.stride[1] == 1 && aligned16(y.addr())) : aligned16(y.addr());
+  if (gemm_fast_ok(a, b, (int)K, 1) && out_ok) {
+    g.a_s0 = a.stride[0];
+    g.b_s0 = b.stride[1];
+    const int tiles = gemm_tiles(g);
+    if (tiles < 0) return fail(G950_USAGE, "matmul_i8: too many tiles");
+    return launch(m, "g950_gemm_i8_256x256", (unsigned)tiles, 512u, g, stream);
+  }
+  if (!dequant && N > 1 && y.stride[1] != 1) return fail(G950_USAGE, "matmul_i8: c_ptr layout");
+  g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
+  g.b_s0 = b.stride[0]; g.b_s1 = b.stride[1];
+  g.tiles_n = (int)((N + 63) / 64);
+  const long long blocks = ((M + 63) / 64) * g.tiles_n;
+  if (blocks > 0x7FFFFFFF) return fail(G950_USAGE, "matmul_i8: too many tiles");
+  return launch(m, "g950_gemm_general_i8", (unsigned)blocks, 256u, g, stream);
+}
+
+// ---------------------------------------------------------------- attention
+int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+                 uint32_t nsc, bool with_lse, void* stream) {
+  const uint32_t want = with_lse ? 5 : 4;
+  if (nviews != want || nsc != 21)
+    return fail(G950_USAGE, "attention: needs views (k_ptr,%s out_ptr, q_ptr, v_ptr) and 21 scalars "
+                "(CAUSAL, H, N_CTX, Z, scale, 16 strides)", with_lse ? " lse_ptr," : "");
+  View k, lse, o, q, v;
+  uint32_t i = 0;
+  if (int rc = check_view(views, i++, "k_ptr", 4, k, false)) return rc;
+  if (with_lse)
+    if (int rc = check_view(views, i++, "lse_ptr", 3, lse, true)) return rc;
+  if (int rc = check_view(views, i++, "out_ptr", 4, o, true)) return rc;
+  if (int rc = check_view(views, i++, "q_ptr", 4, q, false)) return rc;
+  if (int rc = check_view(views, i++, "v_ptr", 4, v, false)) return rc;
+  const uint32_t dt = q.v->dtype;
+  if (!is_float(dt) || k.v->dtype != dt || v.v->dtype != dt || o.v->dtype != dt)
+    return fail(G950_USAGE, "attention: q/k/v/out must share one float dtype");
+  const long long Z = q.shape[0], H = q.shape[1], S = q.shape[2], D = q.shape[3];
+  const long long Hkv = k.shape[1], Sk = k.shape[2];
+  if (k.shape[0] != Z || k.shape[3] != D || v.shape[0] != Z || v.shape[1] != Hkv ||
+      v.shape[2] != Sk || v.shape[3] != D)
+    return fail(G950_USAGE, "attention: k/v shapes must be [Z, Hkv, Sk, D] matching q");
+  if (o.shape[0] != Z || o.shape[1] != H || o.shape[2] != S || o.shape[3] != D)
+    return fail(G950_USAGE, "attention: out must have q's shape");
+  if (Hkv <= 0 || H % Hkv) return fail(G950_USAGE, "attention: H must be a multiple of the KV heads");
+  if (with_lse) {
+    if (lse.v->dtype != G950_DTYPE_FLOAT32) return fail(G950_USAGE, "attention: lse must be float32");
+    if (lse.shape[0] != Z || lse.shape[1] != H || lse.shape[2] != S)
+      return fail(G950_USAGE, "attention: lse must be [Z, H, N_CTX]");
+  }
+  if (D > 1 && (q.stride[3] != 1 || k.stride[3] != 1 || v.stride[3] != 1 || o.stride[3] != 1))
+    return fail(G950_USAGE, "attention: head_dim must be contiguous");
+  long long causal;
+  if (int rc = scalar_int(&sc[0], "CAUSAL", causal)) return rc;
+  if (int rc = expect_int(sc, 1, "H", H)) return rc;
+  if (int rc = expect_int(sc, 2, "N_CTX", S)) return rc;
+  if (int rc = expect_int(sc, 3, "Z", Z)) return rc;
+  double scale;
+  if (int rc = scalar_float(&sc[4], "scale", scale)) return rc;
+  // stride scalars, sorted: k(h,k,n,z) o(h,m,n,z) q(h,k,m,z) v(h,k,n,z)
+  const struct { const View* vw; const char* names[4]; int dims[4]; } st[4] = {
+      {&k, {"stride_kh", "stride_kk", "stride_kn", "stride_kz"}, {1, 3, 2, 0}},
+      {&o, {"stride_oh", "stride_om", "stride_on", "stride_oz"}, {1, 2, 3, 0}},
+      {&q, {"stride_qh", "stride_qk", "stride_qm", "stride_qz"}, {1, 3, 2, 0}},
+      {&v, {"stride_vh", "stride_vk", "stride_vn", "stride_vz"}, {1, 2, 3, 0}},
+  };
+  uint32_t si = 5;
+  for (const auto& e : st)
+    for (int j = 0; j < 4; ++j)
+      if (int rc = expect_int(sc, si++, e.names[j], e.vw->stride[e.dims[j]])) return rc;
+  if (Z * H > 0x7FFFFFF || S > 0x7FFFFFF || Sk > 0x7FFFFFF)
+    return fail(G950_USAGE, "attention: extent too large");
+  AttnArgs a{};
+  a.q = q.v->data; a.k = k.v->data; a.v = v.v->data; a.o = o.v->data;
+  a.lse = with_lse ? (float*)lse.v->data : nullptr;
+  a.q_sz = q.stride[0]; a.q_sh = q.stride[1]; a.q_ss = q.stride[2];
+  a.k_sz = k.stride[0]; a.k_sh = k.stride[1]; a.k_ss = k.stride[2];
+  a.v_sz = v.stride[0]; a.v_sh = v.stride[1]; a.v_ss = v.stride[2];
+  a.o_sz = o.stride[0]; a.o_sh = o.stride[1]; a.o_ss = o.stride[2];
+  if (with_lse) { a.lse_sz = lse.stride[0]; a.lse_sh = lse.stride[1]; a.lse_ss = lse.stride[2]; }
+  a.Z = (int)Z; a.Hq = (int)H; a.Hkv = (int)Hkv; a.Sq = (int)S; a.Sk = (int)Sk;
+  a.scale_log2 = (float)(scale * 1.4426950408889634);
+  a.causal = causal ? 1 : 0;
+  if (Z == 0 || H == 0 || S == 0) return launch(m, "g950_attn_fwd_general", 0, 64, a, stream);
+  if (Sk == 0) return fail(G950_USAGE, "attention: no keys");
+  const bool mfma = is_float16ish(dt) && (D == 64 || D == 128) &&
+                    aligned16(q.addr()) && aligned16(k.addr()) && aligned16(v.addr()) &&
+                    (o.addr() & 7) == 0 && q.stride[0] % 8 == 0 && q.stride[1] % 8 == 0 &&
+                    q.stride[2] % 8 == 0 && k.stride[0] % 8 == 0 && k.stride[1] % 8 == 0 &&
+                    k.stride[2] % 8 == 0 && v.stride[0] % 8 == 0 && v.stride[1] % 8 == 0 &&
+                    v.stride[2] % 8 == 0 && o.stride[0] % 4 == 0 && o.stride[1] % 4 == 0 &&
+                    o.stride[2] % 4 == 0;
+  if (mfma) {
+    a.nqb = (int)((S + 127) / 128);
+    const long long grid = (long long)a.nqb * Z * H;
+    if (grid > 0x7FFFFFFF) return fail(G950_USAGE, "attention: grid too large");
+    char name[64];
+    snprintf(name, sizeof name, "g950_attn_fwd_%s_d%lld", dt == G950_DTYPE_BFLOAT16 ? "bf16" : "f16", D);
+    return launch(m, name, (unsigned)grid, 256u, a, stream);
+  }
+  AttnGenArgs ga{};
+  ga.a = a;
+  ga.D = (int)D;
+  ga.dtype = (int)dt;
+  const long long rows = Z * H * S;
+  return launch(m, "g950_attn_fwd_general", (unsigned)((rows + 63) / 64), 64u, ga, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int g950_open(const char* path, g950_module** out) {
+  if (!path || !out) return fail(G950_USAGE, "g950_open: null argument");
+  *out = nullptr;
+  auto* m = new (std::nothrow) g950_module();
+  if (!m) return fail(G950_RESOURCE, "g950_open: out of host memory");
+  hipError_t e = hipGetDevice(&m->device);
+  if (e == hipSuccess) e = hipModuleLoad(&m->mod, path);
+  if (e != hipSuccess) {
+    delete m;
+    return fail(G950_RESOURCE, "g950_open: loading %s failed: %s", path, hipGetErrorString(e));
+  }
+  *out = m;
+  return G950_OK;
+}
+
+namespace {
+int dispatch(g950_module* m, uint32_t op, const g950_view* views, uint32_t nviews,
+             const g950_scalar* scalars, uint32_t nscalars, void* stream) {
+  t_kernel.clear();
+  if ((!views && nviews) || (!scalars && nscalars)) return fail(G950_USAGE, "null argument");
+  try {
+    switch (op) {
+      case G950_OP_SOFTMAX: return op_softmax(m, views, nviews, scalars, nscalars, stream);
+      case G950_OP_RMS_LAYERNORM: return op_rms(m, views, nviews, scalars, nscalars, stream);
+      case G950_OP_LAYERNORM: return op_layernorm(m, views, nviews, scalars, nscalars, stream);
+      case G950_OP_MATMUL: return op_matmul(m, views, nviews, scalars, nscalars, stream);
+      case G950_OP_MATMUL_I8: return op_matmul_i8(m, views, nviews, scalars, nscalars, false, stream);
+      case G950_OP_MATMUL_I8_DEQUANT:
+        return op_matmul_i8(m, views, nviews, scalars, nscalars, true, stream);
+      case G950_OP_ATTENTION: return op_attention(m, views, nviews, scalars, nscalars, false, stream);
+      case G950_OP_ATTENTION_LSE: return op_attention(m, views, nviews, scalars, nscalars, true, stream);
+      default: return fail(G950_USAGE, "g950_launch: unknown operator contract %u", op);
+    }
+  } catch (...) {
+    return fail(G950_RESOURCE, "g950_launch: internal error");
+  }
+}
+}  // namespace
+
+int g950_launch(g950_module* m, uint32_t op, const g950_view* views, uint32_t nviews,
+                const g950_scalar* scalars, uint32_t nscalars, void* stream) {
+  if (!m) return fail(G950_USAGE, "g950_launch: null module");
+  return dispatch(m, op, views, nviews, scalars, nscalars, stream);
+}
+
+int g950_validate(uint32_t op, const g950_view* views, uint32_t nviews, const g950_scalar* scalars,
+                  uint32_t nscalars) {
+  return dispatch(nullptr, op, views, nviews, scalars, nscalars, nullptr);
+}
+
+const char* g950_last_kernel(void) { return t_kernel.c_str(); }
+
+int g950_sync(void* stream) {
+  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return fail(G950_SYNC, "g950_sync: %s", hipGetErrorString(e));
+  return G950_OK;
+}
+
+const char* g950_strerror(int code) {
+  switch (code) {
+    case G950_OK: return "ok";
+    case G950_USAGE: return "operator contract refused";
+    case G950_REJECTED: return "view rejected";
+    case G950_RESOURCE: return "HIP resource or launch failure";
+    case G950_SYNC: return "stream synchronisation failed";
+    default: return "unknown";
+  }
+}
+
+const char* g950_last_error(void) { return t_error.c_str(); }
+
+void g950_close(g950_module* m) {
+  if (!m) return;
+  if (m->mod) hipModuleUnload(m->mod);
+  delete m;
+}
+
+}  // extern "C"

@@ -1,0 +1,320 @@
+// GEMM family on gfx950: bf16/fp16 (fp32 accumulate) and int8 (int32
+// accumulate, bit-exact) with a fused epilogue.
+//
+// Operator semantics: ops/suite/perf/matmul.py:21-37 (Y = A.B, fp32
+// accumulator, masked M/N/K edges, store in the output pointer dtype);
+// int8 dot family a100c/plan/tiles.py:118-131 (signed operands, modular int32
+// accumulator); dequant rule ops/suite/perf/dequantize_matmul.py:29-38
+// (per-column scale), here with the per-row A scale as well:
+// Y[m,n] = bf16(float(acc[m,n]) * sa[m] * sb[n]).
+//
+// Fast kernel (g950_gemm_*_256x256): both operands K-contiguous (A row-major
+// [M,K]; B stored as Bt[N,K], i.e. column-major [K,N]).
+//   * workgroup tile 256x256, 8 waves (2 x 4), wave tile 128 x 64
+//   * K slab of 128 bytes per row (64 bf16 / 128 int8) per stage, two LDS
+//     stages (2 x 64 KiB), filled by direct global->LDS 16-byte DMA loads
+//     (global_load_lds_dwordx4), so the next slab streams in while MFMAs run
+//     on the current one
+//   * LDS rows are 128 B; the eight 16-byte chunks of a row are XOR-swizzled
+//     with (row>>1)&7 so the 32 rows an MFMA operand read touches spread over
+//     all 64 banks
+//   * MFMA v_mfma_f32_32x32x16_{bf16,f16} / v_mfma_i32_32x32x32_i8; the B tile
+//     feeds the MFMA A port so each lane ends with four consecutive output
+//     columns of one output row (8-byte bf16 stores)
+//   * XCD-aware block order: consecutive tiles go to the same XCD (the
+//     hardware deals workgroups round-robin over 8 XCDs), grouped 8 tile-rows
+//     deep for L2 reuse
+//   * M/N edges: loads clamp the row index (the duplicated rows only feed
+//     output rows/cols that are never stored); stores are masked.  K must be a
+//     multiple of the slab (host checks), otherwise the general kernel runs.
+//
+// General kernel (g950_gemm_general): any strides, any K, fp32/fp16/bf16
+// inputs (fp32 FMA) or int8 (int32 exact); 64x64 tiles.  It serves the
+// reference's row-major-B fixtures and shapes the fast kernel refuses.
+#include "g950_common.h"
+
+namespace g950 {
+
+enum GemmMode : int { GEMM_BF16 = 0, GEMM_F16 = 1, GEMM_I8 = 2 };
+
+
+
+constexpr int BM = 256, BN = 256, SLAB = 128;  // SLAB: bytes of K per row per stage
+constexpr int GEMM_THREADS = 512;
+constexpr int STAGE_BYTES = (BM + BN) * SLAB;    // 64 KiB
+
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
+// Map the linear workgroup id to a (tile_m, tile_n): XCD-contiguous, then
+// grouped by 8 tile-rows.
+__device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+  const int group = 8;
+  const int per_group = group * tiles_n;
+  const int gid = pid / per_group;
+  const int first = gid * group;
+  const int gsize = min(tiles_m - first, group);
+  const int in = pid - gid * per_group;
+  tm = first + in % gsize;
+  tn = in / gsize;
+}
+
+// One wave-instruction of the slab load: 8 rows x 128 B = 1 KiB of LDS.
+__device__ __forceinline__ void dma_rows(const char* gbase, long long ld_bytes, int row0,
+                                         int row_limit, long long kbyte, char* lds_rows,
+                                         int lane) {
+  const int r = lane >> 3;
+  const int slot = lane & 7;
+  const int row = row0 + r;                       // row within the tile
+  const int grow = min(row, row_limit);           // clamped global row (relative)
+  const int chunk = slot ^ swz(row);
+  const char* src = gbase + (long long)grow * ld_bytes + kbyte + chunk * 16;
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                   (__attribute__((address_space(3))) void*)lds_rows, 16, 0, 0);
+}
+
+template <int MODE>
+__device__ __forceinline__ void gemm_fast_body(const GemmArgs& p) {
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE_BYTES];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 2;  // 0..1 -> 128 rows of M
+  const int wn = wave & 3;   // 0..3 -> 64 cols of N
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+  constexpr int ES = (MODE == GEMM_I8) ? 1 : 2;  // element bytes
+  const long long lda_b = p.a_s0 * ES;
+  const long long ldb_b = p.b_s0 * ES;  // Bt row stride (n) in bytes
+  const char* abase = (const char*)p.a + (long long)m0 * lda_b;
+  const char* bbase = (const char*)p.b + (long long)n0 * ldb_b;
+  const int a_lim = p.M - 1 - m0;
+  const int b_lim = p.N - 1 - n0;
+  const int kslabs = (p.K * ES) / SLAB;
+
+  f32x16 accf[4][2];
+  i32x16 acci[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if constexpr (MODE == GEMM_I8) acci[i][j] = (i32x16){};
+      else accf[i][j] = (f32x16){};
+    }
+
+  auto issue = [&](int stage, int slab) {
+    char* sa = lds + stage * STAGE_BYTES;
+    char* sb = sa + BM * SLAB;
+    const long long kb = (long long)slab * SLAB;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int rg = wave * 4 + t;  // 8-row group 0..31
+      dma_rows(abase, lda_b, rg * 8, a_lim, kb, sa + rg * 1024, lane);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int rg = wave * 4 + t;
+      dma_rows(bbase, ldb_b, rg * 8, b_lim, kb, sb + rg * 1024, lane);
+    }
+  };
+
+  issue(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  const int g = lane >> 5;
+  const int r = lane & 31;
+  for (int kt = 0; kt < kslabs; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < kslabs) issue(cur ^ 1, kt + 1);
+    const char* sa = lds + cur * STAGE_BYTES;
+    const char* sb = sa + BM * SLAB;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int chunk = ks * 2 + g;
+      u32x4 af[4], bfr[2];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        const int row = wm * 128 + mi * 32 + r;
+        af[mi] = *(const u32x4*)(sa + row * SLAB + ((chunk ^ swz(row)) << 4));
+      }
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const int row = wn * 64 + ni * 32 + r;
+        bfr[ni] = *(const u32x4*)(sb + row * SLAB + ((chunk ^ swz(row)) << 4));
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+          if constexpr (MODE == GEMM_BF16) {
+            accf[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8, bfr[ni]), __builtin_bit_cast(bf16x8, af[mi]),
+                accf[mi][ni], 0, 0, 0);
+          } else if constexpr (MODE == GEMM_F16) {
+            accf[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                __builtin_bit_cast(f16x8, bfr[ni]), __builtin_bit_cast(f16x8, af[mi]),
+                accf[mi][ni], 0, 0, 0);
+          } else {
+            acci[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                __builtin_bit_cast(i32x4, bfr[ni]), __builtin_bit_cast(i32x4, af[mi]),
+                acci[mi][ni], 0, 0, 0);
+          }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds C[m][n..n+3] for m = row r of each 32-row fragment,
+  // n = 8q + 4g + {0..3} of each 32-column fragment.
+  const bool vec_ok = ((p.c_s0 & 3) == 0);
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    const int m = m0 + wm * 128 + mi * 32 + r;
+    if (m >= p.M) continue;
+    float rs = 1.0f;
+    if constexpr (MODE == GEMM_I8) rs = p.sa ? p.sa[m] : 1.0f;
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * 64 + ni * 32 + q * 8 + g * 4;
+        float v[4];
+        if constexpr (MODE == GEMM_I8) {
+          int iv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) iv[e] = acci[mi][ni][q * 4 + e];
+          if (p.acc_out) {
+            int* dst = p.acc_out + (long long)m * p.acc_s0 + n;
+            if (vec_ok && ((p.acc_s0 & 3) == 0) && n + 3 < p.N) {
+              *(i32x4*)dst = (i32x4){iv[0], iv[1], iv[2], iv[3]};
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (n + e < p.N) dst[e] = iv[e];
+            }
+          }
+          if (!p.sa) continue;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float sbv = (n + e < p.N) ? p.sb[n + e] : 0.0f;
+            v[e] = ((float)iv[e] * rs) * sbv;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = accf[mi][ni][q * 4 + e];
+        }
+        char* crow = (char*)p.c + (long long)m * p.c_s0 * (p.c_dtype == DT_F32 ? 4 : 2);
+        if (p.c_dtype == DT_F32) {
+          float* dst = (float*)crow + n;
+          if (vec_ok && n + 3 < p.N) {
+            *(f32x4*)dst = (f32x4){v[0], v[1], v[2], v[3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < p.N) dst[e] = v[e];
+          }
+        } else {
+          uint16_t h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = (p.c_dtype == DT_BF16) ? f32_to_bf16(v[e]) : f32_to_f16(v[e]);
+          uint16_t* dst = (uint16_t*)crow + n;
+          if (vec_ok && n + 3 < p.N) {
+            *(u32x2*)dst = (u32x2){(uint32_t)h[0] | ((uint32_t)h[1] << 16),
+                                   (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < p.N) dst[e] = h[e];
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ general GEMM
+// 64x64 output tile, 256 threads, each 4x4 outputs; K in steps of 16 staged
+// through LDS with bounds-checked element loads (zero fill past the edges).
+template <bool INT8>
+__device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
+  __shared__ float As[16][64 + 1];
+  __shared__ float Bs[16][64 + 1];
+  __shared__ int Ai[16][64 + 1];
+  __shared__ int Bi[16][64 + 1];
+  const int tid = threadIdx.x;
+  const int tm = blockIdx.x / p.tiles_n;
+  const int tn = blockIdx.x % p.tiles_n;
+  const int m0 = tm * 64, n0 = tn * 64;
+  const int tx = tid & 15, ty = tid >> 4;  // 16 x 16 threads, 4x4 each
+  float accf[4][4] = {};
+  int acci[4][4] = {};
+  for (int k0 = 0; k0 < p.K; k0 += 16) {
+    for (int e = tid; e < 16 * 64; e += 256) {
+      const int kk = e / 64, mm = e % 64;
+      const int m = m0 + mm, k = k0 + kk;
+      const bool inb = (m < p.M) && (k < p.K);
+      const long long ia = (long long)m * p.a_s0 + (long long)k * p.a_s1;
+      if (INT8) Ai[kk][mm] = inb ? (int)((const int8_t*)p.a)[ia] : 0;
+      else As[kk][mm] = inb ? load_as_f32(p.a, ia, p.a_dtype) : 0.0f;
+      const int n = n0 + mm;
+      const bool inbb = (n < p.N) && (k < p.K);
+      const long long ib = (long long)k * p.b_s0 + (long long)n * p.b_s1;
+      if (INT8) Bi[kk][mm] = inbb ? (int)((const int8_t*)p.b)[ib] : 0;
+      else Bs[kk][mm] = inbb ? load_as_f32(p.b, ib, p.b_dtype) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (INT8) acci[i][j] += Ai[kk][ty * 4 + i] * Bi[kk][tx * 4 + j];
+          else accf[i][j] = fmaf(As[kk][ty * 4 + i], Bs[kk][tx * 4 + j], accf[i][j]);
+        }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + ty * 4 + i;
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + tx * 4 + j;
+      if (n >= p.N) continue;
+      float v;
+      if (INT8) {
+        if (p.acc_out) p.acc_out[(long long)m * p.acc_s0 + n] = acci[i][j];
+        if (!p.sa) continue;
+        v = ((float)acci[i][j] * p.sa[m]) * p.sb[n];
+      } else {
+        v = accf[i][j];
+      }
+      store_from_f32(p.c, (long long)m * p.c_s0 + (long long)n * p.c_s1, p.c_dtype, v);
+    }
+  }
+}
+
+}  // namespace g950
+
+extern "C" __global__ __launch_bounds__(512) void g950_gemm_bf16_256x256(const g950::GemmArgs p) {
+  g950::gemm_fast_body<g950::GEMM_BF16>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void g950_gemm_f16_256x256(const g950::GemmArgs p) {
+  g950::gemm_fast_body<g950::GEMM_F16>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void g950_gemm_i8_256x256(const g950::GemmArgs p) {
+  g950::gemm_fast_body<g950::GEMM_I8>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void g950_gemm_general(const g950::GemmArgs p) {
+  g950::gemm_general_body<false>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void g950_gemm_general_i8(const g950::GemmArgs p) {
+  g950::gemm_general_body<true>(p);
+}

@@ -1,0 +1,345 @@
+// Row-reduction family on gfx950: softmax, RMSNorm, LayerNorm.
+//
+// Operator semantics (reference, per row of the last axis):
+//   softmax   ops/suite/perf/softmax.py:21-32 (masked tail reads -inf,
+//             contributes exp(-inf)=0), online form for long rows
+//             ops/suite/dev/softmax_kernel_inner.py:12-72
+//   RMSNorm   ops/suite/perf/fast_rms_layernorm.py:20-42:
+//             inv = 1/sqrt(sum(x^2)/n + eps); r[row] = inv; Y = (x*inv)*w
+//   LayerNorm ops/suite/dev/fused_layernorm_triton.py:27-42: mean; centered
+//             variance; rstd = 1/sqrt(var+eps); Y = (x-mean)*rstd*w + b
+// All arithmetic is fp32; 16-bit inputs widen exactly and outputs round once.
+//
+// Two kernel shapes:
+//   rr_regs  -- the row lives in registers.  One workgroup (BLOCK threads) per
+//               row; each thread owns ITEMS vectors of VEC elements
+//               (VEC*sizeof(T) = 16 B => one 128-bit load each).  The tail of a
+//               non-power-of-two row is a per-vector predicate; x is read from
+//               HBM exactly once and y written once.
+//   rr_loop  -- rows longer than the register budget: scalar strided passes
+//               (softmax: online max/sum then output; norms: statistics then
+//               output), reading x two (three for LayerNorm) times.
+#include "g950_common.h"
+
+namespace g950 {
+
+enum RowOp : int { ROW_SOFTMAX = 0, ROW_RMSNORM = 1, ROW_LAYERNORM = 2 };
+
+
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int VEC = 4;
+  static __device__ __forceinline__ float to_f32(float v) { return v; }
+  static __device__ __forceinline__ float from_f32(float v) { return v; }
+};
+template <> struct Elem<bf16_t> {
+  static constexpr int VEC = 8;
+  static __device__ __forceinline__ float to_f32(uint16_t v) { return bf16_to_f32(v); }
+  static __device__ __forceinline__ uint16_t from_f32(float v) { return f32_to_bf16(v); }
+};
+template <> struct Elem<f16_t> {
+  static constexpr int VEC = 8;
+  static __device__ __forceinline__ float to_f32(uint16_t v) { return f16_to_f32(v); }
+  static __device__ __forceinline__ uint16_t from_f32(float v) { return f32_to_f16(v); }
+};
+
+// Load VEC elements (VEC>1: one aligned 16-byte load) widened to fp32.
+template <typename T, int VEC>
+__device__ __forceinline__ void load_vec(const void* base, long long idx, float* out) {
+  if constexpr (sizeof(T) == 4) {
+    if constexpr (VEC == 4) {
+      f32x4 v = __builtin_nontemporal_load((const f32x4*)((const float*)base + idx));
+      out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+    } else {
+      out[0] = ((const float*)base)[idx];
+    }
+  } else {
+    if constexpr (VEC == 8) {
+      u32x4 v = __builtin_nontemporal_load((const u32x4*)((const uint16_t*)base + idx));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out[2 * i] = Elem<T>::to_f32((uint16_t)(v[i] & 0xFFFFu));
+        out[2 * i + 1] = Elem<T>::to_f32((uint16_t)(v[i] >> 16));
+      }
+    } else {
+      out[0] = Elem<T>::to_f32(((const uint16_t*)base)[idx]);
+    }
+  }
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_vec(void* base, long long idx, const float* in) {
+  if constexpr (sizeof(T) == 4) {
+    if constexpr (VEC == 4) {
+      f32x4 v = {in[0], in[1], in[2], in[3]};
+      __builtin_nontemporal_store(v, (f32x4*)((float*)base + idx));
+    } else {
+      ((float*)base)[idx] = in[0];
+    }
+  } else {
+    if constexpr (VEC == 8) {
+      u32x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[i] = (uint32_t)Elem<T>::from_f32(in[2 * i]) | ((uint32_t)Elem<T>::from_f32(in[2 * i + 1]) << 16);
+      __builtin_nontemporal_store(v, (u32x4*)((uint16_t*)base + idx));
+    } else {
+      ((uint16_t*)base)[idx] = Elem<T>::from_f32(in[0]);
+    }
+  }
+}
+
+// Weights are re-read by every row: keep them cacheable (plain loads).
+template <typename T, int VEC>
+__device__ __forceinline__ void load_param(const void* base, long long idx, float* out) {
+  if constexpr (sizeof(T) == 4) {
+    if constexpr (VEC == 4) {
+      f32x4 v = *(const f32x4*)((const float*)base + idx);
+      out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+    } else {
+      out[0] = ((const float*)base)[idx];
+    }
+  } else {
+    if constexpr (VEC == 8) {
+      u32x4 v = *(const u32x4*)((const uint16_t*)base + idx);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out[2 * i] = Elem<T>::to_f32((uint16_t)(v[i] & 0xFFFFu));
+        out[2 * i + 1] = Elem<T>::to_f32((uint16_t)(v[i] >> 16));
+      }
+    } else {
+      out[0] = Elem<T>::to_f32(((const uint16_t*)base)[idx]);
+    }
+  }
+}
+
+template <int OP, typename T, int VEC, int ITEMS, int BLOCK>
+__device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
+  __shared__ float scratch[BLOCK / 64 > 0 ? BLOCK / 64 : 1];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nvec = a.cols / VEC;  // host guarantees cols % VEC == 0
+  const void* xrow = (const char*)a.x + (long long)row * a.x_row * (long long)sizeof(T);
+  void* yrow = (char*)a.y + (long long)row * a.y_row * (long long)sizeof(T);
+
+  float v[ITEMS][VEC];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int j = tid + i * BLOCK;
+    if (j < nvec) {
+      load_vec<T, VEC>(xrow, (long long)j * VEC, v[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[i][e] = (OP == ROW_SOFTMAX) ? -__builtin_huge_valf() : 0.0f;
+    }
+  }
+
+  if constexpr (OP == ROW_SOFTMAX) {
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) m = fmaxf(m, v[i][e]);
+    m = block_reduce<OpMax, BLOCK>(m, scratch);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        v[i][e] = expf(v[i][e] - m);  // masked lanes: exp(-inf) = 0
+        s += v[i][e];
+      }
+    s = block_reduce<OpSum, BLOCK>(s, scratch);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = tid + i * BLOCK;
+      if (j < nvec) {
+        float o[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * inv;
+        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+      }
+    }
+  } else if constexpr (OP == ROW_RMSNORM) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ss = fmaf(v[i][e], v[i][e], ss);
+    ss = block_reduce<OpSum, BLOCK>(ss, scratch);
+    const float inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+    if (tid == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, inv);
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = tid + i * BLOCK;
+      if (j < nvec) {
+        float w[VEC], o[VEC];
+        load_param<T, VEC>(a.w, (long long)j * VEC, w);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] * inv) * w[e];
+        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+      }
+    }
+  } else {  // LayerNorm, centered two-pass from registers
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += v[i][e];
+    s = block_reduce<OpSum, BLOCK>(s, scratch);
+    const float mean = s / (float)a.cols;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = tid + i * BLOCK;
+      if (j < nvec) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          v[i][e] -= mean;
+          q = fmaf(v[i][e], v[i][e], q);
+        }
+      }
+    }
+    q = block_reduce<OpSum, BLOCK>(q, scratch);
+    const float rstd = 1.0f / sqrtf(q / (float)a.cols + a.eps);
+    if (tid == 0) {
+      store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mean);
+      store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, rstd);
+    }
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = tid + i * BLOCK;
+      if (j < nvec) {
+        float w[VEC], bb[VEC], o[VEC];
+        load_param<T, VEC>(a.w, (long long)j * VEC, w);
+        load_param<T, VEC>(a.b, (long long)j * VEC, bb);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * rstd * w[e] + bb[e];
+        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+      }
+    }
+  }
+}
+
+// Long rows: strided scalar passes over global memory.
+template <int OP, typename T, int BLOCK>
+__device__ __forceinline__ void rr_loop_body(const RowArgs& a) {
+  __shared__ float scratch[BLOCK / 64];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int n = a.cols;
+  const void* xrow = (const char*)a.x + (long long)row * a.x_row * (long long)sizeof(T);
+  void* yrow = (char*)a.y + (long long)row * a.y_row * (long long)sizeof(T);
+  float xv;
+  if constexpr (OP == ROW_SOFTMAX) {
+    // online max/sum (softmax_kernel_inner.py:12-72): z is rescaled whenever
+    // the running max grows
+    float m = -__builtin_huge_valf(), z = 0.0f;
+    for (int j = tid; j < n; j += BLOCK) {
+      load_vec<T, 1>(xrow, j, &xv);
+      const float mn = fmaxf(m, xv);
+      z = z * expf(m - mn) + expf(xv - mn);
+      m = mn;
+    }
+    const float mrow = block_reduce<OpMax, BLOCK>(m, scratch);
+    z = (m == -__builtin_huge_valf()) ? 0.0f : z * expf(m - mrow);
+    const float zrow = block_reduce<OpSum, BLOCK>(z, scratch);
+    const float inv = 1.0f / zrow;
+    for (int j = tid; j < n; j += BLOCK) {
+      load_vec<T, 1>(xrow, j, &xv);
+      float o = expf(xv - mrow) * inv;
+      store_vec<T, 1>(yrow, j, &o);
+    }
+  } else if constexpr (OP == ROW_RMSNORM) {
+    float ss = 0.0f;
+    for (int j = tid; j < n; j += BLOCK) {
+      load_vec<T, 1>(xrow, j, &xv);
+      ss = fmaf(xv, xv, ss);
+    }
+    ss = block_reduce<OpSum, BLOCK>(ss, scratch);
+    const float inv = 1.0f / sqrtf(ss / (float)n + a.eps);
+    if (tid == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, inv);
+    for (int j = tid; j < n; j += BLOCK) {
+      float w;
+      load_vec<T, 1>(xrow, j, &xv);
+      load_param<T, 1>(a.w, j, &w);
+      float o = (xv * inv) * w;
+      store_vec<T, 1>(yrow, j, &o);
+    }
+  } else {
+    float s = 0.0f;
+    for (int j = tid; j < n; j += BLOCK) {
+      load_vec<T, 1>(xrow, j, &xv);
+      s += xv;
+    }
+    const float mean = block_reduce<OpSum, BLOCK>(s, scratch) / (float)n;
+    float q = 0.0f;
+    for (int j = tid; j < n; j += BLOCK) {
+      load_vec<T, 1>(xrow, j, &xv);
+      const float c = xv - mean;
+      q = fmaf(c, c, q);
+    }
+    q = block_reduce<OpSum, BLOCK>(q, scratch);
+    const float rstd = 1.0f / sqrtf(q / (float)n + a.eps);
+    if (tid == 0) {
+      store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mean);
+      store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, rstd);
+    }
+    for (int j = tid; j < n; j += BLOCK) {
+      float w, bb;
+      load_vec<T, 1>(xrow, j, &xv);
+      load_param<T, 1>(a.w, j, &w);
+      load_param<T, 1>(a.b, j, &bb);
+      float o = (xv - mean) * rstd * w + bb;
+      store_vec<T, 1>(yrow, j, &o);
+    }
+  }
+}
+
+}  // namespace g950
+
+// ------------------------------------------------------------------ symbols
+// Kernel names: g950_rr_<op>_<dtype>_v<VEC>_i<ITEMS>_b<BLOCK> and
+// g950_rr_loop_<op>_<dtype>.  The launcher (g950rt.cpp) picks the smallest
+// register configuration whose BLOCK*ITEMS*VEC covers the row.
+#define G950_RR_REGS(OPNAME, OP, TNAME, T, VEC, ITEMS, BLOCK)                              \
+  extern "C" __global__ __launch_bounds__(BLOCK) void                                    \
+      g950_rr_##OPNAME##_##TNAME##_v##VEC##_i##ITEMS##_b##BLOCK(const g950::RowArgs a) { \
+    g950::rr_regs_body<OP, T, VEC, ITEMS, BLOCK>(a);                                     \
+  }
+
+#define G950_RR_LOOP(OPNAME, OP, TNAME, T)                                                 \
+  extern "C" __global__ __launch_bounds__(256) void g950_rr_loop_##OPNAME##_##TNAME(       \
+      const g950::RowArgs a) {                                                             \
+    g950::rr_loop_body<OP, T, 256>(a);                                                     \
+  }
+
+// register configurations: (VEC, ITEMS, BLOCK).  Vector forms need
+// cols % VEC == 0 and 16-byte aligned rows; VEC=1 forms take any row.
+#define G950_RR_SET(OPNAME, OP, TNAME, T, V)            \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 1, 64)          \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 2, 64)          \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 4, 64)          \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 8, 64)          \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 3, 128)         \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 4, 128)         \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 4, 256)         \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 8, 256)         \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 16, 256)
+
+#define G950_RR_ALL(OPNAME, OP)                                          \
+  G950_RR_SET(OPNAME, OP, f32, float, 4)                                 \
+  G950_RR_SET(OPNAME, OP, f32, float, 1)                                 \
+  G950_RR_SET(OPNAME, OP, bf16, g950::bf16_t, 8)                         \
+  G950_RR_SET(OPNAME, OP, bf16, g950::bf16_t, 1)                         \
+  G950_RR_SET(OPNAME, OP, f16, g950::f16_t, 8)                           \
+  G950_RR_SET(OPNAME, OP, f16, g950::f16_t, 1)                           \
+  G950_RR_LOOP(OPNAME, OP, f32, float)                                   \
+  G950_RR_LOOP(OPNAME, OP, bf16, g950::bf16_t)                           \
+  G950_RR_LOOP(OPNAME, OP, f16, g950::f16_t)
+
+G950_RR_ALL(softmax, g950::ROW_SOFTMAX)
+G950_RR_ALL(rmsnorm, g950::ROW_RMSNORM)
+G950_RR_ALL(layernorm, g950::ROW_LAYERNORM)

@@ -1,0 +1,151 @@
+"""The hot-path operators behind the reference kernels' own call signatures.
+
+Each function takes the arguments of the reference Triton kernel it replaces
+(same names, same meaning; pointer arguments are torch-ROCm device tensors,
+runtime scalars are ints/floats) and launches the gfx950 kernel through the
+C ABI.  Views and scalars are handed over in sorted argument-name order, the
+layout the reference host packer produces (a100_support/native_io.py:74,81).
+
+The triton launch grid and constexpr block sizes of the reference are not
+arguments here: the launcher derives the grid from the view extents, and the
+constexprs only shaped the reference's tiles.  The one constexpr with
+semantics, attention's ``CAUSAL``, is a keyword argument.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import runtime as rt
+
+
+def _launch(op, named_tensors: dict, outputs: set, named_scalars: dict, stream=None, sync=False):
+    names = sorted(named_tensors)
+    tensors = [named_tensors[n] for n in names]
+    outs = [n in outputs for n in names]
+    scalars = [named_scalars[n] if isinstance(named_scalars[n], rt.Scalar) else rt.scalar(named_scalars[n])
+               for n in sorted(named_scalars)]
+    return rt.module().launch(op, tensors, outs, scalars, stream=stream, sync=sync)
+
+
+def softmax_kernel(x_ptr, y_ptr, n_cols, *, stream=None, sync=False):
+    """Row softmax (ops/suite/perf/softmax.py:21-32).  x/y: [rows, n_cols]."""
+    return _launch(rt.OP_SOFTMAX, {"x_ptr": x_ptr, "y_ptr": y_ptr}, {"y_ptr"},
+                   {"n_cols": n_cols}, stream, sync)
+
+
+def rms_layernorm_forward_kernel(Y, Y_row_stride, X, X_row_stride, W, W_row_stride, r,
+                                 r_row_stride, n_cols, eps, *, stream=None, sync=False):
+    """RMSNorm forward (ops/suite/perf/fast_rms_layernorm.py:20-42)."""
+    return _launch(rt.OP_RMS_LAYERNORM, {"Y": Y, "X": X, "W": W, "r": r}, {"Y", "r"},
+                   {"Y_row_stride": Y_row_stride, "X_row_stride": X_row_stride,
+                    "W_row_stride": W_row_stride, "r_row_stride": r_row_stride,
+                    "n_cols": n_cols, "eps": np.float32(eps)}, stream, sync)
+
+
+def layernorm_kernel(X, Y, W, B, Mean, Rstd, stride, N, eps, *, stream=None, sync=False):
+    """LayerNorm forward with Mean/Rstd outputs
+    (ops/suite/dev/fused_layernorm_triton.py:27-42)."""
+    return _launch(rt.OP_LAYERNORM, {"X": X, "Y": Y, "W": W, "B": B, "Mean": Mean, "Rstd": Rstd},
+                   {"Y", "Mean", "Rstd"}, {"stride": stride, "N": N, "eps": np.float32(eps)},
+                   stream, sync)
+
+
+def matmul_kernel(a_ptr, b_ptr, y_ptr, M, N, K, *, stream=None, sync=False):
+    """Y = A.B with fp32 accumulation (ops/suite/perf/matmul.py:21-37).
+    ``b_ptr`` is the logical [K, N] operand; a column-major (K-contiguous) b,
+    e.g. ``bt.t()`` of a row-major [N, K] tensor, takes the MFMA path."""
+    return _launch(rt.OP_MATMUL, {"a_ptr": a_ptr, "b_ptr": b_ptr, "y_ptr": y_ptr}, {"y_ptr"},
+                   {"M": M, "N": N, "K": K}, stream, sync)
+
+
+def matmul_i8_kernel(a_ptr, b_ptr, c_ptr, M, N, K, *, stream=None, sync=False):
+    """int8 x int8 -> int32, bit-exact modular accumulation
+    (i8 dot family, a100c/plan/tiles.py:118-131)."""
+    return _launch(rt.OP_MATMUL_I8, {"a_ptr": a_ptr, "b_ptr": b_ptr, "c_ptr": c_ptr}, {"c_ptr"},
+                   {"M": M, "N": N, "K": K}, stream, sync)
+
+
+def matmul_i8_dequant_kernel(a_ptr, b_ptr, sa_ptr, sb_ptr, y_ptr, M, N, K, *, stream=None,
+                             sync=False):
+    """int8 GEMM + dequant epilogue: y = bf16(acc * sa[m] * sb[n])
+    (per-column rule of ops/suite/perf/dequantize_matmul.py:29-38)."""
+    return _launch(rt.OP_MATMUL_I8_DEQUANT,
+                   {"a_ptr": a_ptr, "b_ptr": b_ptr, "sa_ptr": sa_ptr, "sb_ptr": sb_ptr,
+                    "y_ptr": y_ptr}, {"y_ptr"}, {"M": M, "N": N, "K": K}, stream, sync)
+
+
+def attn_fwd_causal_kernel(q_ptr, k_ptr, v_ptr, out_ptr, Z, H, N_CTX, scale,
+                           stride_qz, stride_qh, stride_qm, stride_qk,
+                           stride_kz, stride_kh, stride_kn, stride_kk,
+                           stride_vz, stride_vh, stride_vk, stride_vn,
+                           stride_oz, stride_oh, stride_om, stride_on,
+                           *, CAUSAL=True, lse_ptr=None, stream=None, sync=False):
+    """Attention forward (ops/suite/perf/attn_fwd_causal.py:20-55), with GQA
+    when k/v carry fewer heads (ops/suite/dev/gqa.py:29) and the optional
+    per-row logsumexp (ops/suite/dev/flash_varlen_fwd_kernel.py:309,318-320)."""
+    tensors = {"q_ptr": q_ptr, "k_ptr": k_ptr, "v_ptr": v_ptr, "out_ptr": out_ptr}
+    outputs = {"out_ptr"}
+    op = rt.OP_ATTENTION
+    if lse_ptr is not None:
+        tensors["lse_ptr"] = lse_ptr
+        outputs.add("lse_ptr")
+        op = rt.OP_ATTENTION_LSE
+    scalars = {"CAUSAL": bool(CAUSAL), "Z": Z, "H": H, "N_CTX": N_CTX,
+               "scale": np.float32(scale) if not isinstance(scale, np.generic) else scale,
+               "stride_qz": stride_qz, "stride_qh": stride_qh, "stride_qm": stride_qm,
+               "stride_qk": stride_qk, "stride_kz": stride_kz, "stride_kh": stride_kh,
+               "stride_kn": stride_kn, "stride_kk": stride_kk, "stride_vz": stride_vz,
+               "stride_vh": stride_vh, "stride_vk": stride_vk, "stride_vn": stride_vn,
+               "stride_oz": stride_oz, "stride_oh": stride_oh, "stride_om": stride_om,
+               "stride_on": stride_on}
+    return _launch(op, tensors, outputs, scalars, stream, sync)
+
+
+# ------------------------------------------------------ tensor conveniences
+def softmax(x, out=None, **kw):
+    import torch
+    y = torch.empty_like(x) if out is None else out
+    softmax_kernel(x, y, x.shape[-1], **kw)
+    return y
+
+
+def rmsnorm(x, w, eps, out=None, r=None, **kw):
+    import torch
+    y = torch.empty_like(x) if out is None else out
+    r = torch.empty(x.shape[0], dtype=torch.float32, device=x.device) if r is None else r
+    rms_layernorm_forward_kernel(y, y.stride(0), x, x.stride(0), w, 1, r, r.stride(0),
+                                 x.shape[1], eps, **kw)
+    return y, r
+
+
+def layernorm(x, w, b, eps, out=None, mean=None, rstd=None, **kw):
+    import torch
+    y = torch.empty_like(x) if out is None else out
+    mean = torch.empty(x.shape[0], dtype=torch.float32, device=x.device) if mean is None else mean
+    rstd = torch.empty(x.shape[0], dtype=torch.float32, device=x.device) if rstd is None else rstd
+    layernorm_kernel(x, y, w, b, mean, rstd, x.stride(0), x.shape[1], eps, **kw)
+    return y, mean, rstd
+
+
+def matmul(a, b, out=None, **kw):
+    """a [M,K] @ b [K,N] (pass ``bt.t()`` for a K-contiguous b)."""
+    import torch
+    m, k = a.shape
+    n = b.shape[1]
+    y = torch.empty((m, n), dtype=a.dtype, device=a.device) if out is None else out
+    matmul_kernel(a, b, y, m, n, k, **kw)
+    return y
+
+
+def attention(q, k, v, scale=None, causal=True, out=None, lse=None, **kw):
+    import torch
+    z, h, s, d = q.shape
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    o = torch.empty_like(q) if out is None else out
+    if lse is None:
+        lse = torch.empty((z, h, s), dtype=torch.float32, device=q.device)
+    attn_fwd_causal_kernel(q, k, v, o, z, h, s, scale, *q.stride(), *k.stride(), *v.stride(),
+                           *o.stride(), CAUSAL=causal, lse_ptr=lse, **kw)
+    return o, lse

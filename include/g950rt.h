@@ -1,0 +1,163 @@
+/* g950rt.h -- C ABI of the gfx950 hot-path module loader and launcher.
+ *
+ * One shared library (libg950rt.so) loads ONE code object (g950.hsaco, every
+ * hot-path kernel built for gfx950) and launches an operator on caller-owned
+ * device buffers.  It replaces, for the hot-path operators, the reference's
+ * native runtime boundary:
+ *
+ *   reference                                   here
+ *   a100c/runtime/a100rt.h:79-89  a100rt_view    g950_view   (same fields, 56 B)
+ *   a100c/runtime/a100rt.h:94-98  a100rt_scalar  g950_scalar (same fields, 16 B)
+ *   a100c/runtime/a100rt.h:58-72  dtype codes    G950_DTYPE_* (same values)
+ *   a100c/runtime/a100rt.h:50-55  exit codes     G950_* return codes (same values)
+ *   a100c/runtime/a100rt.h:176    operator_entry(launch)  -> g950_launch(...)
+ *   a100c/runtime/main.c:50-177   operator_exec process    -> g950_open/launch/sync/close
+ *
+ * Views and scalars are passed in SORTED ARGUMENT-NAME order, exactly as the
+ * reference host packer lays them out (a100_support/native_io.py:74,81); the
+ * binary carries no names.  `data` of a view is a DEVICE pointer; shape and
+ * strides (bytes) are host arrays.  Output views carry flag bit 0.
+ *
+ * Calls are asynchronous on `stream` (a hipStream_t; NULL = the null stream);
+ * g950_sync() waits, so "launch then sync" meets the reference contract that a
+ * launch has finished before it returns (ops/harness/compiler_api/
+ * COMPILE_CONTRACT.md:73-74).  No C++ exception crosses this boundary.  Every
+ * refusal happens on the host before any kernel is launched.
+ */
+#ifndef G950RT_H
+#define G950RT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define G950_ABI_VERSION 1
+
+/* return codes (values of A100RT_EXIT_*, a100c/runtime/a100rt.h:50-55) */
+#define G950_OK 0
+#define G950_USAGE 2      /* operator contract / shape / scalar refused */
+#define G950_REJECTED 3   /* a view violates its storage or layout rules */
+#define G950_RESOURCE 4   /* HIP error: module load, launch, allocation */
+#define G950_SYNC 6       /* stream synchronisation failed */
+
+/* dtype codes (a100c/runtime/a100rt.h:58-72) */
+enum g950_dtype {
+  G950_DTYPE_BOOL = 1, G950_DTYPE_INT8 = 2, G950_DTYPE_UINT8 = 3,
+  G950_DTYPE_INT16 = 4, G950_DTYPE_UINT16 = 5, G950_DTYPE_INT32 = 6,
+  G950_DTYPE_UINT32 = 7, G950_DTYPE_INT64 = 8, G950_DTYPE_UINT64 = 9,
+  G950_DTYPE_FLOAT16 = 10, G950_DTYPE_BFLOAT16 = 11, G950_DTYPE_FLOAT32 = 12,
+  G950_DTYPE_FLOAT64 = 13
+};
+
+#define G950_VIEW_OUTPUT 1u
+
+/* A strided view over one device allocation (layout of a100rt_view). */
+typedef struct g950_view {
+  void *data;              /* element base (device address) */
+  const int64_t *shape;    /* ndim extents (host) */
+  const int64_t *strides;  /* ndim BYTE strides (host) */
+  uint64_t storage_size;   /* bytes of the allocation `storage` points at */
+  uint32_t dtype;          /* enum g950_dtype */
+  uint32_t ndim;
+  uint32_t flags;          /* bit 0: output */
+  uint32_t reserved_;
+  void *storage;           /* allocation base (device address) */
+} g950_view;
+
+/* A typed scalar (layout of a100rt_scalar): raw little-endian value bits. */
+typedef struct g950_scalar {
+  uint32_t dtype;
+  uint32_t size;
+  uint64_t bits;
+} g950_scalar;
+
+/* Operator contracts.  Each names the reference kernel whose call signature
+ * it takes; views / scalars are that kernel's arguments in sorted-name order.
+ *
+ * G950_OP_SOFTMAX      softmax_kernel (ops/suite/perf/softmax.py:21-32)
+ *   views   x_ptr[R,C], y_ptr[R,C]                  f32 | bf16 | f16 (same)
+ *   scalars n_cols
+ * G950_OP_RMS_LAYERNORM  rms_layernorm_forward_kernel
+ *                      (ops/suite/perf/fast_rms_layernorm.py:20-42)
+ *   views   W[C], X[R,C], Y[R,C], r[R]
+ *   scalars W_row_stride, X_row_stride, Y_row_stride, eps, n_cols, r_row_stride
+ * G950_OP_LAYERNORM    layernorm_kernel (ops/suite/dev/fused_layernorm_triton.py:27-42)
+ *   views   B[C], Mean[R], Rstd[R], W[C], X[R,C], Y[R,C]
+ *   scalars N, eps, stride
+ * G950_OP_MATMUL       matmul_kernel (ops/suite/perf/matmul.py:21-37)
+ *   views   a_ptr[M,K], b_ptr[K,N] (any strides; K-contiguous b = column-major
+ *           takes the MFMA path), y_ptr[M,N]
+ *   scalars K, M, N
+ * G950_OP_MATMUL_I8    int8 tl.dot, int32 accumulate (a100c/plan/tiles.py:118-131)
+ *   views   a_ptr i8[M,K], b_ptr i8[K,N], c_ptr i32[M,N]
+ *   scalars K, M, N
+ * G950_OP_MATMUL_I8_DEQUANT  int8 GEMM + dequant epilogue
+ *                      (per-column rule of ops/suite/perf/dequantize_matmul.py:29-38
+ *                      plus a per-row A scale): y = bf16(acc * sa[m] * sb[n])
+ *   views   a_ptr i8[M,K], b_ptr i8[K,N], sa_ptr f32[M], sb_ptr f32[N], y_ptr[M,N]
+ *   scalars K, M, N
+ * G950_OP_ATTENTION    attn_fwd_causal_kernel (ops/suite/perf/attn_fwd_causal.py:20-55)
+ *                      with GQA (K/V may have fewer heads, ops/suite/dev/gqa.py:29)
+ *   views   k_ptr[Z,Hkv,S,D], out_ptr[Z,H,S,D], q_ptr[Z,H,S,D], v_ptr[Z,Hkv,S,D]
+ *   scalars CAUSAL, H, N_CTX, Z, scale, stride_* (16 element strides)
+ * G950_OP_ATTENTION_LSE  same plus the per-row logsumexp output
+ *                      (ops/suite/dev/flash_varlen_fwd_kernel.py:309,318-320)
+ *   views   k_ptr, lse_ptr f32[Z,H,S], out_ptr, q_ptr, v_ptr
+ *   scalars as G950_OP_ATTENTION
+ */
+enum g950_op {
+  G950_OP_SOFTMAX = 1,
+  G950_OP_RMS_LAYERNORM = 2,
+  G950_OP_LAYERNORM = 3,
+  G950_OP_MATMUL = 4,
+  G950_OP_MATMUL_I8 = 5,
+  G950_OP_MATMUL_I8_DEQUANT = 6,
+  G950_OP_ATTENTION = 7,
+  G950_OP_ATTENTION_LSE = 8
+};
+
+typedef struct g950_module g950_module;
+
+/* Load the code object at `code_object_path` on the current HIP device.
+ * Replaces the reference's per-operator executable load (a100c/runtime/main.c:50-110). */
+int g950_open(const char *code_object_path, g950_module **out);
+
+/* Validate the views/scalars against the operator contract, choose the kernel
+ * variant from dtypes, shapes and strides, and launch it on `stream`.
+ * Replaces operator_entry (a100c/runtime/a100rt.h:176) run by the worker pool
+ * (a100c/runtime/pool.c:155-161). */
+int g950_launch(g950_module *module, uint32_t op, const g950_view *views, uint32_t nviews,
+                const g950_scalar *scalars, uint32_t nscalars, void *stream);
+
+/* Run every contract check and the kernel choice of g950_launch without
+ * touching a device (no module, no HIP call).  On success
+ * g950_last_kernel() names the kernel g950_launch would run.  The views'
+ * pointers are only compared, never dereferenced. */
+int g950_validate(uint32_t op, const g950_view *views, uint32_t nviews,
+                  const g950_scalar *scalars, uint32_t nscalars);
+
+/* Name of the kernel symbol the last successful g950_launch on this thread
+ * ran (for profiling and tests); empty string if none. */
+const char *g950_last_kernel(void);
+
+/* Wait for all work on `stream`. */
+int g950_sync(void *stream);
+
+/* Static description of a return code. */
+const char *g950_strerror(int code);
+
+/* Detailed message of the last failure on this thread (like
+ * a100rt_reject_reason, a100c/runtime/bundle.c:59-88, but with context). */
+const char *g950_last_error(void);
+
+/* Unload the code object. */
+void g950_close(g950_module *module);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* G950RT_H */

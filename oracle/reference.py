@@ -1,0 +1,232 @@
+"""CPU oracle for the g950 hot path -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker, never the product: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it.  The product path (``compiler_amd``) never routes through it.
+
+Each function restates, in numpy float64, the reference operator's own ``ref``
+semantics (file:line cited per function, paths relative to the reference
+checkout).  Low-precision rounding follows the reference host conversion
+``_bf16_host`` (``ops/harness/opslib/case.py:214-220``).
+
+How each function is pinned (besides restating the formula):
+  * ``softmax``              -- reference-held post-run fixtures softmax16/97 in
+                                3 dtypes; rows sum to 1; constant row -> 1/n.
+  * ``rms_layernorm``        -- closed form: constant row c -> sign(c)*w (eps->0);
+                                scale invariance; brute-force loop on tiny rows.
+  * ``layernorm``            -- per-row output mean == beta, std == gamma when
+                                gamma/beta are constant; brute-force loop.
+  * ``matmul``               -- reference-held matmul16/128/tail fixtures in 3
+                                dtypes + matmul256 fp16; brute-force triple loop.
+  * ``matmul_i8``            -- exact integer brute force on tiny shapes; int32
+                                no-overflow bound 8192*127^2 < 2^31.
+  * ``dequant``              -- closed form vs a scalar loop; bf16 RNE rule.
+  * ``attention``            -- reference-held attention fixtures (non-causal) in
+                                3 dtypes; causal row 0 == V[0]; uniform V -> V;
+                                LSE of equal scores == s + log(n).
+  * ``bf16_round``           -- known bit patterns (ties-to-even, NaN quieting,
+                                overflow to inf) and torch's RNE conversion.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+__all__ = [
+    "bf16_round", "bf16_bits", "bf16_from_bits", "softmax", "rms_layernorm",
+    "layernorm", "matmul", "matmul_i8", "dequant", "attention", "isclose_verdict",
+    "TOLERANCES",
+]
+
+# Shared value tolerances per dtype (ops/harness/opslib/case.py:153-157) and the
+# tighter bars the hot-path contract states for the build's own configs.
+TOLERANCES = {
+    "float32": (1e-3, 1e-3),
+    "float16": (1e-2, 1e-2),
+    "bfloat16": (2e-2, 2e-2),
+}
+
+
+# --------------------------------------------------------------------- bf16
+def bf16_round(array) -> np.ndarray:
+    """float32 values rounded to bfloat16, returned as float32.
+
+    Round-to-nearest-even on the upper 16 bits; NaN keeps its payload with the
+    quiet bit set (ops/harness/opslib/case.py:214-220).
+    """
+    values = np.ascontiguousarray(array, dtype=np.float32)
+    bits = values.view(np.uint32)
+    rounded = (bits + np.uint32(0x7FFF) + ((bits >> 16) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    rounded = np.where(np.isnan(values), bits | np.uint32(0x00400000), rounded)
+    return rounded.astype(np.uint32).view(np.float32)
+
+
+def bf16_bits(array) -> np.ndarray:
+    """uint16 storage bits of ``bf16_round(array)``."""
+    return (bf16_round(array).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_from_bits(bits) -> np.ndarray:
+    """Decode uint16 bf16 storage to float32 (exact widening)."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# --------------------------------------------------------------- reductions
+def softmax(x) -> np.ndarray:
+    """Row softmax over the last axis in float64.
+
+    ops/suite/perf/softmax.py:40-45: ``e = exp(x - max); e / sum(e)``.  The
+    masked-tail form (ops/suite/dev/softmax_kernel_inner.py:12-72) pads with
+    -inf, which contributes exp(-inf) = 0, so the unpadded row is the result.
+    """
+    x64 = np.asarray(x, dtype=np.float64)
+    e = np.exp(x64 - x64.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def rms_layernorm(x, w, eps):
+    """RMSNorm forward: returns (Y, r) in float64.
+
+    ops/suite/perf/fast_rms_layernorm.py:52-61: ``var = sum(x*x)/n``,
+    ``inv = 1/sqrt(var + eps)``, ``Y = (x*inv)*w``, ``r[row] = inv``.
+    """
+    x64 = np.asarray(x, dtype=np.float64)
+    w64 = np.asarray(w, dtype=np.float64)
+    n_cols = x64.shape[-1]
+    var = (x64 * x64).sum(axis=-1, keepdims=True) / n_cols
+    inv = 1.0 / np.sqrt(var + float(eps))
+    y = (x64 * inv) * w64[None, :]
+    return y, inv.reshape(-1)
+
+
+def layernorm(x, w, b, eps):
+    """LayerNorm forward: returns (Y, Mean, Rstd) in float64.
+
+    ops/suite/dev/fused_layernorm_triton.py:49-60: centered variance
+    ``var = mean((x-mean)^2)`` (numpy ``var``), ``rstd = 1/sqrt(var+eps)``,
+    ``Y = (x-mean)*rstd*w + b``.
+    """
+    x64 = np.asarray(x, dtype=np.float64)
+    w64 = np.asarray(w, dtype=np.float64)
+    b64 = np.asarray(b, dtype=np.float64)
+    mean = x64.mean(axis=-1)
+    var = x64.var(axis=-1)
+    rstd = 1.0 / np.sqrt(var + float(eps))
+    y = (x64 - mean[:, None]) * rstd[:, None] * w64[None, :] + b64[None, :]
+    return y, mean, rstd
+
+
+# -------------------------------------------------------------------- GEMM
+def matmul(a, b) -> np.ndarray:
+    """``Y = A @ B`` in float64 (ops/suite/perf/matmul.py:46-50).
+
+    ``b`` is the logical [K, N] operand whatever its memory order.
+    """
+    return np.asarray(a, dtype=np.float64) @ np.asarray(b, dtype=np.float64)
+
+
+def matmul_i8(a, b) -> np.ndarray:
+    """Exact integer ``C = A @ B`` for int8 operands, returned as int64.
+
+    Semantics of the i8 dot family: signed operands, 32-bit accumulator
+    (a100c/plan/tiles.py:118-131; a100c/tests/test_matrix_breadth.py:365-452
+    accumulates in int64 and narrows to int32).  float64 BLAS is exact here:
+    every partial sum is an integer below 2**53 (|a*b| <= 127*128, K <= 2**20).
+    """
+    a = np.asarray(a)
+    b = np.asarray(b)
+    if a.shape[1] > (1 << 20):
+        raise ValueError("K too large for the exact float64 path")
+    return np.rint(a.astype(np.float64) @ b.astype(np.float64)).astype(np.int64)
+
+
+def dequant(acc, sa, sb) -> np.ndarray:
+    """Dequant epilogue ``acc[m,n] * sa[m] * sb[n]`` in float64.
+
+    The per-column scale is the ``dequantize_kernel`` rule
+    (ops/suite/perf/dequantize_matmul.py:29-38, ref :49-52); the per-row A
+    scale is the symmetric-activation half of the same rule.
+    """
+    acc64 = np.asarray(acc, dtype=np.float64)
+    return acc64 * np.asarray(sa, dtype=np.float64)[:, None] * np.asarray(sb, dtype=np.float64)[None, :]
+
+
+# --------------------------------------------------------------- attention
+def attention(q, k, v, scale, causal=True, block_rows=512):
+    """Flash-style attention forward in float64: returns (O, LSE).
+
+    Scores and softmax follow ops/suite/perf/attn_fwd_causal.py:63-76 (causal
+    mask ``j <= i``); the GQA head map ``h_kv = h // (Hq // Hkv)`` follows
+    ops/suite/dev/gqa.py:29 and the LSE rule ``rowmax + log(rowsum)`` on scaled
+    scores (natural log, ``+inf`` for an empty or NaN row) follows
+    ops/suite/dev/flash_varlen_fwd_kernel.py:309 and :411-418.
+
+    q: [Z, Hq, S, D]; k, v: [Z, Hkv, S, D].  Computed per (z, h) in row blocks
+    so that the score tensor never exceeds ``block_rows * S`` doubles.
+    """
+    q = np.asarray(q)
+    k = np.asarray(k)
+    v = np.asarray(v)
+    z_count, hq, s_q, d = q.shape
+    hkv = k.shape[1]
+    if hq % hkv:
+        raise ValueError("Hq must be a multiple of Hkv")
+    group = hq // hkv
+    s_k = k.shape[2]
+    out = np.empty((z_count, hq, s_q, d), dtype=np.float64)
+    lse = np.empty((z_count, hq, s_q), dtype=np.float64)
+    for z in range(z_count):
+        for h in range(hq):
+            kh = k[z, h // group].astype(np.float64)
+            vh = v[z, h // group].astype(np.float64)
+            for r0 in range(0, s_q, block_rows):
+                r1 = min(s_q, r0 + block_rows)
+                qb = q[z, h, r0:r1].astype(np.float64)
+                s = (qb @ kh.T) * float(scale)
+                if causal:
+                    rows = np.arange(r0, r1)[:, None]
+                    cols = np.arange(s_k)[None, :]
+                    s = np.where(cols <= rows, s, -np.inf)
+                m = s.max(axis=1, keepdims=True)
+                finite = np.isfinite(m)
+                m_safe = np.where(finite, m, 0.0)
+                p = np.exp(s - m_safe)
+                l = p.sum(axis=1, keepdims=True)
+                empty = (l == 0) | np.isnan(l)
+                out[z, h, r0:r1] = np.where(empty, 0.0, p / np.where(empty, 1.0, l)) @ vh
+                with np.errstate(divide="ignore"):
+                    row_lse = (m_safe + np.log(l))[:, 0]
+                lse[z, h, r0:r1] = np.where(empty[:, 0], np.inf, row_lse)
+    return out, lse
+
+
+# ------------------------------------------------------------- comparison
+def isclose_verdict(actual, expected, rtol, atol, equal_nan=True):
+    """(ok, max_abs_error) with the corpus comparator rule.
+
+    Verdict is ``np.isclose`` (|a-b| <= atol + rtol*|b|) and the error metric
+    ignores exactly-equal entries (ops/harness/opslib/compare.py:107-140).
+    """
+    a = np.asarray(actual).reshape(-1)
+    b = np.asarray(expected).reshape(-1)
+    close = np.isclose(a, b, rtol=rtol, atol=atol, equal_nan=equal_nan)
+    with np.errstate(invalid="ignore", over="ignore"):
+        delta = np.abs(a.astype(np.float64) - b.astype(np.float64))
+        equal = a == b
+        if equal_nan:
+            equal = equal | (np.isnan(a) & np.isnan(b))
+        err = float(np.where(equal, 0.0, delta).max(initial=0.0))
+    return bool(close.all()), err
+
+
+def max_rel_error(actual, expected, floor=1e-30) -> float:
+    """max |a-b| / max(|b|, floor) over all entries (the north-star 'relative')."""
+    a = np.asarray(actual, dtype=np.float64)
+    b = np.asarray(expected, dtype=np.float64)
+    return float((np.abs(a - b) / np.maximum(np.abs(b), floor)).max(initial=0.0))
+
+
+def lse_equal_scores(score: float, n: int) -> float:
+    """LSE of n equal scaled scores: s + log(n) (closed form used as a pin)."""
+    return score + math.log(n)

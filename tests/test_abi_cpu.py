@@ -1,0 +1,226 @@
+"""C-ABI library checks that need no GPU: it loads, exports every function
+include/g950rt.h declares, and its host-side contract checks and kernel
+selection (g950_validate, which never touches a device) behave as specified.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from compiler_amd import runtime as rt
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "g950rt.h"
+BASE = 0x7F0000000000  # fake device address: validate compares, never dereferences
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(g950_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_function():
+    lib = rt.load_library()
+    names = declared_functions()
+    assert set(names) == set(rt.EXPORTS)
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_record_layouts_match_reference_abi():
+    # a100c/runtime/a100rt.h:186-199 pins these sizes and offsets
+    assert ctypes.sizeof(rt.View) == 56
+    assert rt.View.data.offset == 0 and rt.View.shape.offset == 8
+    assert rt.View.strides.offset == 16 and rt.View.storage_size.offset == 24
+    assert rt.View.dtype.offset == 32 and rt.View.ndim.offset == 36
+    assert rt.View.flags.offset == 40 and rt.View.storage.offset == 48
+    assert ctypes.sizeof(rt.Scalar) == 16 and rt.Scalar.bits.offset == 8
+
+
+def test_strerror_codes():
+    lib = rt.load_library()
+    assert lib.g950_strerror(0) == b"ok"
+    assert b"refused" in lib.g950_strerror(2)
+    assert b"rejected" in lib.g950_strerror(3)
+
+
+class Args:
+    """Builds fake views (host shape/stride arrays, fake device addresses)."""
+
+    ITEM = {rt.DT_F32: 4, rt.DT_BF16: 2, rt.DT_F16: 2, rt.DT_INT8: 1, rt.DT_INT32: 4}
+
+    def __init__(self):
+        self.specs = []
+        self.keep = []
+        self.next = BASE
+
+    def view(self, shape, dtype, strides=None, output=False, offset=0, storage_extra=0):
+        isz = self.ITEM[dtype]
+        if strides is None:
+            strides = []
+            acc = 1
+            for n in reversed(shape):
+                strides.insert(0, acc)
+                acc *= n
+        reach = sum((n - 1) * s for n, s in zip(shape, strides)) + 1 if all(shape) else 0
+        storage = self.next
+        self.next += ((reach + offset) * isz + storage_extra + 4096 + 255) // 256 * 256
+        self.specs.append((shape, [s * isz for s in strides], dtype, output, storage + offset * isz,
+                           storage, (reach + offset) * isz + storage_extra))
+        return self
+
+    def build(self):
+        arr = (rt.View * len(self.specs))()
+        for i, (shape, strides, dtype, output, data, storage, size) in enumerate(self.specs):
+            s = (ctypes.c_int64 * len(shape))(*shape)
+            st = (ctypes.c_int64 * len(shape))(*strides)
+            self.keep += [s, st]
+            arr[i].data, arr[i].shape, arr[i].strides = data, s, st
+            arr[i].storage_size, arr[i].dtype, arr[i].ndim = size, dtype, len(shape)
+            arr[i].flags, arr[i].storage = int(output), storage
+        return arr
+
+
+def validate(op, args, scalars):
+    lib = rt.load_library()
+    views = args.build()
+    sc = (rt.Scalar * max(len(scalars), 1))(*[rt.scalar(*s) if isinstance(s, tuple) else rt.scalar(s)
+                                              for s in scalars])
+    rc = lib.g950_validate(op, views, len(args.specs), sc, len(scalars))
+    return rc, lib.g950_last_kernel().decode(), lib.g950_last_error().decode()
+
+
+def softmax_args(rows, cols, dtype):
+    return Args().view([rows, cols], dtype).view([rows, cols], dtype, output=True)
+
+
+@pytest.mark.parametrize("rows,cols,dtype,kernel", [
+    (4096, 4096, rt.DT_F32, "g950_rr_softmax_f32_v4_i4_b256"),
+    (8191, 3000, rt.DT_BF16, "g950_rr_softmax_bf16_v8_i3_b128"),
+    (4, 97, rt.DT_F32, "g950_rr_softmax_f32_v1_i2_b64"),
+    (4, 16, rt.DT_F16, "g950_rr_softmax_f16_v8_i1_b64"),
+    (2, 100000, rt.DT_F32, "g950_rr_loop_softmax_f32"),
+])
+def test_softmax_kernel_selection(rows, cols, dtype, kernel):
+    rc, name, err = validate(rt.OP_SOFTMAX, softmax_args(rows, cols, dtype), [cols])
+    assert rc == 0, err
+    assert name == kernel
+
+
+def test_softmax_refusals():
+    rc, _, err = validate(rt.OP_SOFTMAX, softmax_args(4, 97, rt.DT_F32), [96])
+    assert rc == rt.USAGE and "n_cols" in err
+    # output view without the output flag
+    a = Args().view([4, 97], rt.DT_F32).view([4, 97], rt.DT_F32, output=False)
+    assert validate(rt.OP_SOFTMAX, a, [97])[0] == rt.REJECTED
+    # mixed dtypes
+    a = Args().view([4, 97], rt.DT_F32).view([4, 97], rt.DT_BF16, output=True)
+    assert validate(rt.OP_SOFTMAX, a, [97])[0] == rt.USAGE
+    # wrong arity
+    assert validate(rt.OP_SOFTMAX, softmax_args(4, 97, rt.DT_F32), [97, 1])[0] == rt.USAGE
+
+
+def test_view_reach_outside_storage_is_rejected():
+    a = softmax_args(4, 97, rt.DT_F32)
+    shape, strides, dtype, out, data, storage, size = a.specs[0]
+    a.specs[0] = (shape, strides, dtype, out, data, storage, size - 4)  # one element short
+    rc, _, err = validate(rt.OP_SOFTMAX, a, [97])
+    assert rc == rt.REJECTED and "outside" in err
+
+
+def test_rms_and_layernorm_contracts():
+    a = (Args().view([3000], rt.DT_BF16).view([8191, 3000], rt.DT_BF16)
+         .view([8191, 3000], rt.DT_BF16, output=True).view([8191], rt.DT_F32, output=True))
+    scal = [1, 3000, 3000, np.float32(1e-6), 3000, 1]
+    rc, name, err = validate(rt.OP_RMS_LAYERNORM, a, scal)
+    assert rc == 0, err
+    assert name == "g950_rr_rmsnorm_bf16_v8_i3_b128"
+    bad = [1, 2999, 3000, np.float32(1e-6), 3000, 1]
+    assert validate(rt.OP_RMS_LAYERNORM, a, bad)[0] == rt.USAGE
+    ln = (Args().view([3000], rt.DT_BF16).view([8191], rt.DT_F32, output=True)
+          .view([8191], rt.DT_F32, output=True).view([3000], rt.DT_BF16)
+          .view([8191, 3000], rt.DT_BF16).view([8191, 3000], rt.DT_BF16, output=True))
+    rc, name, err = validate(rt.OP_LAYERNORM, ln, [3000, np.float32(1e-5), 3000])
+    assert rc == 0, err
+    assert name == "g950_rr_layernorm_bf16_v8_i3_b128"
+    assert validate(rt.OP_LAYERNORM, ln, [3000, np.float32(1e-5), 3001])[0] == rt.USAGE
+
+
+def gemm_args(m, n, k, dtype, col_major_b=True, out=rt.DT_BF16):
+    a = Args().view([m, k], dtype)
+    if col_major_b:
+        a.view([k, n], dtype, strides=[1, k])
+    else:
+        a.view([k, n], dtype)
+    return a.view([m, n], out, output=True)
+
+
+@pytest.mark.parametrize("m,n,k,colb,kernel", [
+    (8192, 8192, 8192, True, "g950_gemm_bf16_256x256"),
+    (4097, 11008, 4096, True, "g950_gemm_bf16_256x256"),
+    (128, 128, 128, False, "g950_gemm_general"),   # row-major B (the corpus fixtures)
+    (64, 64, 96, True, "g950_gemm_general"),       # K not a whole 64-element slab
+])
+def test_matmul_selection(m, n, k, colb, kernel):
+    rc, name, err = validate(rt.OP_MATMUL, gemm_args(m, n, k, rt.DT_BF16, colb), [k, m, n])
+    assert rc == 0, err
+    assert name == kernel
+
+
+def test_matmul_refusals():
+    assert validate(rt.OP_MATMUL, gemm_args(64, 64, 64, rt.DT_BF16), [64, 64, 65])[0] == rt.USAGE
+    a = Args().view([64, 64], rt.DT_BF16).view([32, 64], rt.DT_BF16).view([64, 64], rt.DT_BF16, output=True)
+    assert validate(rt.OP_MATMUL, a, [64, 64, 64])[0] == rt.USAGE
+
+
+def test_int8_selection():
+    a = (Args().view([4096, 8192], rt.DT_INT8).view([8192, 8192], rt.DT_INT8, strides=[1, 8192])
+         .view([4096], rt.DT_F32).view([8192], rt.DT_F32).view([4096, 8192], rt.DT_BF16, output=True))
+    rc, name, err = validate(rt.OP_MATMUL_I8_DEQUANT, a, [8192, 4096, 8192])
+    assert rc == 0, err
+    assert name == "g950_gemm_i8_256x256"
+    c = (Args().view([64, 100], rt.DT_INT8).view([100, 64], rt.DT_INT8)
+         .view([64, 64], rt.DT_INT32, output=True))
+    rc, name, err = validate(rt.OP_MATMUL_I8, c, [100, 64, 64])
+    assert rc == 0 and name == "g950_gemm_general_i8", err
+
+
+def attn_args(z, h, hkv, s, d, dtype, lse=True):
+    a = Args().view([z, hkv, s, d], dtype)
+    if lse:
+        a.view([z, h, s], rt.DT_F32, output=True)
+    a.view([z, h, s, d], dtype, output=True).view([z, h, s, d], dtype).view([z, hkv, s, d], dtype)
+    return a
+
+
+def attn_scalars(z, h, hkv, s, d, causal=True):
+    qs = [h * s * d, s * d, d, 1]
+    ks = [hkv * s * d, s * d, d, 1]
+    # sorted: CAUSAL H N_CTX Z scale stride_k(h,k,n,z) stride_o(h,m,n,z) stride_q(h,k,m,z) stride_v(h,k,n,z)
+    return [bool(causal), np.int32(h), np.int32(s), np.int32(z), np.float32(d ** -0.5),
+            ks[1], ks[3], ks[2], ks[0], qs[1], qs[2], qs[3], qs[0],
+            qs[1], qs[3], qs[2], qs[0], ks[1], ks[2], ks[3], ks[0]]
+
+
+def test_attention_selection_and_refusals():
+    rc, name, err = validate(rt.OP_ATTENTION_LSE, attn_args(4, 32, 8, 4096, 128, rt.DT_BF16),
+                             attn_scalars(4, 32, 8, 4096, 128))
+    assert rc == 0, err
+    assert name == "g950_attn_fwd_bf16_d128"
+    rc, name, err = validate(rt.OP_ATTENTION_LSE, attn_args(4, 4, 4, 32, 64, rt.DT_F32),
+                             attn_scalars(4, 4, 4, 32, 64, causal=False))
+    assert rc == 0 and name == "g950_attn_fwd_general", err
+    bad = attn_scalars(4, 32, 8, 4096, 128)
+    bad[5] += 1  # stride_kh disagrees with the k view
+    rc, _, err = validate(rt.OP_ATTENTION_LSE, attn_args(4, 32, 8, 4096, 128, rt.DT_BF16), bad)
+    assert rc == rt.USAGE and "stride_kh" in err
+    # Hq not a multiple of Hkv
+    rc, _, err = validate(rt.OP_ATTENTION_LSE, attn_args(1, 6, 4, 64, 64, rt.DT_BF16),
+                          attn_scalars(1, 6, 4, 64, 64))
+    assert rc == rt.USAGE
+
+
+def test_unknown_operator_refused():
+    rc, _, err = validate(99, softmax_args(4, 16, rt.DT_F32), [16])
+    assert rc == rt.USAGE and "unknown" in err

@@ -1,0 +1,261 @@
+"""GPU parity: every hot-path kernel, called through the C ABI, against the CPU
+oracle on the same seeded inputs and against the reference's held fixtures.
+
+Bars (written per test): fp32 reductions <= 1e-5 relative; bf16 reductions
+<= 1e-2; bf16 GEMM / attention <= 2e-2 absolute+relative (np.isclose form of
+ops/harness/opslib/compare.py:107-140); int8 accumulators bit-exact.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from compiler_amd import operators as ops  # noqa: E402
+from compiler_amd import runtime as rt  # noqa: E402
+from oracle import inputs  # noqa: E402
+from oracle import reference as ref  # noqa: E402
+from tests._fixtures import dtype_of, golden_cases, load, values  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TD = {"float32": torch.float32, "bfloat16": torch.bfloat16, "float16": torch.float16}
+
+
+def dev(a, dtype="float32"):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(DEV).to(TD[dtype])
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def rel_err(actual, expected, floor):
+    a = np.asarray(actual, dtype=np.float64)
+    b = np.asarray(expected, dtype=np.float64)
+    return float((np.abs(a - b) / np.maximum(np.abs(b), floor)).max())
+
+
+def close(actual, expected, rtol, atol):
+    ok, err = ref.isclose_verdict(actual, expected, rtol, atol)
+    assert ok, f"max abs err {err} exceeds rtol={rtol} atol={atol}"
+
+
+# ------------------------------------------------------------ reductions
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (37, 97), (5, 1), (3, 70001)])
+def test_softmax_rmsnorm_fp32(rows, cols):
+    """Config 1 (and ragged / long-row cases): fp32 <= 1e-5 relative."""
+    c = inputs.config1(rows, cols)
+    x = dev(c["x"])
+    y = ops.softmax(x, sync=True)
+    expect = ref.softmax(c["x"])
+    assert rel_err(host(y), expect, 1e-30) <= 1e-5
+    assert np.allclose(host(y).sum(axis=1), 1.0, atol=1e-5)
+    yr, r = ops.rmsnorm(x, dev(c["w"]), c["eps"], sync=True)
+    ey, er = ref.rms_layernorm(c["x"], c["w"], c["eps"])
+    assert rel_err(host(yr), ey, 1e-6) <= 1e-5
+    assert rel_err(host(r), er, 1e-30) <= 1e-5
+
+
+@pytest.mark.parametrize("rows,cols", [(8191, 3000), (64, 3001), (7, 67)])
+def test_layernorm_softmax_bf16_masked_tail(rows, cols):
+    """Config 2: bf16 in/out, fp32 statistics, +-60 outliers; <= 1e-2."""
+    c = inputs.config2(rows, cols)
+    x = dev(c["x"], "bfloat16")
+    y, mean, rstd = ops.layernorm(x, dev(c["gamma"], "bfloat16"), dev(c["beta"], "bfloat16"),
+                                  c["eps"], sync=True)
+    ey, em, es = ref.layernorm(c["x"], c["gamma"], c["beta"], c["eps"])
+    close(host(y), ey, 1e-2, 1e-2)
+    assert rel_err(host(mean), em, 1e-3) <= 1e-5
+    assert rel_err(host(rstd), es, 1e-30) <= 1e-5
+    s = ops.softmax(x, sync=True)
+    close(host(s), ref.softmax(c["x"]), 1e-2, 1e-2)
+    assert np.allclose(host(s).sum(axis=1), 1.0, atol=2e-2)
+
+
+def test_reduction_tail_guard_untouched():
+    """Outputs are written only inside the view: a poisoned guard behind each
+    row stays intact (the masked-tail witness idea of tools/check_masked_tails.py)."""
+    rows, cols, pad = 9, 3000, 8
+    c = inputs.config2(rows, cols)
+    x = dev(c["x"], "bfloat16")
+    buf = torch.full((rows, cols + pad), 7.0, dtype=torch.bfloat16, device=DEV)
+    y = buf[:, :cols]
+    ops.softmax_kernel(x, y, cols, sync=True)
+    assert torch.all(buf[:, cols:] == 7.0)
+    close(host(y), ref.softmax(c["x"]), 1e-2, 1e-2)
+
+
+@pytest.mark.parametrize("case", golden_cases("softmax"))
+def test_softmax_reference_fixture(case):
+    b = load(case)
+    dt = dtype_of(case)
+    x = values(b, "x_ptr")
+    y = torch.zeros(x.shape, dtype=TD[dt], device=DEV)
+    ops.softmax_kernel(dev(x, dt), y, int(b.scalar("n_cols")), sync=True)
+    rtol, atol = ref.TOLERANCES[dt]
+    close(host(y), values(b, "y_ptr"), rtol, atol)
+
+
+def test_rms_fixture_shapes_all_dtypes():
+    """The reference case shapes of fast_rms_layernorm (:48) in 3 dtypes."""
+    for dt in ("float32", "bfloat16", "float16"):
+        for rows, cols in ((4, 64), (7, 67)):
+            rng = np.random.default_rng(30)
+            x = (rng.standard_normal((rows, cols)) * 0.5).astype(np.float32)
+            w = (rng.standard_normal(cols) * 0.5 + 1.0).astype(np.float32)
+            if dt == "bfloat16":
+                x, w = ref.bf16_round(x), ref.bf16_round(w)
+            elif dt == "float16":
+                x, w = x.astype(np.float16).astype(np.float32), w.astype(np.float16).astype(np.float32)
+            yr, r = ops.rmsnorm(dev(x, dt), dev(w, dt), 1e-5, sync=True)
+            ey, er = ref.rms_layernorm(x, w, 1e-5)
+            rtol, atol = ref.TOLERANCES[dt]
+            close(host(yr), ey, rtol, atol)
+            close(host(r), er, 1e-5, 1e-6)
+
+
+# ------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (300, 260, 256), (513, 1000, 1024), (1, 7, 64)])
+def test_gemm_bf16_mfma(m, n, k):
+    c = inputs.config3(m, n, k)
+    y = ops.matmul(dev(c["a"], "bfloat16"), dev(c["bt"], "bfloat16").t(), sync=True)
+    assert rt.module().last_kernel == "g950_gemm_bf16_256x256"
+    close(host(y), ref.matmul(c["a"], c["bt"].T), 2e-2, 2e-2)
+
+
+@pytest.mark.parametrize("m,n,k", [(8192, 8192, 8192), (4097, 11008, 4096)])
+def test_gemm_bf16_config3_sampled(m, n, k):
+    """Config 3 at full size: sampled rows (incl. the ragged last row) and all
+    columns checked against float64."""
+    c = inputs.config3(m, n, k)
+    a = dev(c["a"], "bfloat16")
+    y = ops.matmul(a, dev(c["bt"], "bfloat16").t(), sync=True)
+    rows = np.unique(np.r_[0, 1, 255, 256, m // 2, m - 2, m - 1,
+                           np.random.default_rng(9).integers(0, m, 24)])
+    got = host(y[torch.from_numpy(rows).to(DEV)])
+    close(got, ref.matmul(c["a"][rows], c["bt"].T), 2e-2, 2e-2)
+
+
+def test_gemm_f16_and_general_paths():
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((130, 192)).astype(np.float16).astype(np.float32)
+    b = rng.standard_normal((192, 70)).astype(np.float16).astype(np.float32)
+    expect = ref.matmul(a, b)
+    # K-contiguous B -> MFMA f16 kernel
+    y = ops.matmul(dev(a, "float16"), dev(b.T.copy(), "float16").t(), sync=True)
+    assert rt.module().last_kernel == "g950_gemm_f16_256x256"
+    close(host(y), expect, 1e-2, 1e-2)
+    # row-major B -> general kernel, fp32 output
+    out = torch.empty((130, 70), dtype=torch.float32, device=DEV)
+    ops.matmul_kernel(dev(a, "float16"), dev(b, "float16"), out, 130, 70, 192, sync=True)
+    assert rt.module().last_kernel == "g950_gemm_general"
+    close(host(out), expect, 1e-3, 1e-3)
+
+
+@pytest.mark.parametrize("case", golden_cases("matmul"))
+def test_matmul_reference_fixture(case):
+    b = load(case)
+    dt = dtype_of(case)
+    a, bb = values(b, "a_ptr"), values(b, "b_ptr")
+    m, k = a.shape
+    n = bb.shape[1]
+    rtol, atol = ref.TOLERANCES[dt]
+    # the fixture layout (row-major B) ...
+    y = torch.zeros((m, n), dtype=TD[dt], device=DEV)
+    ops.matmul_kernel(dev(a, dt), dev(bb, dt), y, m, n, k, sync=True)
+    close(host(y), values(b, "y_ptr"), rtol, atol)
+    # ... and the same values column-major, which takes the MFMA kernel when K allows
+    if dt != "float32":
+        y2 = torch.zeros((m, n), dtype=TD[dt], device=DEV)
+        ops.matmul_kernel(dev(a, dt), dev(bb.T.copy(), dt).t(), y2, m, n, k, sync=True)
+        close(host(y2), values(b, "y_ptr"), rtol, atol)
+
+
+# ------------------------------------------------------------------ int8
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (300, 200, 384), (4096, 8192, 8192)])
+def test_int8_gemm_exact_and_dequant(m, n, k):
+    c = inputs.config5(m, n, k)
+    a = torch.from_numpy(c["a"]).to(DEV)
+    bt = torch.from_numpy(c["bt"]).to(DEV)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    ops.matmul_i8_kernel(a, bt.t(), acc, m, n, k, sync=True)
+    assert rt.module().last_kernel == "g950_gemm_i8_256x256"
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    ops.matmul_i8_dequant_kernel(a, bt.t(), torch.from_numpy(c["sa"]).to(DEV),
+                                 torch.from_numpy(c["sb"]).to(DEV), y, m, n, k, sync=True)
+    rows = np.arange(m) if m * n <= 1 << 20 else np.unique(
+        np.r_[0, m - 1, np.random.default_rng(11).integers(0, m, 16)])
+    exact = ref.matmul_i8(c["a"][rows], c["bt"].T)
+    assert np.abs(exact).max() < 2 ** 31
+    got = acc[torch.from_numpy(rows).to(DEV)].cpu().numpy()
+    assert np.array_equal(got, exact)  # bit-exact int32
+    deq = ref.dequant(exact, c["sa"][rows], c["sb"])
+    close(host(y[torch.from_numpy(rows).to(DEV)]), deq, 2e-2, 2e-2)
+
+
+def test_int8_general_path_exact():
+    rng = np.random.default_rng(12)
+    a = rng.integers(-128, 128, (37, 100), dtype=np.int8)   # K not a slab multiple
+    b = rng.integers(-128, 128, (100, 45), dtype=np.int8)   # row-major
+    acc = torch.empty((37, 45), dtype=torch.int32, device=DEV)
+    ops.matmul_i8_kernel(torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV), acc, 37, 45, 100,
+                         sync=True)
+    assert rt.module().last_kernel == "g950_gemm_general_i8"
+    assert np.array_equal(acc.cpu().numpy(), ref.matmul_i8(a, b))
+
+
+# ------------------------------------------------------------- attention
+@pytest.mark.parametrize("z,h,hkv,s,d,causal", [
+    (1, 4, 2, 200, 128, True), (2, 2, 1, 333, 64, True), (1, 2, 2, 130, 128, False),
+    (1, 1, 1, 1, 128, True)])
+def test_attention_small(z, h, hkv, s, d, causal):
+    c = inputs.config4(z, h, hkv, s, d)
+    o, lse = ops.attention(dev(c["q"], "bfloat16"), dev(c["k"], "bfloat16"), dev(c["v"], "bfloat16"),
+                           causal=causal, sync=True)
+    assert rt.module().last_kernel == f"g950_attn_fwd_bf16_d{d}"
+    eo, el = ref.attention(c["q"], c["k"], c["v"], c["scale"], causal=causal)
+    close(host(o), eo, 2e-2, 2e-2)
+    close(lse.cpu().numpy(), el, 1e-4, 1e-4)
+
+
+def test_attention_config4_sampled_heads():
+    """Config 4 at full size; three (batch, head) pairs checked in full."""
+    c = inputs.config4()
+    o, lse = ops.attention(dev(c["q"], "bfloat16"), dev(c["k"], "bfloat16"), dev(c["v"], "bfloat16"),
+                           causal=True, sync=True)
+    for z, h in ((0, 0), (1, 13), (3, 31)):
+        eo, el = ref.attention(c["q"][z:z + 1, h:h + 1], c["k"][z:z + 1, h // 4:h // 4 + 1],
+                               c["v"][z:z + 1, h // 4:h // 4 + 1], c["scale"], causal=True)
+        close(host(o[z, h]), eo[0, 0], 2e-2, 2e-2)
+        close(lse[z, h].cpu().numpy(), el[0, 0], 1e-4, 1e-4)
+    # causal row 0 attends to key 0 only: O = V[0] exactly (up to bf16 rounding)
+    close(host(o[:, :, 0]), np.repeat(c["v"][:, :, 0], 4, axis=1), 0, 1e-6)
+
+
+@pytest.mark.parametrize("case", golden_cases("attention"))
+def test_attention_reference_fixture(case):
+    b = load(case)
+    dt = dtype_of(case)
+    q, k, v = (values(b, n) for n in ("q_ptr", "k_ptr", "v_ptr"))
+    out = torch.zeros(q.shape, dtype=TD[dt], device=DEV)
+    qd, kd, vd = dev(q, dt), dev(k, dt), dev(v, dt)
+    z, h, s, d = q.shape
+    ops.attn_fwd_causal_kernel(qd, kd, vd, out, z, h, s, np.float32(b.scalar("scale")),
+                               *qd.stride(), *kd.stride(), *vd.stride(), *out.stride(),
+                               CAUSAL=False, sync=True)
+    rtol, atol = ref.TOLERANCES[dt]
+    close(host(out), values(b, "out_ptr"), rtol, atol)
+
+
+def test_run_twice_bit_identical():
+    """Determinism (the runtime's repeat self-check, a100c/runtime/main.c:136-151)."""
+    c = inputs.config3(512, 512, 512)
+    a, bt = dev(c["a"], "bfloat16"), dev(c["bt"], "bfloat16").t()
+    y1 = ops.matmul(a, bt, sync=True)
+    y2 = ops.matmul(a, bt, sync=True)
+    assert torch.equal(y1, y2)
+    q = inputs.config4(1, 4, 2, 256, 128)
+    o1, _ = ops.attention(dev(q["q"], "bfloat16"), dev(q["k"], "bfloat16"), dev(q["v"], "bfloat16"), sync=True)
+    o2, _ = ops.attention(dev(q["q"], "bfloat16"), dev(q["k"], "bfloat16"), dev(q["v"], "bfloat16"), sync=True)
+    assert torch.equal(o1, o2)
