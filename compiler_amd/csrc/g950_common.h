@@ -31,13 +31,11 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
 
-// float -> bf16 bits, round-to-nearest-even; NaN keeps its payload with the
-// quiet bit set (the reference host rule).
+// float -> bf16 bits, round-to-nearest-even (gfx950 v_cvt_pk_bf16_f32).  For
+// every non-NaN input this is the reference host rule bit for bit; a NaN stays
+// a quiet NaN.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  uint32_t r = u + 0x7FFFu + ((u >> 16) & 1u);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) r = u | 0x00400000u;
-  return (uint16_t)(r >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t b) {

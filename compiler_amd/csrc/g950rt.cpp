@@ -33,6 +33,7 @@ using namespace g950;
 struct g950_module {
   hipModule_t mod = nullptr;
   int device = -1;
+  int cus = 256;  // compute units of the device (persistent grid sizing)
   std::mutex mu;
   std::unordered_map<std::string, hipFunction_t> fns;
 };
@@ -189,9 +190,27 @@ int launch(g950_module* m, const std::string& name, unsigned grid, unsigned bloc
 bool aligned16(uintptr_t p) { return (p & 15) == 0; }
 
 // ------------------------------------------------------------ row reductions
-struct RowCfg { int items, block; };
-const RowCfg kRowCfgs[] = {{1, 64}, {2, 64}, {4, 64}, {3, 128}, {8, 64}, {4, 128},
-                           {4, 256}, {8, 256}, {16, 256}};
+// Register configurations in order of preference: the first whose
+// items*block vectors cover the row is used.  One wavefront per row while the
+// row fits (no LDS round trip in the reductions), then 4-wave workgroups.
+// `waves` is the resident-wave target per CU that sizes the persistent grid
+// (measured on MI355X: one-row-per-wave shapes do best with many small
+// workgroups, the 16-vector shapes with fewer, longer-lived ones).
+struct RowCfg { int items, block, waves; };
+const RowCfg kRowCfgs[] = {{1, 64, 32}, {2, 64, 32}, {4, 64, 32}, {6, 64, 32}, {8, 64, 32},
+                           {16, 64, 8}, {8, 256, 16}, {16, 256, 8}};
+
+// Persistent grid for `rows` rows of BLOCK-thread workgroups: at most
+// `waves` resident waves per CU, balanced so every workgroup gets
+// ceil(rows / grid) or one fewer rows.
+unsigned row_grid(const g950_module* m, long long rows, int block, int waves) {
+  const long long cus = m ? m->cus : 256;
+  const long long per_cu = waves / (block / 64) > 0 ? waves / (block / 64) : 1;
+  const long long cap = cus * per_cu;
+  if (rows <= cap) return (unsigned)rows;
+  const long long k = (rows + cap - 1) / cap;
+  return (unsigned)((rows + k - 1) / k);
+}
 
 const char* rr_dtype(uint32_t dt) {
   return dt == G950_DTYPE_FLOAT32 ? "f32" : dt == G950_DTYPE_BFLOAT16 ? "bf16" : "f16";
@@ -216,7 +235,8 @@ int launch_rows(g950_module* m, const char* op, RowArgs& a, uint32_t dt, const V
   if (pick) {
     snprintf(name, sizeof name, "g950_rr_%s_%s_v%d_i%d_b%d", op, rr_dtype(dt), v, pick->items,
              pick->block);
-    return launch(m, name, (unsigned)a.rows, (unsigned)pick->block, a, stream);
+    return launch(m, name, row_grid(m, a.rows, pick->block, pick->waves), (unsigned)pick->block, a,
+                  stream);
   }
   snprintf(name, sizeof name, "g950_rr_loop_%s_%s", op, rr_dtype(dt));
   return launch(m, name, (unsigned)a.rows, 256u, a, stream);
@@ -545,6 +565,7 @@ int g950_open(const char* path, g950_module** out) {
   auto* m = new (std::nothrow) g950_module();
   if (!m) return fail(G950_RESOURCE, "g950_open: out of host memory");
   hipError_t e = hipGetDevice(&m->device);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&m->cus, hipDeviceAttributeMultiprocessorCount, m->device);
   if (e == hipSuccess) e = hipModuleLoad(&m->mod, path);
   if (e != hipSuccess) {
     delete m;

@@ -11,11 +11,15 @@
 // All arithmetic is fp32; 16-bit inputs widen exactly and outputs round once.
 //
 // Two kernel shapes:
-//   rr_regs  -- the row lives in registers.  One workgroup (BLOCK threads) per
-//               row; each thread owns ITEMS vectors of VEC elements
-//               (VEC*sizeof(T) = 16 B => one 128-bit load each).  The tail of a
-//               non-power-of-two row is a per-vector predicate; x is read from
-//               HBM exactly once and y written once.
+//   rr_regs  -- the row lives in registers.  Each thread owns ITEMS vectors of
+//               VEC elements (VEC*sizeof(T) = 16 B => one 128-bit nontemporal
+//               load each) of a row handled by one BLOCK-thread workgroup.
+//               Workgroups are persistent: the launcher sizes the grid to the
+//               resident capacity (balanced so every workgroup gets the same
+//               number of rows), each workgroup walks rows g, g+G, ..., and the
+//               next row's loads are in flight while the current row is
+//               reduced.  The tail of a non-power-of-two row is a per-vector
+//               predicate; x is read from HBM once and y written once.
 //   rr_loop  -- rows longer than the register budget: scalar strided passes
 //               (softmax: online max/sum then output; norms: statistics then
 //               output), reading x two (three for LayerNorm) times.
@@ -114,112 +118,228 @@ __device__ __forceinline__ void load_param(const void* base, long long idx, floa
   }
 }
 
+// Raw (undecoded) row vectors: what one 16-byte (or scalar) load returns.
+template <typename T, int VEC> struct RawIO;
+template <> struct RawIO<float, 4> {
+  using type = f32x4;
+  static __device__ __forceinline__ type load(const void* base, long long idx) {
+    return __builtin_nontemporal_load((const f32x4*)((const float*)base + idx));
+  }
+  static __device__ __forceinline__ type load_cached(const void* base, long long idx) {
+    return *(const f32x4*)((const float*)base + idx);
+  }
+  static __device__ __forceinline__ void unpack(const type& r, float* out) {
+    out[0] = r[0]; out[1] = r[1]; out[2] = r[2]; out[3] = r[3];
+  }
+};
+template <> struct RawIO<float, 1> {
+  using type = float;
+  static __device__ __forceinline__ type load(const void* base, long long idx) {
+    return ((const float*)base)[idx];
+  }
+  static __device__ __forceinline__ type load_cached(const void* base, long long idx) {
+    return ((const float*)base)[idx];
+  }
+  static __device__ __forceinline__ void unpack(const type& r, float* out) { out[0] = r; }
+};
+template <typename T> struct RawIO16 {
+  using type = u32x4;
+  static __device__ __forceinline__ type load(const void* base, long long idx) {
+    return __builtin_nontemporal_load((const u32x4*)((const uint16_t*)base + idx));
+  }
+  static __device__ __forceinline__ type load_cached(const void* base, long long idx) {
+    return *(const u32x4*)((const uint16_t*)base + idx);
+  }
+  static __device__ __forceinline__ void unpack(const type& r, float* out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = Elem<T>::to_f32((uint16_t)(r[i] & 0xFFFFu));
+      out[2 * i + 1] = Elem<T>::to_f32((uint16_t)(r[i] >> 16));
+    }
+  }
+};
+template <typename T> struct RawIO16s {
+  using type = uint16_t;
+  static __device__ __forceinline__ type load(const void* base, long long idx) {
+    return ((const uint16_t*)base)[idx];
+  }
+  static __device__ __forceinline__ type load_cached(const void* base, long long idx) {
+    return ((const uint16_t*)base)[idx];
+  }
+  static __device__ __forceinline__ void unpack(const type& r, float* out) { out[0] = Elem<T>::to_f32(r); }
+};
+template <> struct RawIO<bf16_t, 8> : RawIO16<bf16_t> {};
+template <> struct RawIO<f16_t, 8> : RawIO16<f16_t> {};
+template <> struct RawIO<bf16_t, 1> : RawIO16s<bf16_t> {};
+template <> struct RawIO<f16_t, 1> : RawIO16s<f16_t> {};
+
+// e^x.  fp32 rows keep libm expf (about 1 ulp); 16-bit rows,
+// whose results are rounded to 8 or 11 mantissa bits, use v_exp_f32 on
+// x*log2(e) (relative error ~1e-6 for |x| < 20, far inside one bf16/fp16 ulp).
+template <typename T>
+__device__ __forceinline__ float row_exp(float x) {
+  if constexpr (sizeof(T) == 4) return expf(x);
+  else return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+// Persistent register-resident row kernel.  Workgroup g handles rows
+// g, g + G, g + 2G, ... (the reference's persistent form
+// tl.range(pid, n_rows, num_progs), ops/suite/dev/layer_norm_forward_row.py);
+// the next row's loads are issued before the current row is reduced, and the
+// per-column parameters (weight, bias) are loaded once per workgroup.
 template <int OP, typename T, int VEC, int ITEMS, int BLOCK>
 __device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
+  using IO = RawIO<T, VEC>;
+  using R = typename IO::type;
   __shared__ float scratch[BLOCK / 64 > 0 ? BLOCK / 64 : 1];
-  const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int nvec = a.cols / VEC;  // host guarantees cols % VEC == 0
-  const void* xrow = (const char*)a.x + (long long)row * a.x_row * (long long)sizeof(T);
-  void* yrow = (char*)a.y + (long long)row * a.y_row * (long long)sizeof(T);
+  const long long xstride = a.x_row * (long long)sizeof(T);
+  const long long ystride = a.y_row * (long long)sizeof(T);
 
-  float v[ITEMS][VEC];
+  // parameters stay packed in registers (16-bit types: half the VGPRs)
+  R wr[ITEMS], br[ITEMS];
+  if constexpr (OP != ROW_SOFTMAX) {
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    const int j = tid + i * BLOCK;
-    if (j < nvec) {
-      load_vec<T, VEC>(xrow, (long long)j * VEC, v[i]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) v[i][e] = (OP == ROW_SOFTMAX) ? -__builtin_huge_valf() : 0.0f;
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = tid + i * BLOCK;
+      if (j < nvec) {
+        wr[i] = IO::load_cached(a.w, (long long)j * VEC);
+        if constexpr (OP == ROW_LAYERNORM) br[i] = IO::load_cached(a.b, (long long)j * VEC);
+      }
     }
   }
 
-  if constexpr (OP == ROW_SOFTMAX) {
-    float m = -__builtin_huge_valf();
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) m = fmaxf(m, v[i][e]);
-    m = block_reduce<OpMax, BLOCK>(m, scratch);
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        v[i][e] = expf(v[i][e] - m);  // masked lanes: exp(-inf) = 0
-        s += v[i][e];
-      }
-    s = block_reduce<OpSum, BLOCK>(s, scratch);
-    const float inv = 1.0f / s;
+  R cur[ITEMS], nxt[ITEMS];
+  int row = blockIdx.x;
+  {
+    const char* xrow = (const char*)a.x + (long long)row * xstride;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
       const int j = tid + i * BLOCK;
-      if (j < nvec) {
-        float o[VEC];
+      if (j < nvec) cur[i] = IO::load(xrow, (long long)j * VEC);
+    }
+  }
+  for (; row < a.rows; row += gridDim.x) {
+    const int nrow = row + gridDim.x;
+    if (nrow < a.rows) {
+      const char* xrow = (const char*)a.x + (long long)nrow * xstride;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * inv;
-        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+      for (int i = 0; i < ITEMS; ++i) {
+        const int j = tid + i * BLOCK;
+        if (j < nvec) nxt[i] = IO::load(xrow, (long long)j * VEC);
       }
     }
-  } else if constexpr (OP == ROW_RMSNORM) {
-    float ss = 0.0f;
+    if constexpr (OP != ROW_SOFTMAX) {
+      // keep the decode of the packed parameters inside the loop: hoisting it
+      // would hold them as fp32 for the whole kernel (twice the VGPRs)
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) ss = fmaf(v[i][e], v[i][e], ss);
-    ss = block_reduce<OpSum, BLOCK>(ss, scratch);
-    const float inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
-    if (tid == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, inv);
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      const int j = tid + i * BLOCK;
-      if (j < nvec) {
-        float w[VEC], o[VEC];
-        load_param<T, VEC>(a.w, (long long)j * VEC, w);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] * inv) * w[e];
-        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+      for (int i = 0; i < ITEMS; ++i) {
+        asm volatile("" : "+v"(wr[i]));
+        if constexpr (OP == ROW_LAYERNORM) asm volatile("" : "+v"(br[i]));
       }
     }
-  } else {  // LayerNorm, centered two-pass from registers
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) s += v[i][e];
-    s = block_reduce<OpSum, BLOCK>(s, scratch);
-    const float mean = s / (float)a.cols;
-    float q = 0.0f;
+    void* yrow = (char*)a.y + (long long)row * ystride;
+    float v[ITEMS][VEC];
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
       const int j = tid + i * BLOCK;
       if (j < nvec) {
+        IO::unpack(cur[i], v[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[i][e] = (OP == ROW_SOFTMAX) ? -__builtin_huge_valf() : 0.0f;
+      }
+    }
+
+    if constexpr (OP == ROW_SOFTMAX) {
+      float m = -__builtin_huge_valf();
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) m = fmaxf(m, v[i][e]);
+      m = block_reduce<OpMax, BLOCK>(m, scratch);
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          v[i][e] -= mean;
-          q = fmaf(v[i][e], v[i][e], q);
+          v[i][e] = row_exp<T>(v[i][e] - m);  // masked lanes: exp(-inf) = 0
+          s += v[i][e];
+        }
+      s = block_reduce<OpSum, BLOCK>(s, scratch);
+      const float inv = 1.0f / s;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        const int j = tid + i * BLOCK;
+        if (j < nvec) {
+          float o[VEC];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * inv;
+          store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+        }
+      }
+    } else if constexpr (OP == ROW_RMSNORM) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) ss = fmaf(v[i][e], v[i][e], ss);
+      ss = block_reduce<OpSum, BLOCK>(ss, scratch);
+      const float inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+      if (tid == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, inv);
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        const int j = tid + i * BLOCK;
+        if (j < nvec) {
+          float o[VEC], w[VEC];
+          IO::unpack(wr[i], w);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] * inv) * w[e];
+          store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+        }
+      }
+    } else {  // LayerNorm, centered two-pass from registers
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s += v[i][e];
+      s = block_reduce<OpSum, BLOCK>(s, scratch);
+      const float mean = s / (float)a.cols;
+      float q = 0.0f;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        const int j = tid + i * BLOCK;
+        if (j < nvec) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            v[i][e] -= mean;
+            q = fmaf(v[i][e], v[i][e], q);
+          }
+        }
+      }
+      q = block_reduce<OpSum, BLOCK>(q, scratch);
+      const float rstd = 1.0f / sqrtf(q / (float)a.cols + a.eps);
+      if (tid == 0) {
+        store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mean);
+        store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, rstd);
+      }
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        const int j = tid + i * BLOCK;
+        if (j < nvec) {
+          float o[VEC], w[VEC], bb[VEC];
+          IO::unpack(wr[i], w);
+          IO::unpack(br[i], bb);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * rstd * w[e] + bb[e];
+          store_vec<T, VEC>(yrow, (long long)j * VEC, o);
         }
       }
     }
-    q = block_reduce<OpSum, BLOCK>(q, scratch);
-    const float rstd = 1.0f / sqrtf(q / (float)a.cols + a.eps);
-    if (tid == 0) {
-      store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mean);
-      store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, rstd);
-    }
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      const int j = tid + i * BLOCK;
-      if (j < nvec) {
-        float w[VEC], bb[VEC], o[VEC];
-        load_param<T, VEC>(a.w, (long long)j * VEC, w);
-        load_param<T, VEC>(a.b, (long long)j * VEC, bb);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * rstd * w[e] + bb[e];
-        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
-      }
-    }
+    for (int i = 0; i < ITEMS; ++i) cur[i] = nxt[i];
   }
 }
 
@@ -322,10 +442,9 @@ __device__ __forceinline__ void rr_loop_body(const RowArgs& a) {
   G950_RR_REGS(OPNAME, OP, TNAME, T, V, 1, 64)          \
   G950_RR_REGS(OPNAME, OP, TNAME, T, V, 2, 64)          \
   G950_RR_REGS(OPNAME, OP, TNAME, T, V, 4, 64)          \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 6, 64)          \
   G950_RR_REGS(OPNAME, OP, TNAME, T, V, 8, 64)          \
-  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 3, 128)         \
-  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 4, 128)         \
-  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 4, 256)         \
+  G950_RR_REGS(OPNAME, OP, TNAME, T, V, 16, 64)         \
   G950_RR_REGS(OPNAME, OP, TNAME, T, V, 8, 256)         \
   G950_RR_REGS(OPNAME, OP, TNAME, T, V, 16, 256)
 

@@ -1,0 +1,167 @@
+"""A harness ``Device`` for the gfx950 hot path.
+
+It implements the reference harness's Device protocol
+(ops/harness/opslib/device.py:79-118: alloc / upload / download / pointer /
+synchronize / compare / launch) so the reference's own case loop
+(``stage_case`` -> ``StagedCase.launch`` -> ``Device.launch``, device.py:323-415)
+can drive these kernels unchanged.  ``launch`` receives the reference kernel
+object (or any callable with the same parameter names), binds the positional
+arguments by that signature exactly as ``bind_arguments`` produced them
+(device.py:232-260), and dispatches by the kernel's NAME to the matching
+operator of ``compiler_amd.operators``.  Kernels outside the hot path are
+refused with ``NotImplementedError`` -- there is no fallback.
+
+bf16 follows the harness's pointer duality (ops/harness/compiler_api/
+AGENT_GUIDE.md:253): a float32 host array is rounded to bf16 on upload, a
+uint16 host array is taken as raw bf16 bits; bf16 buffers download as float32
+values.  Launches are synchronous, as the contract requires
+(ops/harness/compiler_api/COMPILE_CONTRACT.md:73-74).
+"""
+from __future__ import annotations
+
+import inspect
+
+import numpy as np
+
+from . import operators as ops
+
+_NP_TO_TORCH = {"float32": "float32", "float16": "float16", "bfloat16": "bfloat16",
+                "int8": "int8", "uint8": "uint8", "int16": "int16", "int32": "int32",
+                "int64": "int64", "float64": "float64", "bool": "bool"}
+
+
+class G950Buffer:
+    """A device buffer: a torch-ROCm tensor plus its logical dtype name."""
+
+    def __init__(self, tensor, dtype_name: str):
+        self.tensor = tensor
+        self._dtype = dtype_name
+
+    def data_ptr(self):
+        return self.tensor.data_ptr()
+
+    @property
+    def dtype(self):
+        return self._dtype
+
+    @property
+    def shape(self):
+        return tuple(self.tensor.shape)
+
+
+def _kernel_name(kernel) -> str:
+    target = kernel
+    for attr in ("fn", "fn"):  # autotuner -> JITFunction -> python function
+        target = getattr(target, attr, target)
+    return getattr(target, "__name__", str(kernel))
+
+
+def _kernel_params(kernel):
+    target = kernel
+    for attr in ("fn", "fn"):
+        target = getattr(target, attr, target)
+    return list(inspect.signature(target).parameters)
+
+
+def _softmax(a):
+    ops.softmax_kernel(a["x_ptr"], a["y_ptr"], a["n_cols"], sync=True)
+
+
+def _rms(a):
+    ops.rms_layernorm_forward_kernel(a["Y"], a["Y_row_stride"], a["X"], a["X_row_stride"], a["W"],
+                                     a["W_row_stride"], a["r"], a["r_row_stride"], a["n_cols"],
+                                     a["eps"], sync=True)
+
+
+def _layernorm(a):
+    ops.layernorm_kernel(a["X"], a["Y"], a["W"], a["B"], a["Mean"], a["Rstd"], a["stride"], a["N"],
+                         a["eps"], sync=True)
+
+
+def _matmul(a):
+    ops.matmul_kernel(a["a_ptr"], a["b_ptr"], a["y_ptr"], a["M"], a["N"], a["K"], sync=True)
+
+
+def _attention(a, causal_default):
+    names = ["stride_qz", "stride_qh", "stride_qm", "stride_qk", "stride_kz", "stride_kh",
+             "stride_kn", "stride_kk", "stride_vz", "stride_vh", "stride_vk", "stride_vn",
+             "stride_oz", "stride_oh", "stride_om", "stride_on"]
+    ops.attn_fwd_causal_kernel(a["q_ptr"], a["k_ptr"], a["v_ptr"], a["out_ptr"], a["Z"], a["H"],
+                               a["N_CTX"], a["scale"], *[a[n] for n in names],
+                               CAUSAL=bool(a.get("CAUSAL", causal_default)), sync=True)
+
+
+# reference kernel name -> operator (hot path only)
+KERNELS = {
+    "softmax_kernel": _softmax,
+    "rms_layernorm_forward_kernel": _rms,
+    "layernorm_kernel": _layernorm,
+    "matmul_kernel": _matmul,
+    "attn_fwd_causal_kernel": lambda a: _attention(a, True),
+    "attention_forward_kernel": lambda a: _attention(a, False),
+}
+
+
+class G950Device:
+    """Device protocol implementation over torch-ROCm memory and the g950 C ABI."""
+
+    name = "g950"
+
+    def __init__(self, device: str = "cuda:0"):
+        import torch
+        if not torch.cuda.is_available():
+            raise RuntimeError("G950Device needs an MI355X (gfx950) GPU")
+        self.torch = torch
+        self.device = torch.device(device)
+
+    # -- memory -----------------------------------------------------------
+    def _tdtype(self, name):
+        return getattr(self.torch, _NP_TO_TORCH[name])
+
+    def alloc(self, shape, dtype):
+        name = np.dtype(dtype).name if dtype != "bfloat16" else "bfloat16"
+        return G950Buffer(self.torch.zeros(tuple(shape), dtype=self._tdtype(name), device=self.device), name)
+
+    def upload(self, array, dtype=None):
+        array = np.ascontiguousarray(array)
+        target = dtype if dtype is not None else array.dtype.name
+        if target == "bfloat16":
+            if array.dtype == np.uint16:
+                t = self.torch.from_numpy(array.view(np.int16)).to(self.device).view(self.torch.bfloat16)
+            else:
+                t = self.torch.from_numpy(array.astype(np.float32)).to(self.device).to(self.torch.bfloat16)
+            return G950Buffer(t, "bfloat16")
+        t = self.torch.from_numpy(array.astype(target, copy=False)).to(self.device)
+        return G950Buffer(t, target)
+
+    def download(self, buffer):
+        t = buffer.tensor
+        if buffer.dtype == "bfloat16":
+            return t.float().cpu().numpy()
+        return t.cpu().numpy()
+
+    def pointer(self, buffer):
+        return buffer.data_ptr()
+
+    def synchronize(self):
+        self.torch.cuda.synchronize(self.device)
+
+    def compare(self, buffer, expected, policy):
+        return None  # host comparison by the harness
+
+    def properties(self):
+        p = self.torch.cuda.get_device_properties(self.device)
+        return {"name": p.name, "gcn_arch": getattr(p, "gcnArchName", ""),
+                "multiprocessors": p.multi_processor_count, "total_memory": p.total_memory}
+
+    # -- launch -----------------------------------------------------------
+    def launch(self, kernel, grid, positional, keywords):
+        name = _kernel_name(kernel)
+        if name not in KERNELS:
+            raise NotImplementedError(f"{name} is not a g950 hot-path operator")
+        params = _kernel_params(kernel)
+        values = dict(zip(params, positional))
+        values.update(keywords or {})
+        args = {k: (v.tensor if isinstance(v, G950Buffer) else v) for k, v in values.items()}
+        with self.torch.cuda.device(self.device):
+            KERNELS[name](args)

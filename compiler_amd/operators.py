@@ -20,60 +20,63 @@ import numpy as np
 from . import runtime as rt
 
 
-def _launch(op, named_tensors: dict, outputs: set, named_scalars: dict, stream=None, sync=False):
+def _launch(op, named_tensors: dict, outputs: set, named_scalars: dict, stream=None, sync=False,
+            prepare=False):
     names = sorted(named_tensors)
     tensors = [named_tensors[n] for n in names]
     outs = [n in outputs for n in names]
     scalars = [named_scalars[n] if isinstance(named_scalars[n], rt.Scalar) else rt.scalar(named_scalars[n])
                for n in sorted(named_scalars)]
+    if prepare:
+        return rt.module().prepare(op, tensors, outs, scalars, stream=stream)
     return rt.module().launch(op, tensors, outs, scalars, stream=stream, sync=sync)
 
 
-def softmax_kernel(x_ptr, y_ptr, n_cols, *, stream=None, sync=False):
+def softmax_kernel(x_ptr, y_ptr, n_cols, *, stream=None, sync=False, prepare=False):
     """Row softmax (ops/suite/perf/softmax.py:21-32).  x/y: [rows, n_cols]."""
     return _launch(rt.OP_SOFTMAX, {"x_ptr": x_ptr, "y_ptr": y_ptr}, {"y_ptr"},
-                   {"n_cols": n_cols}, stream, sync)
+                   {"n_cols": n_cols}, stream, sync, prepare)
 
 
 def rms_layernorm_forward_kernel(Y, Y_row_stride, X, X_row_stride, W, W_row_stride, r,
-                                 r_row_stride, n_cols, eps, *, stream=None, sync=False):
+                                 r_row_stride, n_cols, eps, *, stream=None, sync=False, prepare=False):
     """RMSNorm forward (ops/suite/perf/fast_rms_layernorm.py:20-42)."""
     return _launch(rt.OP_RMS_LAYERNORM, {"Y": Y, "X": X, "W": W, "r": r}, {"Y", "r"},
                    {"Y_row_stride": Y_row_stride, "X_row_stride": X_row_stride,
                     "W_row_stride": W_row_stride, "r_row_stride": r_row_stride,
-                    "n_cols": n_cols, "eps": np.float32(eps)}, stream, sync)
+                    "n_cols": n_cols, "eps": np.float32(eps)}, stream, sync, prepare)
 
 
-def layernorm_kernel(X, Y, W, B, Mean, Rstd, stride, N, eps, *, stream=None, sync=False):
+def layernorm_kernel(X, Y, W, B, Mean, Rstd, stride, N, eps, *, stream=None, sync=False, prepare=False):
     """LayerNorm forward with Mean/Rstd outputs
     (ops/suite/dev/fused_layernorm_triton.py:27-42)."""
     return _launch(rt.OP_LAYERNORM, {"X": X, "Y": Y, "W": W, "B": B, "Mean": Mean, "Rstd": Rstd},
                    {"Y", "Mean", "Rstd"}, {"stride": stride, "N": N, "eps": np.float32(eps)},
-                   stream, sync)
+                   stream, sync, prepare)
 
 
-def matmul_kernel(a_ptr, b_ptr, y_ptr, M, N, K, *, stream=None, sync=False):
+def matmul_kernel(a_ptr, b_ptr, y_ptr, M, N, K, *, stream=None, sync=False, prepare=False):
     """Y = A.B with fp32 accumulation (ops/suite/perf/matmul.py:21-37).
     ``b_ptr`` is the logical [K, N] operand; a column-major (K-contiguous) b,
     e.g. ``bt.t()`` of a row-major [N, K] tensor, takes the MFMA path."""
     return _launch(rt.OP_MATMUL, {"a_ptr": a_ptr, "b_ptr": b_ptr, "y_ptr": y_ptr}, {"y_ptr"},
-                   {"M": M, "N": N, "K": K}, stream, sync)
+                   {"M": M, "N": N, "K": K}, stream, sync, prepare)
 
 
-def matmul_i8_kernel(a_ptr, b_ptr, c_ptr, M, N, K, *, stream=None, sync=False):
+def matmul_i8_kernel(a_ptr, b_ptr, c_ptr, M, N, K, *, stream=None, sync=False, prepare=False):
     """int8 x int8 -> int32, bit-exact modular accumulation
     (i8 dot family, a100c/plan/tiles.py:118-131)."""
     return _launch(rt.OP_MATMUL_I8, {"a_ptr": a_ptr, "b_ptr": b_ptr, "c_ptr": c_ptr}, {"c_ptr"},
-                   {"M": M, "N": N, "K": K}, stream, sync)
+                   {"M": M, "N": N, "K": K}, stream, sync, prepare)
 
 
 def matmul_i8_dequant_kernel(a_ptr, b_ptr, sa_ptr, sb_ptr, y_ptr, M, N, K, *, stream=None,
-                             sync=False):
+                             sync=False, prepare=False):
     """int8 GEMM + dequant epilogue: y = bf16(acc * sa[m] * sb[n])
     (per-column rule of ops/suite/perf/dequantize_matmul.py:29-38)."""
     return _launch(rt.OP_MATMUL_I8_DEQUANT,
                    {"a_ptr": a_ptr, "b_ptr": b_ptr, "sa_ptr": sa_ptr, "sb_ptr": sb_ptr,
-                    "y_ptr": y_ptr}, {"y_ptr"}, {"M": M, "N": N, "K": K}, stream, sync)
+                    "y_ptr": y_ptr}, {"y_ptr"}, {"M": M, "N": N, "K": K}, stream, sync, prepare)
 
 
 def attn_fwd_causal_kernel(q_ptr, k_ptr, v_ptr, out_ptr, Z, H, N_CTX, scale,
@@ -81,7 +84,8 @@ def attn_fwd_causal_kernel(q_ptr, k_ptr, v_ptr, out_ptr, Z, H, N_CTX, scale,
                            stride_kz, stride_kh, stride_kn, stride_kk,
                            stride_vz, stride_vh, stride_vk, stride_vn,
                            stride_oz, stride_oh, stride_om, stride_on,
-                           *, CAUSAL=True, lse_ptr=None, stream=None, sync=False):
+                           *, CAUSAL=True, lse_ptr=None, stream=None, sync=False,
+                           prepare=False):
     """Attention forward (ops/suite/perf/attn_fwd_causal.py:20-55), with GQA
     when k/v carry fewer heads (ops/suite/dev/gqa.py:29) and the optional
     per-row logsumexp (ops/suite/dev/flash_varlen_fwd_kernel.py:309,318-320)."""
@@ -100,7 +104,7 @@ def attn_fwd_causal_kernel(q_ptr, k_ptr, v_ptr, out_ptr, Z, H, N_CTX, scale,
                "stride_vh": stride_vh, "stride_vk": stride_vk, "stride_vn": stride_vn,
                "stride_oz": stride_oz, "stride_oh": stride_oh, "stride_om": stride_om,
                "stride_on": stride_on}
-    return _launch(op, tensors, outputs, scalars, stream, sync)
+    return _launch(op, tensors, outputs, scalars, stream, sync, prepare)
 
 
 # ------------------------------------------------------ tensor conveniences

@@ -190,6 +190,11 @@ class Module:
                 raise G950Error(rc, self._lib.g950_last_error().decode())
         return self.last_kernel
 
+    def prepare(self, op: int, tensors, outputs, scalars, stream=None):
+        """Pack the call once; the returned object re-launches it with one C
+        call (the launcher still validates every launch)."""
+        return Prepared(self, op, tensors, outputs, scalars, stream)
+
     def close(self):
         if getattr(self, "_handle", None):
             self._lib.g950_close(self._handle)
@@ -208,3 +213,31 @@ def module() -> Module:
         mod = Module()
         _modules[dev] = mod
     return mod
+
+
+class Prepared:
+    """A packed operator call: views, scalars and stream built once."""
+
+    def __init__(self, module: Module, op, tensors, outputs, scalars, stream=None):
+        import torch
+        self._module = module
+        self._tensors = list(tensors)  # keep the storages alive
+        self._views = _ViewArray(self._tensors, outputs)
+        self._n = len(self._tensors)
+        self._scalars = (Scalar * max(len(scalars), 1))(*scalars)
+        self._ns = len(scalars)
+        self._op = op
+        if stream is None:
+            stream = torch.cuda.current_stream(module.device)
+        self._stream = ctypes.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else stream)
+        self.kernel = ""
+
+    def __call__(self):
+        lib = self._module._lib
+        rc = lib.g950_launch(self._module._handle, self._op, self._views.views, self._n,
+                             self._scalars, self._ns, self._stream)
+        if rc != OK:
+            raise G950Error(rc, lib.g950_last_error().decode())
+        if not self.kernel:
+            self.kernel = lib.g950_last_kernel().decode()
+            self._module.last_kernel = self.kernel

@@ -96,8 +96,8 @@ def softmax_args(rows, cols, dtype):
 
 
 @pytest.mark.parametrize("rows,cols,dtype,kernel", [
-    (4096, 4096, rt.DT_F32, "g950_rr_softmax_f32_v4_i4_b256"),
-    (8191, 3000, rt.DT_BF16, "g950_rr_softmax_bf16_v8_i3_b128"),
+    (4096, 4096, rt.DT_F32, "g950_rr_softmax_f32_v4_i16_b64"),
+    (8191, 3000, rt.DT_BF16, "g950_rr_softmax_bf16_v8_i6_b64"),
     (4, 97, rt.DT_F32, "g950_rr_softmax_f32_v1_i2_b64"),
     (4, 16, rt.DT_F16, "g950_rr_softmax_f16_v8_i1_b64"),
     (2, 100000, rt.DT_F32, "g950_rr_loop_softmax_f32"),
@@ -135,7 +135,7 @@ def test_rms_and_layernorm_contracts():
     scal = [1, 3000, 3000, np.float32(1e-6), 3000, 1]
     rc, name, err = validate(rt.OP_RMS_LAYERNORM, a, scal)
     assert rc == 0, err
-    assert name == "g950_rr_rmsnorm_bf16_v8_i3_b128"
+    assert name == "g950_rr_rmsnorm_bf16_v8_i6_b64"
     bad = [1, 2999, 3000, np.float32(1e-6), 3000, 1]
     assert validate(rt.OP_RMS_LAYERNORM, a, bad)[0] == rt.USAGE
     ln = (Args().view([3000], rt.DT_BF16).view([8191], rt.DT_F32, output=True)
@@ -143,7 +143,7 @@ def test_rms_and_layernorm_contracts():
           .view([8191, 3000], rt.DT_BF16).view([8191, 3000], rt.DT_BF16, output=True))
     rc, name, err = validate(rt.OP_LAYERNORM, ln, [3000, np.float32(1e-5), 3000])
     assert rc == 0, err
-    assert name == "g950_rr_layernorm_bf16_v8_i3_b128"
+    assert name == "g950_rr_layernorm_bf16_v8_i6_b64"
     assert validate(rt.OP_LAYERNORM, ln, [3000, np.float32(1e-5), 3001])[0] == rt.USAGE
 
 

@@ -66,7 +66,10 @@ def test_layernorm_softmax_bf16_masked_tail(rows, cols):
                                   c["eps"], sync=True)
     ey, em, es = ref.layernorm(c["x"], c["gamma"], c["beta"], c["eps"])
     close(host(y), ey, 1e-2, 1e-2)
-    assert rel_err(host(mean), em, 1e-3) <= 1e-5
+    # fp32 statistics: rstd to 1e-5 relative; the mean of +-60-outlier rows
+    # cancels to ~0.05, so it is held to 1e-5 relative or 1e-6 absolute
+    # (2e-8 of the rows' mean |x|)
+    close(host(mean), em, 1e-5, 1e-6)
     assert rel_err(host(rstd), es, 1e-30) <= 1e-5
     s = ops.softmax(x, sync=True)
     close(host(s), ref.softmax(c["x"]), 1e-2, 1e-2)
