@@ -540,12 +540,13 @@ int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const 
                     v.stride[2] % 8 == 0 && o.stride[0] % 4 == 0 && o.stride[1] % 4 == 0 &&
                     o.stride[2] % 4 == 0;
   if (mfma) {
-    a.nqb = (int)((S + 127) / 128);
+    // 8 waves x 32 queries per workgroup (attention.hip instantiations)
+    a.nqb = (int)((S + 255) / 256);
     const long long grid = (long long)a.nqb * Z * H;
     if (grid > 0x7FFFFFFF) return fail(G950_USAGE, "attention: grid too large");
     char name[64];
     snprintf(name, sizeof name, "g950_attn_fwd_%s_d%lld", dt == G950_DTYPE_BFLOAT16 ? "bf16" : "f16", D);
-    return launch(m, name, (unsigned)grid, 256u, a, stream);
+    return launch(m, name, (unsigned)grid, 512u, a, stream);
   }
   AttnGenArgs ga{};
   ga.a = a;

@@ -10,7 +10,7 @@
 //
 // Fast kernel (g950_gemm_*_256x256): both operands K-contiguous (A row-major
 // [M,K]; B stored as Bt[N,K], i.e. column-major [K,N]).
-//   * workgroup tile 256x256, 8 waves (2 x 4), wave tile 128 x 64
+//   * workgroup tile 256x256, 8 waves (4 x 2), wave tile 64 x 128
 //   * K slab of 128 bytes per row (64 bf16 / 128 int8) per stage, two LDS
 //     stages (2 x 64 KiB), filled by direct global->LDS 16-byte DMA loads
 //     (global_load_lds_dwordx4), so the next slab streams in while MFMAs run
@@ -40,7 +40,6 @@ enum GemmMode : int { GEMM_BF16 = 0, GEMM_F16 = 1, GEMM_I8 = 2 };
 
 
 constexpr int BM = 256, BN = 256, SLAB = 128;  // SLAB: bytes of K per row per stage
-constexpr int GEMM_THREADS = 512;
 constexpr int STAGE_BYTES = (BM + BN) * SLAB;    // 64 KiB
 
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
@@ -75,13 +74,39 @@ __device__ __forceinline__ void dma_rows(const char* gbase, long long ld_bytes, 
 }
 
 template <int MODE>
+__device__ __forceinline__ void mfma_step(const u32x4& bfrag, const u32x4& afrag, f32x16& accf,
+                                          i32x16& acci) {
+  if constexpr (MODE == GEMM_BF16) {
+    accf = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, bfrag),
+                                                   __builtin_bit_cast(bf16x8, afrag), accf, 0, 0, 0);
+  } else if constexpr (MODE == GEMM_F16) {
+    accf = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bfrag),
+                                                  __builtin_bit_cast(f16x8, afrag), accf, 0, 0, 0);
+  } else {
+    acci = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bfrag),
+                                                 __builtin_bit_cast(i32x4, afrag), acci, 0, 0, 0);
+  }
+}
+
+// WM x WN waves; wave tile (BM/WM) x (BN/WN) = FM x FN fragments of 32x32.
+// SCHED selects the in-slab instruction schedule:
+//   0  read a k-step's fragments, then its MFMAs
+//   1  fragments of k-step ks+1 read (second register set) before the MFMAs of ks
+//   2  as 1, with the LDS reads interleaved one-by-one between the MFMAs
+//   3  as 2, with the wave's issue priority raised while its MFMAs issue
+//   4  as 0, with the priority raise
+template <int MODE, int WM, int WN, int SCHED = 0>
 __device__ __forceinline__ void gemm_fast_body(const GemmArgs& p) {
+  constexpr int NW = WM * WN;
+  constexpr int FM = BM / WM / 32;
+  constexpr int FN = BN / WN / 32;
+  constexpr int GROUPS = (BM + BN) / 8 / NW;  // 8-row DMA groups per wave per slab
   __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE_BYTES];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 2;  // 0..1 -> 128 rows of M
-  const int wn = wave & 3;   // 0..3 -> 64 cols of N
+  const int wm = wave / WN;
+  const int wn = wave % WN;
   int tm, tn;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * BM;
@@ -95,29 +120,43 @@ __device__ __forceinline__ void gemm_fast_body(const GemmArgs& p) {
   const int b_lim = p.N - 1 - n0;
   const int kslabs = (p.K * ES) / SLAB;
 
-  f32x16 accf[4][2];
-  i32x16 acci[4][2];
+  f32x16 accf[FM][FN];
+  i32x16 acci[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < FN; ++j) {
       if constexpr (MODE == GEMM_I8) acci[i][j] = (i32x16){};
       else accf[i][j] = (f32x16){};
     }
 
+  // slab loads: row groups 0..31 are A rows, 32..63 are B rows
   auto issue = [&](int stage, int slab) {
     char* sa = lds + stage * STAGE_BYTES;
-    char* sb = sa + BM * SLAB;
     const long long kb = (long long)slab * SLAB;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int rg = wave * 4 + t;  // 8-row group 0..31
-      dma_rows(abase, lda_b, rg * 8, a_lim, kb, sa + rg * 1024, lane);
+    for (int t = 0; t < GROUPS; ++t) {
+      const int rg = wave * GROUPS + t;
+      if (rg < BM / 8) dma_rows(abase, lda_b, rg * 8, a_lim, kb, sa + rg * 1024, lane);
+      else dma_rows(bbase, ldb_b, (rg - BM / 8) * 8, b_lim, kb, sa + rg * 1024, lane);
+    }
+  };
+
+  const int g = lane >> 5;
+  const int r = lane & 31;
+  u32x4 af[2][FM], bfr[2][FN];
+  auto frags = [&](const char* sa, int ks, int buf) {
+    const char* sb = sa + BM * SLAB;
+    const int chunk = ks * 2 + g;
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi) {
+      const int row = wm * (BM / WM) + mi * 32 + r;
+      af[buf][mi] = *(const u32x4*)(sa + row * SLAB + ((chunk ^ swz(row)) << 4));
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int rg = wave * 4 + t;
-      dma_rows(bbase, ldb_b, rg * 8, b_lim, kb, sb + rg * 1024, lane);
+    for (int ni = 0; ni < FN; ++ni) {
+      const int row = wn * (BN / WN) + ni * 32 + r;
+      bfr[buf][ni] = *(const u32x4*)(sb + row * SLAB + ((chunk ^ swz(row)) << 4));
     }
   };
 
@@ -125,45 +164,39 @@ __device__ __forceinline__ void gemm_fast_body(const GemmArgs& p) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  const int g = lane >> 5;
-  const int r = lane & 31;
+  constexpr bool DB = (SCHED == 1 || SCHED == 2 || SCHED == 3);
+  constexpr bool PRIO = (SCHED == 3 || SCHED == 4);
   for (int kt = 0; kt < kslabs; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < kslabs) issue(cur ^ 1, kt + 1);
     const char* sa = lds + cur * STAGE_BYTES;
-    const char* sb = sa + BM * SLAB;
+    if constexpr (DB) frags(sa, 0, 0);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int chunk = ks * 2 + g;
-      u32x4 af[4], bfr[2];
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi) {
-        const int row = wm * 128 + mi * 32 + r;
-        af[mi] = *(const u32x4*)(sa + row * SLAB + ((chunk ^ swz(row)) << 4));
+      const int buf = DB ? (ks & 1) : 0;
+      if constexpr (DB) {
+        // fragments of the next k-step are read while this step's MFMAs run
+        if (ks + 1 < 4) frags(sa, ks + 1, (ks + 1) & 1);
+      } else {
+        frags(sa, ks, 0);
       }
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        const int row = wn * 64 + ni * 32 + r;
-        bfr[ni] = *(const u32x4*)(sb + row * SLAB + ((chunk ^ swz(row)) << 4));
-      }
+      for (int mi = 0; mi < FM; ++mi)
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+        for (int ni = 0; ni < FN; ++ni)
+          mfma_step<MODE>(bfr[buf][ni], af[buf][mi], accf[mi][ni], acci[mi][ni]);
+      if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
+      if constexpr (SCHED == 2 || SCHED == 3) {
+        if (ks + 1 < 4) {
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-          if constexpr (MODE == GEMM_BF16) {
-            accf[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(bf16x8, bfr[ni]), __builtin_bit_cast(bf16x8, af[mi]),
-                accf[mi][ni], 0, 0, 0);
-          } else if constexpr (MODE == GEMM_F16) {
-            accf[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                __builtin_bit_cast(f16x8, bfr[ni]), __builtin_bit_cast(f16x8, af[mi]),
-                accf[mi][ni], 0, 0, 0);
-          } else {
-            acci[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                __builtin_bit_cast(i32x4, bfr[ni]), __builtin_bit_cast(i32x4, af[mi]),
-                acci[mi][ni], 0, 0, 0);
+          for (int i = 0; i < FM + FN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
           }
+          __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + FN), 0);
         }
+      }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -173,16 +206,16 @@ __device__ __forceinline__ void gemm_fast_body(const GemmArgs& p) {
   // n = 8q + 4g + {0..3} of each 32-column fragment.
   const bool vec_ok = ((p.c_s0 & 3) == 0);
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-    const int m = m0 + wm * 128 + mi * 32 + r;
+  for (int mi = 0; mi < FM; ++mi) {
+    const int m = m0 + wm * (BM / WM) + mi * 32 + r;
     if (m >= p.M) continue;
     float rs = 1.0f;
     if constexpr (MODE == GEMM_I8) rs = p.sa ? p.sa[m] : 1.0f;
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
+    for (int ni = 0; ni < FN; ++ni) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * 64 + ni * 32 + q * 8 + g * 4;
+        const int n = n0 + wn * (BN / WN) + ni * 32 + q * 8 + g * 4;
         float v[4];
         if constexpr (MODE == GEMM_I8) {
           int iv[4];
@@ -190,7 +223,7 @@ __device__ __forceinline__ void gemm_fast_body(const GemmArgs& p) {
           for (int e = 0; e < 4; ++e) iv[e] = acci[mi][ni][q * 4 + e];
           if (p.acc_out) {
             int* dst = p.acc_out + (long long)m * p.acc_s0 + n;
-            if (vec_ok && ((p.acc_s0 & 3) == 0) && n + 3 < p.N) {
+            if (((p.acc_s0 & 3) == 0) && n + 3 < p.N) {
               *(i32x4*)dst = (i32x4){iv[0], iv[1], iv[2], iv[3]};
             } else {
 #pragma unroll
@@ -303,15 +336,15 @@ __device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
 
 }  // namespace g950
 
-extern "C" __global__ __launch_bounds__(512) void g950_gemm_bf16_256x256(const g950::GemmArgs p) {
-  g950::gemm_fast_body<g950::GEMM_BF16>(p);
-}
-extern "C" __global__ __launch_bounds__(512) void g950_gemm_f16_256x256(const g950::GemmArgs p) {
-  g950::gemm_fast_body<g950::GEMM_F16>(p);
-}
-extern "C" __global__ __launch_bounds__(512) void g950_gemm_i8_256x256(const g950::GemmArgs p) {
-  g950::gemm_fast_body<g950::GEMM_I8>(p);
-}
+#define G950_GEMM_FAST(NAME, MODE, WM, WN, SCHED)                                           \
+  extern "C" __global__ __launch_bounds__(WM * WN * 64) void NAME(const g950::GemmArgs p) {  \
+    g950::gemm_fast_body<MODE, WM, WN, SCHED>(p);                                          \
+  }
+// measured on MI355X (8192^3 bf16, 4096x8192x8192 int8): 4 x 2 waves of
+// 64 x 128 tiles; interleaved fragment reads for the 16-bit kernels
+G950_GEMM_FAST(g950_gemm_bf16_256x256, g950::GEMM_BF16, 4, 2, 2)
+G950_GEMM_FAST(g950_gemm_f16_256x256, g950::GEMM_F16, 4, 2, 2)
+G950_GEMM_FAST(g950_gemm_i8_256x256, g950::GEMM_I8, 4, 2, 0)
 extern "C" __global__ __launch_bounds__(256) void g950_gemm_general(const g950::GemmArgs p) {
   g950::gemm_general_body<false>(p);
 }
