@@ -13,15 +13,24 @@
 //     lane then holds 16 scores of ONE query (lane%32) per 32-key block, so
 //     the running max / sum of the online softmax are per-lane scalars; the
 //     two half-waves holding the same query combine with one cross-lane swap.
-//   * O^T = V^T . P^T: V^T (LDS, written transposed from the row-major V tile)
-//     feeds the A port and the lane's own probabilities, packed to 16 bits in
-//     register order, feed the B port -- P never leaves registers.  The O^T
-//     accumulator again holds one query per lane, so the rescale by
-//     exp2(m_old - m_new) is a per-lane scalar multiply.
-//   * exp2 domain: scores are pre-multiplied by scale*log2(e) and exponentiated
-//     with v_exp_f32; lse is converted back to natural log at the end.
-//   * K/V tiles of 64 keys are register-staged: the next tile's global loads
-//     are issued before the current tile's MFMAs and written to LDS after.
+//   * O^T = V^T . P^T: the A port takes V^T straight from the row-major V
+//     tile through ds_read_b64_tr_b16 (gfx950's transposing LDS read: in each
+//     16-lane group, output lane i, slot k = element i%4 of the 8 bytes read
+//     by lane 4k + i/4; lane j therefore reads V[key0 + j/4][d0 + 4(j%4)..+3]
+//     and receives V[key0..key0+3][d0 + i]).  The lane's own probabilities,
+//     packed to 16 bits in register order, feed the B port -- P never leaves
+//     registers.  The O^T accumulator holds one query per lane, so the online
+//     rescale is a per-lane scalar multiply.
+//   * exp2 domain: scores are scaled by scale*log2(e) inside the exponent's
+//     fma and exponentiated with v_exp_f32; lse returns to natural log at the
+//     end.  The reference max of a row is only moved when the tile max exceeds
+//     it by more than 8 (p <= 2^8, exact because l and O share the reference);
+//     the O rescale is skipped when no row of the wave moved.
+//   * K and V tiles (64 keys) are filled by direct global->LDS DMA
+//     (global_load_lds_dwordx4) into a 3-stage ring, two tiles ahead; the
+//     16-byte chunks of a row are XOR-swizzled (K: key&15, V: 2*(key&7)) so the
+//     MFMA operand reads are bank-conflict free.  The S^T MFMAs of tile j+1 are
+//     issued before the softmax of tile j, so VALU and MFMA work overlap.
 //   * causal: a q-block stops at its diagonal tile, waves skip key tiles that
 //     lie wholly above their queries, and the mask is applied only on tiles
 //     crossing the diagonal.  Q-blocks are issued longest-first, and the Hq/Hkv
@@ -40,16 +49,13 @@ template <int D, int NW>
 struct AttnCfg {
   static constexpr int NT = NW * 64;              // threads per workgroup
   static constexpr int BQ = NW * 32;              // queries per workgroup
-  static constexpr int KROW = D * 2;              // K tile row bytes
-  static constexpr int KCHUNKS = D / 8;           // 16-byte chunks per K row
-  static constexpr int VT_PITCH = ATT_BK + 4;     // V^T row pitch in elements (pad: conflict-free reads)
-  static constexpr int K_BYTES = ATT_BK * KROW;
-  static constexpr int VT_BYTES = D * VT_PITCH * 2;
-  static constexpr int STAGE = K_BYTES + VT_BYTES;
-  static constexpr int K_TOTAL = ATT_BK * KCHUNKS;           // 16-B chunks per K tile
-  static constexpr int V_TOTAL = (ATT_BK / 2) * (D / 8);     // key-pair x 8-d units per V tile
-  static constexpr int K_LOADS = (K_TOTAL + NT - 1) / NT;    // per thread
-  static constexpr int V_UNITS = (V_TOTAL + NT - 1) / NT;
+  static constexpr int ROW = D * 2;               // tile row bytes (K and V)
+  static constexpr int CHUNKS = D / 8;            // 16-byte chunks per row
+  static constexpr int TILE = ATT_BK * ROW;       // one K or V tile
+  static constexpr int STAGE = 2 * TILE;          // K then V
+  static constexpr int ROWS_PER_DMA = 1024 / ROW; // rows one wave-instruction fills
+  static constexpr int DMAS = TILE / 1024;        // wave-instructions per tile
+  static constexpr int DMA_PER_WAVE = (2 * DMAS + NW - 1) / NW;
   static constexpr int DBLK = D / 32;
   static constexpr int DSTEPS = D / 16;
 };
@@ -59,13 +65,21 @@ __device__ __forceinline__ int kslot(int key, int chunk) {
   if constexpr (D == 128) return chunk ^ (key & 15);
   else return chunk ^ ((key >> 1) & 7);
 }
+template <int D>
+__device__ __forceinline__ int vslot(int key, int chunk) {
+  if constexpr (D == 128) return chunk ^ ((key & 7) << 1);
+  else return chunk ^ ((key & 3) << 1);
+}
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// two fp32 -> one packed 16-bit pair (a in the low half): one
+// v_cvt_pk_bf16_f32 / v_cvt_pkrtz-free f16 conversion
 __device__ __forceinline__ uint32_t pack2(float a, float b, bool f16) {
-  if (f16)
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
-  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)a) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)b) << 16);
+  if (f16) return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
 }
 
 template <bool F16>
@@ -78,15 +92,41 @@ __device__ __forceinline__ f32x16 mfma16(const u32x4& a, const u32x4& b, const f
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Eight ds_read_b64_tr_b16 of the row-major V tile (transposed across each
+// 16-lane group) followed by their completion wait.  Written as one asm block
+// because the compiler, unable to see the address of a transposing read,
+// would otherwise wait for every outstanding global->LDS DMA before it -- the
+// in-flight prefetch of the next tile; the ring's own vmcnt wait + barrier
+// already order these reads after the DMA that filled this tile.
+__device__ __forceinline__ void read_tr8(const uint32_t (&a)[8], u32x2 (&v)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %9\n\t"
+      "ds_read_b64_tr_b16 %2, %10\n\t"
+      "ds_read_b64_tr_b16 %3, %11\n\t"
+      "ds_read_b64_tr_b16 %4, %12\n\t"
+      "ds_read_b64_tr_b16 %5, %13\n\t"
+      "ds_read_b64_tr_b16 %6, %14\n\t"
+      "ds_read_b64_tr_b16 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+        "=&v"(v[6]), "=&v"(v[7])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
+      : "memory");
+}
+
 // NW waves x 32 queries of one (z, q-head); key tiles of 64 in a 3-stage LDS
-// ring.  Iteration j: barrier; stage tile j+2 (already in registers) into LDS;
-// issue the global loads of tile j+3; issue the S^T MFMAs of tile j+1; run the
-// online softmax of tile j on the VALU while those MFMAs execute; O^T += V^T.P^T
-// for tile j.
+// ring.  Iteration j: wait for this wave's DMA of tile j+1; barrier; issue
+// the DMA of tile j+2; issue the S^T MFMAs of tile j+1; online softmax of
+// tile j on the VALU while those MFMAs execute; O^T += V^T.P^T for tile j.
 template <int D, bool F16, int NW>
 __device__ __forceinline__ void attn_body(const AttnArgs& p) {
   using C = AttnCfg<D, NW>;
-  __shared__ __attribute__((aligned(16))) char lds[ATT_STAGES * C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds[ATT_STAGES * C::STAGE];
   if (blockDim.x != C::NT) return;  // launch shape must match the instantiation
 
   const int tid = threadIdx.x;
@@ -138,67 +178,40 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
   if (p.causal) kend = min(kend, q_last_block + 1);
   const int ntiles = (kend + ATT_BK - 1) / ATT_BK;
 
-  // ---- register staging of one tile
-  u32x4 kst[C::K_LOADS];
-  u32x4 vst[C::V_UNITS][2];
-  auto gload = [&](int t) {
+  // ---- DMA of one K+V tile: wave-instruction d (0..2*DMAS-1) fills 1 KiB
+  // (ROWS_PER_DMA rows); instructions are dealt round-robin over the waves
+  auto dma_tile = [&](int t) {
+    char* stage = lds + (t % ATT_STAGES) * C::STAGE;
     const int kv0 = t * ATT_BK;
 #pragma unroll
-    for (int u = 0; u < C::K_LOADS; ++u) {
-      const int c = tid + u * C::NT;
-      if (C::K_TOTAL % C::NT && c >= C::K_TOTAL) break;
-      const int key = c / C::KCHUNKS, ch = c % C::KCHUNKS;
-      const int gk = min(kv0 + key, p.Sk - 1);
-      kst[u] = *(const u32x4*)(kbase + 2 * (long long)gk * p.k_ss + ch * 16);
-    }
-#pragma unroll
-    for (int u = 0; u < C::V_UNITS; ++u) {
-      const int c = tid + u * C::NT;
-      if (C::V_TOTAL % C::NT && c >= C::V_TOTAL) break;
-      const int kp = c % (ATT_BK / 2), dc = c / (ATT_BK / 2);
-      const int k0 = min(kv0 + 2 * kp, p.Sk - 1), k1 = min(kv0 + 2 * kp + 1, p.Sk - 1);
-      vst[u][0] = *(const u32x4*)(vbase + 2 * (long long)k0 * p.v_ss + dc * 16);
-      vst[u][1] = *(const u32x4*)(vbase + 2 * (long long)k1 * p.v_ss + dc * 16);
-    }
-  };
-  auto lstore = [&](int stage) {
-    char* k_lds = lds + stage * C::STAGE;
-    char* vt_lds = k_lds + C::K_BYTES;
-#pragma unroll
-    for (int u = 0; u < C::K_LOADS; ++u) {
-      const int c = tid + u * C::NT;
-      if (C::K_TOTAL % C::NT && c >= C::K_TOTAL) break;
-      const int key = c / C::KCHUNKS, ch = c % C::KCHUNKS;
-      *(u32x4*)(k_lds + key * C::KROW + (kslot<D>(key, ch) << 4)) = kst[u];
-    }
-#pragma unroll
-    for (int u = 0; u < C::V_UNITS; ++u) {
-      const int c = tid + u * C::NT;
-      if (C::V_TOTAL % C::NT && c >= C::V_TOTAL) break;
-      const int kp = c % (ATT_BK / 2), dc = c / (ATT_BK / 2);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // element pair (2e, 2e+1) of the 8 d-values, for keys 2kp and 2kp+1
-        const uint32_t a = vst[u][0][e], b = vst[u][1][e];
-        const uint32_t lo = (a & 0xFFFFu) | (b << 16);      // d = 8dc+2e
-        const uint32_t hi = (a >> 16) | (b & 0xFFFF0000u);  // d = 8dc+2e+1
-        const int d = dc * 8 + 2 * e;
-        *(uint32_t*)(vt_lds + (d * C::VT_PITCH + 2 * kp) * 2) = lo;
-        *(uint32_t*)(vt_lds + ((d + 1) * C::VT_PITCH + 2 * kp) * 2) = hi;
+    for (int u = 0; u < C::DMA_PER_WAVE; ++u) {
+      const int d = wave + u * NW;
+      if (d < 2 * C::DMAS) {
+        const bool is_v = d >= C::DMAS;
+        const int blk = is_v ? d - C::DMAS : d;
+        const int row = blk * C::ROWS_PER_DMA + lane / C::CHUNKS;  // key within the tile
+        const int slot = lane % C::CHUNKS;
+        const int chunk = is_v ? vslot<D>(row, slot) : kslot<D>(row, slot);
+        const int gk = min(kv0 + row, p.Sk - 1);
+        const char* src = is_v ? vbase + 2 * (long long)gk * p.v_ss : kbase + 2 * (long long)gk * p.k_ss;
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void*)(src + chunk * 16),
+            (__attribute__((address_space(3))) void*)(stage + (is_v ? C::TILE : 0) + blk * 1024),
+            16, 0, 0);
       }
     }
   };
   auto active = [&](int t) { return !(p.causal && t * ATT_BK > qw + 31) && (qw < p.Sq); };
-  // S^T tile (2 blocks of 32 keys) from the K tile in `stage`
-  auto qk = [&](int stage, f32x16* s) {
-    const char* k_lds = lds + stage * C::STAGE;
+  // S^T tile (2 blocks of 32 keys) from the K tile of tile t
+  auto qk = [&](int t, f32x16* s) {
+    const char* k_lds = lds + (t % ATT_STAGES) * C::STAGE;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       s[kb] = (f32x16){};
       const int key = kb * 32 + r;
 #pragma unroll
       for (int ks = 0; ks < C::DSTEPS; ++ks) {
-        const u32x4 kf = *(const u32x4*)(k_lds + key * C::KROW + (kslot<D>(key, ks * 2 + g) << 4));
+        const u32x4 kf = *(const u32x4*)(k_lds + key * C::ROW + (kslot<D>(key, ks * 2 + g) << 4));
         s[kb] = mfma16<F16>(kf, qf[ks], s[kb]);
       }
     }
@@ -208,14 +221,20 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
 #pragma unroll
   for (int b = 0; b < C::DBLK; ++b) oacc[b] = (f32x16){};
   const float c2 = p.scale_log2;
-  float m_run = -__builtin_huge_valf();  // running max of the RAW scores
-  float l_run = 0.0f;                    // this lane's partial row sum
+  float ms = -__builtin_huge_valf();  // reference max of the row, scaled (log2 units)
+  float l_run = 0.0f;                 // this lane's partial row sum
+  // transposing-read geometry: 16-lane group q -> (g, half), lane j in group
+  const int trj = lane & 15;
+  const int tr_key = (lane >> 5) * 4 + (trj >> 2);              // + kb*32 + 16*tt (+8)
+  const int tr_d = ((lane >> 4) & 1) * 16 + 4 * (trj & 3);      // + b*32
 
   // softmax of one S^T tile + O^T += V^T P^T
   auto consume = [&](int t, f32x16* s) {
     const int kv0 = t * ATT_BK;
     const bool need_mask = (p.causal && kv0 + ATT_BK - 1 > qw) || (kv0 + ATT_BK > p.Sk);
     if (need_mask) {
+      // key kv0 + 32kb + 8(vv>>2) + 4g + (vv&3) is kept iff its in-tile
+      // offset 32kb + 8(vv>>2) + (vv&3) <= thr (one compare per score)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -229,19 +248,21 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
     for (int vv = 2; vv < 16; vv += 2) mt = fmaxf(mt, fmaxf(s[0][vv], s[0][vv + 1]));
 #pragma unroll
     for (int vv = 0; vv < 16; vv += 2) mt = fmaxf(mt, fmaxf(s[1][vv], s[1][vv + 1]));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float m_new = fmaxf(m_run, mt);
-    // rows whose keys so far are all masked keep m = -inf; exponent base 0
-    // then gives exp2(-inf) = 0 instead of NaN
-    const float mb = (m_new == -__builtin_huge_valf()) ? 0.0f : m_new * c2;
-    if (__any(m_new > m_run)) {  // wave-uniform: skip the O rescale when no max moved
-      const float alpha = __builtin_amdgcn_exp2f(m_run * c2 - mb);
+    mt = fmaxf(mt, __shfl_xor(mt, 32)) * c2;
+    // move the reference only when the tile max exceeds it by more than 8
+    const bool move = mt > ms + 8.0f;
+    if (__any(move)) {
+      const float ms_new = move ? mt : ms;
+      const float alpha = __builtin_amdgcn_exp2f(ms - ms_new);  // 0 on the first tile
       l_run *= alpha;
 #pragma unroll
       for (int b = 0; b < C::DBLK; ++b) oacc[b] *= alpha;
+      ms = ms_new;
     }
-    m_run = m_new;
-    const char* vt_lds = lds + (t % ATT_STAGES) * C::STAGE + C::K_BYTES;
+    // a row whose keys so far are all masked keeps ms = -inf: exponent base 0
+    // gives exp2(-inf) = 0 instead of NaN
+    const float mb = (ms == -__builtin_huge_valf()) ? 0.0f : ms;
+    const char* v_lds = lds + (t % ATT_STAGES) * C::STAGE + C::TILE;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -254,33 +275,42 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
         u32x4 pf;
 #pragma unroll
         for (int e = 0; e < 4; ++e) pf[e] = pack2(s[kb][8 * tt + 2 * e], s[kb][8 * tt + 2 * e + 1], F16);
-        const int kcol = kb * 32 + 16 * tt + 4 * g;
+        const int key0 = kb * 32 + 16 * tt + tr_key;
+        const int key1 = key0 + 8;
+        uint32_t addr[8];
+        u32x2 vt[8];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int bb = b < C::DBLK ? b : 0;
+          const int db = (bb * 32 + tr_d) * 2;  // byte offset of the 4 d-values in the row
+          addr[2 * b] = lds_addr(v_lds + key0 * C::ROW + (vslot<D>(key0, db >> 4) << 4) + (db & 15));
+          addr[2 * b + 1] = lds_addr(v_lds + key1 * C::ROW + (vslot<D>(key1, db >> 4) << 4) + (db & 15));
+        }
+        read_tr8(addr, vt);
 #pragma unroll
         for (int b = 0; b < C::DBLK; ++b) {
-          const char* row = vt_lds + (b * 32 + r) * C::VT_PITCH * 2;
-          const u32x2 lo = *(const u32x2*)(row + kcol * 2);
-          const u32x2 hi = *(const u32x2*)(row + (kcol + 8) * 2);
-          const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
+          const u32x4 vf = {vt[2 * b][0], vt[2 * b][1], vt[2 * b + 1][0], vt[2 * b + 1][1]};
           oacc[b] = mfma16<F16>(vf, pf, oacc[b]);
         }
       }
     }
   };
 
-  // ---- prologue: tiles 0 and 1 in LDS, tile 2 in registers, S of tile 0
+  // ---- prologue: DMA of tiles 0 and 1, S of tile 0
   f32x16 sa[2], sb[2];
-  if (ntiles > 0) { gload(0); lstore(0); }
-  if (ntiles > 1) { gload(1); lstore(1); }
+  if (ntiles > 0) dma_tile(0);
+  if (ntiles > 1) dma_tile(1);
+  if (ntiles > 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::DMA_PER_WAVE) : "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (ntiles > 2) gload(2);
   if (ntiles > 0 && active(0)) qk(0, sa);
 
   // ---- main loop, unrolled by two so the S buffers alternate without copies
   auto iteration = [&](int t, f32x16* s_cur, f32x16* s_next) {
-    __syncthreads();  // every wave is done with tile t-1 (its stage is free)
-    if (t + 2 < ntiles) lstore((t + 2) % ATT_STAGES);
-    if (t + 3 < ntiles) gload(t + 3);
-    if (t + 1 < ntiles && active(t + 1)) qk((t + 1) % ATT_STAGES, s_next);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA of tile t+1
+    __syncthreads();  // tile t+1 visible; every wave is done with tile t-1
+    if (t + 2 < ntiles) dma_tile(t + 2);
+    if (t + 1 < ntiles && active(t + 1)) qk(t + 1, s_next);
     if (active(t)) consume(t, s_cur);
   };
   int t = 0;
@@ -289,8 +319,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
     iteration(t + 1, sb, sa);
   }
   if (t < ntiles) iteration(t, sa, sb);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // ---- epilogue: O = O / l ; lse = (m*c2 + log2 l) * ln2
+  // ---- epilogue: O = O / l ; lse = (ms + log2 l) * ln2
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   if (my_q < p.Sq) {
     const bool empty = !(l_tot > 0.0f);  // zero or NaN
@@ -311,8 +342,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
                                           (uint32_t)hv[2] | ((uint32_t)hv[3] << 16)};
       }
     if (p.lse && g == 0) {
-      const float lse = empty ? __builtin_huge_valf()
-                              : (m_run * c2 + __log2f(l_tot)) * 0.69314718055994530942f;
+      const float lse = empty ? __builtin_huge_valf() : (ms + __log2f(l_tot)) * 0.69314718055994530942f;
       p.lse[(long long)z * p.lse_sz + (long long)h * p.lse_sh + (long long)my_q * p.lse_ss] = lse;
     }
   }
