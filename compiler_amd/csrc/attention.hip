@@ -27,10 +27,13 @@
 //     it by more than 8 (p <= 2^8, exact because l and O share the reference);
 //     the O rescale is skipped when no row of the wave moved.
 //   * K and V tiles (64 keys) are filled by direct global->LDS DMA
-//     (global_load_lds_dwordx4) into a 3-stage ring, two tiles ahead; the
-//     16-byte chunks of a row are XOR-swizzled (K: key&15, V: 2*(key&7)) so the
-//     MFMA operand reads are bank-conflict free.  The S^T MFMAs of tile j+1 are
-//     issued before the softmax of tile j, so VALU and MFMA work overlap.
+//     (global_load_lds_dwordx4) into a 3-stage ring, two tiles ahead.  Tile
+//     layouts make every MFMA operand read a per-lane base plus a compile-time
+//     offset, bank-conflict free:  K as [16-d slab][key][32 B] with the two
+//     16-byte halves swapped on odd (key>>3); V as [32-d block][key][64 B], so
+//     the four rows a transposing read touches form one contiguous 256 B run.
+//     The S^T MFMAs of tile j+1 are issued before the softmax of tile j, so
+//     VALU and MFMA work overlap.
 //   * causal: a q-block stops at its diagonal tile, waves skip key tiles that
 //     lie wholly above their queries, and the mask is applied only on tiles
 //     crossing the diagonal.  Q-blocks are issued longest-first, and the Hq/Hkv
@@ -53,23 +56,11 @@ struct AttnCfg {
   static constexpr int CHUNKS = D / 8;            // 16-byte chunks per row
   static constexpr int TILE = ATT_BK * ROW;       // one K or V tile
   static constexpr int STAGE = 2 * TILE;          // K then V
-  static constexpr int ROWS_PER_DMA = 1024 / ROW; // rows one wave-instruction fills
   static constexpr int DMAS = TILE / 1024;        // wave-instructions per tile
   static constexpr int DMA_PER_WAVE = (2 * DMAS + NW - 1) / NW;
   static constexpr int DBLK = D / 32;
   static constexpr int DSTEPS = D / 16;
 };
-
-template <int D>
-__device__ __forceinline__ int kslot(int key, int chunk) {
-  if constexpr (D == 128) return chunk ^ (key & 15);
-  else return chunk ^ ((key >> 1) & 7);
-}
-template <int D>
-__device__ __forceinline__ int vslot(int key, int chunk) {
-  if constexpr (D == 128) return chunk ^ ((key & 7) << 1);
-  else return chunk ^ ((key & 3) << 1);
-}
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -96,26 +87,40 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
 
-// Eight ds_read_b64_tr_b16 of the row-major V tile (transposed across each
-// 16-lane group) followed by their completion wait.  Written as one asm block
-// because the compiler, unable to see the address of a transposing read,
-// would otherwise wait for every outstanding global->LDS DMA before it -- the
-// in-flight prefetch of the next tile; the ring's own vmcnt wait + barrier
-// already order these reads after the DMA that filled this tile.
-__device__ __forceinline__ void read_tr8(const uint32_t (&a)[8], u32x2 (&v)[8]) {
+// Eight ds_read_b64_tr_b16 of the V tile (transposed across each 16-lane
+// group) at `base` + compile-time offsets, followed by their completion wait.
+// Written as one asm block because the compiler, unable to see the address of
+// a transposing read, would otherwise wait for every outstanding
+// global->LDS DMA before it -- the in-flight prefetch of the next tile; the
+// ring's own vmcnt wait + barrier already order these reads after the DMA
+// that filled this tile.
+template <int O0, int O1, int O2, int O3>
+__device__ __forceinline__ void read_tr4(uint32_t base, u32x2 (&v)[8]) {
   asm volatile(
-      "ds_read_b64_tr_b16 %0, %8\n\t"
-      "ds_read_b64_tr_b16 %1, %9\n\t"
-      "ds_read_b64_tr_b16 %2, %10\n\t"
-      "ds_read_b64_tr_b16 %3, %11\n\t"
-      "ds_read_b64_tr_b16 %4, %12\n\t"
-      "ds_read_b64_tr_b16 %5, %13\n\t"
-      "ds_read_b64_tr_b16 %6, %14\n\t"
-      "ds_read_b64_tr_b16 %7, %15\n\t"
+      "ds_read_b64_tr_b16 %0, %4 offset:%5\n\t"
+      "ds_read_b64_tr_b16 %1, %4 offset:%6\n\t"
+      "ds_read_b64_tr_b16 %2, %4 offset:%7\n\t"
+      "ds_read_b64_tr_b16 %3, %4 offset:%8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "v"(base), "i"(O0), "i"(O1), "i"(O2), "i"(O3)
+      : "memory");
+}
+template <int O0, int O1, int O2, int O3, int O4, int O5, int O6, int O7>
+__device__ __forceinline__ void read_tr8(uint32_t base, u32x2 (&v)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8 offset:%9\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:%10\n\t"
+      "ds_read_b64_tr_b16 %2, %8 offset:%11\n\t"
+      "ds_read_b64_tr_b16 %3, %8 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %4, %8 offset:%13\n\t"
+      "ds_read_b64_tr_b16 %5, %8 offset:%14\n\t"
+      "ds_read_b64_tr_b16 %6, %8 offset:%15\n\t"
+      "ds_read_b64_tr_b16 %7, %8 offset:%16\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
         "=&v"(v[6]), "=&v"(v[7])
-      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
+      : "v"(base), "i"(O0), "i"(O1), "i"(O2), "i"(O3), "i"(O4), "i"(O5), "i"(O6), "i"(O7)
       : "memory");
 }
 
@@ -178,8 +183,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
   if (p.causal) kend = min(kend, q_last_block + 1);
   const int ntiles = (kend + ATT_BK - 1) / ATT_BK;
 
-  // ---- DMA of one K+V tile: wave-instruction d (0..2*DMAS-1) fills 1 KiB
-  // (ROWS_PER_DMA rows); instructions are dealt round-robin over the waves
+  // ---- DMA of one K+V tile: wave-instruction d (0..2*DMAS-1) fills 1 KiB,
+  // dealt round-robin over the waves.  K instruction d = (slab ks, key half
+  // kh): 32 keys x 32 B; V instruction (block b, key quarter kq): 16 keys x 64 B.
   auto dma_tile = [&](int t) {
     char* stage = lds + (t % ATT_STAGES) * C::STAGE;
     const int kv0 = t * ATT_BK;
@@ -187,31 +193,36 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
     for (int u = 0; u < C::DMA_PER_WAVE; ++u) {
       const int d = wave + u * NW;
       if (d < 2 * C::DMAS) {
-        const bool is_v = d >= C::DMAS;
-        const int blk = is_v ? d - C::DMAS : d;
-        const int row = blk * C::ROWS_PER_DMA + lane / C::CHUNKS;  // key within the tile
-        const int slot = lane % C::CHUNKS;
-        const int chunk = is_v ? vslot<D>(row, slot) : kslot<D>(row, slot);
-        const int gk = min(kv0 + row, p.Sk - 1);
-        const char* src = is_v ? vbase + 2 * (long long)gk * p.v_ss : kbase + 2 * (long long)gk * p.k_ss;
-        __builtin_amdgcn_global_load_lds(
-            (const __attribute__((address_space(1))) void*)(src + chunk * 16),
-            (__attribute__((address_space(3))) void*)(stage + (is_v ? C::TILE : 0) + blk * 1024),
-            16, 0, 0);
+        const char* src;
+        if (d < C::DMAS) {
+          const int ks = d >> 1, key = (d & 1) * 32 + (lane >> 1);
+          const int half = (lane & 1) ^ ((key >> 3) & 1);
+          const int gk = min(kv0 + key, p.Sk - 1);
+          src = kbase + 2 * (long long)gk * p.k_ss + ks * 32 + half * 16;
+        } else {
+          const int dv = d - C::DMAS;
+          const int b = dv >> 2, key = (dv & 3) * 16 + (lane >> 2);
+          const int gk = min(kv0 + key, p.Sk - 1);
+          src = vbase + 2 * (long long)gk * p.v_ss + b * 64 + (lane & 3) * 16;
+        }
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                         (__attribute__((address_space(3))) void*)(stage + d * 1024),
+                                         16, 0, 0);
       }
     }
   };
   auto active = [&](int t) { return !(p.causal && t * ATT_BK > qw + 31) && (qw < p.Sq); };
-  // S^T tile (2 blocks of 32 keys) from the K tile of tile t
+  // S^T tile (2 blocks of 32 keys) from the K tile of tile t; lane (g, r)
+  // reads 16 B of key kb*32 + r in slab ks at ks*2048 + kb*1024 + k_lane
+  const int k_lane = r * 32 + ((g ^ ((r >> 3) & 1)) << 4);
   auto qk = [&](int t, f32x16* s) {
-    const char* k_lds = lds + (t % ATT_STAGES) * C::STAGE;
+    const char* k_lds = lds + (t % ATT_STAGES) * C::STAGE + k_lane;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       s[kb] = (f32x16){};
-      const int key = kb * 32 + r;
 #pragma unroll
       for (int ks = 0; ks < C::DSTEPS; ++ks) {
-        const u32x4 kf = *(const u32x4*)(k_lds + key * C::ROW + (kslot<D>(key, ks * 2 + g) << 4));
+        const u32x4 kf = *(const u32x4*)(k_lds + ks * 2048 + kb * 1024);
         s[kb] = mfma16<F16>(kf, qf[ks], s[kb]);
       }
     }
@@ -223,10 +234,10 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
   const float c2 = p.scale_log2;
   float ms = -__builtin_huge_valf();  // reference max of the row, scaled (log2 units)
   float l_run = 0.0f;                 // this lane's partial row sum
-  // transposing-read geometry: 16-lane group q -> (g, half), lane j in group
+  // transposing-read geometry: lane j of 16-lane group (g, half) reads key
+  // 4g + j/4 (+ kb*32 + 16tt (+8)), d = 32b + 16*half + 4*(j%4) .. +3
   const int trj = lane & 15;
-  const int tr_key = (lane >> 5) * 4 + (trj >> 2);              // + kb*32 + 16*tt (+8)
-  const int tr_d = ((lane >> 4) & 1) * 16 + 4 * (trj & 3);      // + b*32
+  const int v_lane = ((lane >> 5) * 4 + (trj >> 2)) * 64 + ((lane >> 4) & 1) * 32 + (trj & 3) * 8;
 
   // softmax of one S^T tile + O^T += V^T P^T
   auto consume = [&](int t, f32x16* s) {
@@ -275,18 +286,20 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
         u32x4 pf;
 #pragma unroll
         for (int e = 0; e < 4; ++e) pf[e] = pack2(s[kb][8 * tt + 2 * e], s[kb][8 * tt + 2 * e + 1], F16);
-        const int key0 = kb * 32 + 16 * tt + tr_key;
-        const int key1 = key0 + 8;
-        uint32_t addr[8];
         u32x2 vt[8];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int bb = b < C::DBLK ? b : 0;
-          const int db = (bb * 32 + tr_d) * 2;  // byte offset of the 4 d-values in the row
-          addr[2 * b] = lds_addr(v_lds + key0 * C::ROW + (vslot<D>(key0, db >> 4) << 4) + (db & 15));
-          addr[2 * b + 1] = lds_addr(v_lds + key1 * C::ROW + (vslot<D>(key1, db >> 4) << 4) + (db & 15));
+        const uint32_t vb = lds_addr(v_lds) + v_lane;
+        // offsets: 32-d block b at b*4096, key row (kb*32 + 16tt [+8]) * 64
+        if constexpr (C::DBLK == 4) {
+          if (kb == 0 && tt == 0) read_tr8<0, 512, 4096, 4608, 8192, 8704, 12288, 12800>(vb, vt);
+          if (kb == 0 && tt == 1) read_tr8<1024, 1536, 5120, 5632, 9216, 9728, 13312, 13824>(vb, vt);
+          if (kb == 1 && tt == 0) read_tr8<2048, 2560, 6144, 6656, 10240, 10752, 14336, 14848>(vb, vt);
+          if (kb == 1 && tt == 1) read_tr8<3072, 3584, 7168, 7680, 11264, 11776, 15360, 15872>(vb, vt);
+        } else {
+          if (kb == 0 && tt == 0) read_tr4<0, 512, 4096, 4608>(vb, vt);
+          if (kb == 0 && tt == 1) read_tr4<1024, 1536, 5120, 5632>(vb, vt);
+          if (kb == 1 && tt == 0) read_tr4<2048, 2560, 6144, 6656>(vb, vt);
+          if (kb == 1 && tt == 1) read_tr4<3072, 3584, 7168, 7680>(vb, vt);
         }
-        read_tr8(addr, vt);
 #pragma unroll
         for (int b = 0; b < C::DBLK; ++b) {
           const u32x4 vf = {vt[2 * b][0], vt[2 * b][1], vt[2 * b + 1][0], vt[2 * b + 1][1]};
