@@ -240,6 +240,35 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
   const int v_lane = ((lane >> 5) * 4 + (trj >> 2)) * 64 + ((lane >> 4) & 1) * 32 + (trj & 3) * 8;
 
   // softmax of one S^T tile + O^T += V^T P^T
+  // O^T += V^T . P^T for tile t (P packed in registers)
+  auto pv = [&](int t, const u32x4 (&pf)[2][2]) {
+    const char* v_lds = lds + (t % ATT_STAGES) * C::STAGE + C::TILE;
+    const uint32_t vb = lds_addr(v_lds) + v_lane;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        u32x2 vt[8];
+        // offsets: 32-d block b at b*4096, key row (kb*32 + 16tt [+8]) * 64
+        if constexpr (C::DBLK == 4) {
+          if (kb == 0 && tt == 0) read_tr8<0, 512, 4096, 4608, 8192, 8704, 12288, 12800>(vb, vt);
+          if (kb == 0 && tt == 1) read_tr8<1024, 1536, 5120, 5632, 9216, 9728, 13312, 13824>(vb, vt);
+          if (kb == 1 && tt == 0) read_tr8<2048, 2560, 6144, 6656, 10240, 10752, 14336, 14848>(vb, vt);
+          if (kb == 1 && tt == 1) read_tr8<3072, 3584, 7168, 7680, 11264, 11776, 15360, 15872>(vb, vt);
+        } else {
+          if (kb == 0 && tt == 0) read_tr4<0, 512, 4096, 4608>(vb, vt);
+          if (kb == 0 && tt == 1) read_tr4<1024, 1536, 5120, 5632>(vb, vt);
+          if (kb == 1 && tt == 0) read_tr4<2048, 2560, 6144, 6656>(vb, vt);
+          if (kb == 1 && tt == 1) read_tr4<3072, 3584, 7168, 7680>(vb, vt);
+        }
+#pragma unroll
+        for (int b = 0; b < C::DBLK; ++b) {
+          const u32x4 vf = {vt[2 * b][0], vt[2 * b][1], vt[2 * b + 1][0], vt[2 * b + 1][1]};
+          oacc[b] = mfma16<F16>(vf, pf[kb][tt], oacc[b]);
+        }
+      }
+  };
+
   auto consume = [&](int t, f32x16* s) {
     const int kv0 = t * ATT_BK;
     const bool need_mask = (p.causal && kv0 + ATT_BK - 1 > qw) || (kv0 + ATT_BK > p.Sk);
@@ -273,7 +302,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
     // a row whose keys so far are all masked keeps ms = -inf: exponent base 0
     // gives exp2(-inf) = 0 instead of NaN
     const float mb = (ms == -__builtin_huge_valf()) ? 0.0f : ms;
-    const char* v_lds = lds + (t % ATT_STAGES) * C::STAGE + C::TILE;
+    u32x4 pf[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -282,33 +311,13 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
         l_run += s[kb][vv];
       }
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        u32x4 pf;
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) pf[e] = pack2(s[kb][8 * tt + 2 * e], s[kb][8 * tt + 2 * e + 1], F16);
-        u32x2 vt[8];
-        const uint32_t vb = lds_addr(v_lds) + v_lane;
-        // offsets: 32-d block b at b*4096, key row (kb*32 + 16tt [+8]) * 64
-        if constexpr (C::DBLK == 4) {
-          if (kb == 0 && tt == 0) read_tr8<0, 512, 4096, 4608, 8192, 8704, 12288, 12800>(vb, vt);
-          if (kb == 0 && tt == 1) read_tr8<1024, 1536, 5120, 5632, 9216, 9728, 13312, 13824>(vb, vt);
-          if (kb == 1 && tt == 0) read_tr8<2048, 2560, 6144, 6656, 10240, 10752, 14336, 14848>(vb, vt);
-          if (kb == 1 && tt == 1) read_tr8<3072, 3584, 7168, 7680, 11264, 11776, 15360, 15872>(vb, vt);
-        } else {
-          if (kb == 0 && tt == 0) read_tr4<0, 512, 4096, 4608>(vb, vt);
-          if (kb == 0 && tt == 1) read_tr4<1024, 1536, 5120, 5632>(vb, vt);
-          if (kb == 1 && tt == 0) read_tr4<2048, 2560, 6144, 6656>(vb, vt);
-          if (kb == 1 && tt == 1) read_tr4<3072, 3584, 7168, 7680>(vb, vt);
-        }
-#pragma unroll
-        for (int b = 0; b < C::DBLK; ++b) {
-          const u32x4 vf = {vt[2 * b][0], vt[2 * b][1], vt[2 * b + 1][0], vt[2 * b + 1][1]};
-          oacc[b] = mfma16<F16>(vf, pf, oacc[b]);
-        }
-      }
+        for (int e = 0; e < 4; ++e)
+          pf[kb][tt][e] = pack2(s[kb][8 * tt + 2 * e], s[kb][8 * tt + 2 * e + 1], F16);
     }
+    pv(t, pf);
   };
-
   // ---- prologue: DMA of tiles 0 and 1, S of tile 0
   f32x16 sa[2], sb[2];
   if (ntiles > 0) dma_tile(0);
@@ -319,6 +328,57 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
   if (ntiles > 0 && active(0)) qk(0, sa);
 
   // ---- main loop, unrolled by two so the S buffers alternate without copies
+  // Interior tiles (this and the next tile active, no mask) take a branch-free
+  // path: the S^T MFMAs of tile t+1 and the softmax VALU/exp work of tile t
+  // form one basic block, interleaved one MFMA at a time with the operand
+  // read and ~10 VALU/transcendental instructions, so the wave issues VALU
+  // work while its MFMAs execute.  The rare O rescale and the P.V MFMAs follow.
+  auto fast = [&](int t, f32x16* s, f32x16* s_next) {
+    qk(t + 1, s_next);
+    float mt = fmaxf(s[0][0], s[0][1]);
+#pragma unroll
+    for (int vv = 2; vv < 16; vv += 2) mt = fmaxf(mt, fmaxf(s[0][vv], s[0][vv + 1]));
+#pragma unroll
+    for (int vv = 0; vv < 16; vv += 2) mt = fmaxf(mt, fmaxf(s[1][vv], s[1][vv + 1]));
+    mt = fmaxf(mt, __shfl_xor(mt, 32)) * c2;
+    const bool move = mt > ms + 8.0f;
+    const float ms_new = move ? mt : ms;
+    const float alpha = __builtin_amdgcn_exp2f(ms - ms_new);  // 1 unless moved
+    l_run *= alpha;
+    ms = ms_new;
+    u32x4 pf[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int vv = 0; vv < 16; ++vv) {
+        s[kb][vv] = __builtin_amdgcn_exp2f(fmaf(s[kb][vv], c2, -ms));
+        l_run += s[kb][vv];
+      }
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          pf[kb][tt][e] = pack2(s[kb][8 * tt + 2 * e], s[kb][8 * tt + 2 * e + 1], F16);
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * C::DSTEPS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // operand read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
+    }
+    if (__any(move)) {
+#pragma unroll
+      for (int b = 0; b < C::DBLK; ++b) oacc[b] *= alpha;
+    }
+    pv(t, pf);
+  };
+  auto fast_iteration = [&](int t, f32x16* s_cur, f32x16* s_next) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA of tile t+1
+    __syncthreads();  // tile t+1 visible; every wave is done with tile t-1
+    if (t + 2 < ntiles) dma_tile(t + 2);
+    fast(t, s_cur, s_next);
+  };
   auto iteration = [&](int t, f32x16* s_cur, f32x16* s_next) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA of tile t+1
     __syncthreads();  // tile t+1 visible; every wave is done with tile t-1
@@ -326,7 +386,16 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
     if (t + 1 < ntiles && active(t + 1)) qk(t + 1, s_next);
     if (active(t)) consume(t, s_cur);
   };
+  // interior tiles: below every wave's diagonal (causal) and inside Sk, with
+  // a successor tile; rounded down to even so both loops start on sa
+  int full = (p.causal ? q0 : p.Sk) / ATT_BK;
+  full = min(min(full, p.Sk / ATT_BK), ntiles - 1);
+  const int nfast = full > 0 ? (full & ~1) : 0;
   int t = 0;
+  for (; t < nfast; t += 2) {
+    fast_iteration(t, sa, sb);
+    fast_iteration(t + 1, sb, sa);
+  }
   for (; t + 1 < ntiles; t += 2) {
     iteration(t, sa, sb);
     iteration(t + 1, sb, sa);
