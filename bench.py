@@ -117,7 +117,7 @@ def headline(torch, ops, args):
     dom = ("layernorm", ln_kernel, ln_bytes, ln_ms) if ln_ms >= sm_ms else ("softmax", sm_kernel, sm_bytes, sm_ms)
     achieved = dom[2] / (dom[3] * 1e-3) / 1e9
     roof = {"bound": "hbm", "kernel": dom[1], "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(dom[1]),
             "algorithmic_bytes": dom[2], "avg_launch_us": round(dom[3] * 1e3, 2)}
     per_kernel = {
         "layernorm": {"kernel": ln_kernel, "us": round(ln_ms * 1e3, 2),
@@ -251,6 +251,54 @@ def suite(torch, ops):
     return out
 
 
+def pmc_probe(torch, ops):
+    """Counter-collection workload (run under rocprofv3 --pmc): the streaming
+    copy kernel on exactly the bytes of one x (the calibration kernel: same
+    nontemporal 16-byte loads/stores as the row kernels), then 8 launches of
+    each headline kernel on 4 rotating buffer sets, as in the timed region."""
+    from oracle import inputs
+    rows, cols = 8191, 3000
+    dev = "cuda:0"
+    srcs = [torch.empty(rows * cols, dtype=torch.bfloat16, device=dev).normal_() for _ in range(ROTATE)]
+    dsts = [torch.empty_like(x) for x in srcs]
+    copies = [ops.stream_copy(x, y, prepare=True) for x, y in zip(srcs, dsts)]
+    torch.cuda.synchronize()
+    for i in range(8):
+        copies[i % ROTATE]()
+    torch.cuda.synchronize()
+    src = srcs[0]
+    del dsts
+    sets = []
+    for s in range(ROTATE):
+        c = inputs.config2(rows, cols, seed=inputs.SEEDS["c2"] + s)
+        bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
+        sets.append((bf(c["x"]), bf(c["gamma"]), bf(c["beta"]), torch.empty((rows, cols), dtype=torch.bfloat16, device=dev),
+                     torch.empty(rows, device=dev), torch.empty(rows, device=dev)))
+    ln = [ops.layernorm_kernel(x, y, g, b, m, r, cols, cols, 1e-5, prepare=True) for x, g, b, y, m, r in sets]
+    sm = [ops.softmax_kernel(x, y, cols, prepare=True) for x, g, b, y, m, r in sets]
+    torch.cuda.synchronize()
+    for i in range(8):
+        ln[i % ROTATE]()
+    torch.cuda.synchronize()
+    for i in range(8):
+        sm[i % ROTATE]()
+    torch.cuda.synchronize()
+    log(f"pmc probe: copy {src.numel() * 2} B read + write; layernorm/softmax x8 each")
+
+
+def traffic_for(kernel):
+    """HBM bytes per launch measured for `kernel` (profiles/hbm_traffic.json,
+    from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes, copy-calibrated)."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    row = data.get("kernels", {}).get(kernel)
+    return None if row is None else int(row["traffic_bytes"])
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -259,6 +307,8 @@ def main():
     ap.add_argument("--no-suite", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run only the counter-collection workload (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the multi-GPU "
@@ -269,6 +319,9 @@ def main():
     from compiler_amd import operators as ops
     if not torch.cuda.is_available():
         sys.exit("bench.py needs the MI355X")
+    if args.pmc_probe:
+        pmc_probe(torch, ops)
+        return
     log("bench: headline (config 2) ...")
     value, ms_step, wall, roof, per_kernel, step_bytes = headline(torch, ops, args)
     log(f"bench: headline {value:.1f} GB/s, {ms_step * 1e3:.1f} us/step")

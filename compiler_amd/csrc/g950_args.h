@@ -55,6 +55,12 @@ struct AttnArgs {
   int nqb;           // query blocks of 128
 };
 
+struct CopyArgs {
+  const void* x;
+  void* y;
+  long long n16;  // 16-byte vectors
+};
+
 struct AttnGenArgs {
   AttnArgs a;
   int D;

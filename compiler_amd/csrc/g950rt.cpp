@@ -556,6 +556,33 @@ int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const 
   return launch(m, "g950_attn_fwd_general", (unsigned)((rows + 63) / 64), 64u, ga, stream);
 }
 
+// ------------------------------------------------------------------- copy
+int op_copy(g950_module* m, const g950_view* views, uint32_t nviews, uint32_t nsc, void* stream) {
+  if (nviews != 2 || nsc != 0) return fail(G950_USAGE, "copy: needs views (x, y) and no scalars");
+  const g950_view& x = views[0];
+  const g950_view& y = views[1];
+  View vx, vy;
+  if (int rc = check_view(views, 0, "x", (int)x.ndim, vx, false)) return rc;
+  if (int rc = check_view(views, 1, "y", (int)y.ndim, vy, true)) return rc;
+  if (x.ndim != y.ndim || x.dtype != y.dtype) return fail(G950_USAGE, "copy: x and y differ in rank or dtype");
+  long long n = 1, expect = vx.isz;
+  for (int i = (int)x.ndim - 1; i >= 0; --i) {
+    if (vx.shape[i] != vy.shape[i]) return fail(G950_USAGE, "copy: shapes differ");
+    if (vx.shape[i] > 1 && (x.strides[i] != expect || y.strides[i] != expect))
+      return fail(G950_USAGE, "copy: views must be contiguous");
+    expect *= vx.shape[i];
+    n *= vx.shape[i];
+  }
+  const long long bytes = n * vx.isz;
+  if (bytes % 16 || !aligned16(vx.addr()) || !aligned16(vy.addr()))
+    return fail(G950_USAGE, "copy: size and addresses must be multiples of 16 bytes");
+  CopyArgs a{};
+  a.x = x.data; a.y = y.data; a.n16 = bytes / 16;
+  const long long blocks = (a.n16 + 1023) / 1024;
+  const unsigned grid = (unsigned)(blocks < 4096 ? blocks : 4096);
+  return launch(m, "g950_stream_copy", grid, 256u, a, stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -592,6 +619,7 @@ int dispatch(g950_module* m, uint32_t op, const g950_view* views, uint32_t nview
         return op_matmul_i8(m, views, nviews, scalars, nscalars, true, stream);
       case G950_OP_ATTENTION: return op_attention(m, views, nviews, scalars, nscalars, false, stream);
       case G950_OP_ATTENTION_LSE: return op_attention(m, views, nviews, scalars, nscalars, true, stream);
+      case G950_OP_COPY: return op_copy(m, views, nviews, nscalars, stream);
       default: return fail(G950_USAGE, "g950_launch: unknown operator contract %u", op);
     }
   } catch (...) {

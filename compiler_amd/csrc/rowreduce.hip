@@ -462,3 +462,23 @@ __device__ __forceinline__ void rr_loop_body(const RowArgs& a) {
 G950_RR_ALL(softmax, g950::ROW_SOFTMAX)
 G950_RR_ALL(rmsnorm, g950::ROW_RMSNORM)
 G950_RR_ALL(layernorm, g950::ROW_LAYERNORM)
+
+// ------------------------------------------------------------- stream copy
+// y = x for n 16-byte vectors, grid-stride, nontemporal loads and stores --
+// the same memory path as the row kernels.  It is the calibration kernel for
+// the HBM traffic counters (its bytes are known exactly) and a plain copy op.
+extern "C" __global__ __launch_bounds__(256) void g950_stream_copy(const g950::CopyArgs a) {
+  using g950::u32x4;
+  const u32x4* x = (const u32x4*)a.x;
+  u32x4* y = (u32x4*)a.y;
+  const long long stride = (long long)gridDim.x * 256 * 4;
+  for (long long i = (long long)blockIdx.x * 256 * 4 + threadIdx.x; i < a.n16; i += stride) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i + u * 256 < a.n16) v[u] = __builtin_nontemporal_load(x + i + u * 256);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i + u * 256 < a.n16) __builtin_nontemporal_store(v[u], y + i + u * 256);
+  }
+}

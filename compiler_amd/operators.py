@@ -107,6 +107,12 @@ def attn_fwd_causal_kernel(q_ptr, k_ptr, v_ptr, out_ptr, Z, H, N_CTX, scale,
     return _launch(op, tensors, outputs, scalars, stream, sync, prepare)
 
 
+def stream_copy(x, y, *, stream=None, sync=False, prepare=False):
+    """y = x through the streaming-copy kernel (nontemporal 16-byte loads and
+    stores, the row kernels' memory path); used to calibrate HBM counters."""
+    return _launch(rt.OP_COPY, {"x": x, "y": y}, {"y"}, {}, stream, sync, prepare)
+
+
 # ------------------------------------------------------ tensor conveniences
 def softmax(x, out=None, **kw):
     import torch

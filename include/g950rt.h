@@ -107,6 +107,11 @@ typedef struct g950_scalar {
  *                      (ops/suite/dev/flash_varlen_fwd_kernel.py:309,318-320)
  *   views   k_ptr, lse_ptr f32[Z,H,S], out_ptr, q_ptr, v_ptr
  *   scalars as G950_OP_ATTENTION
+ * G950_OP_COPY         y = x, contiguous, 16-byte multiple (no reference
+ *                      counterpart: the streaming-copy kernel that calibrates
+ *                      the HBM traffic counters; same load/store path as the
+ *                      row kernels)
+ *   views   x, y
  */
 enum g950_op {
   G950_OP_SOFTMAX = 1,
@@ -116,7 +121,8 @@ enum g950_op {
   G950_OP_MATMUL_I8 = 5,
   G950_OP_MATMUL_I8_DEQUANT = 6,
   G950_OP_ATTENTION = 7,
-  G950_OP_ATTENTION_LSE = 8
+  G950_OP_ATTENTION_LSE = 8,
+  G950_OP_COPY = 9
 };
 
 typedef struct g950_module g950_module;

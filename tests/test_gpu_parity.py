@@ -89,6 +89,14 @@ def test_reduction_tail_guard_untouched():
     close(host(y), ref.softmax(c["x"]), 1e-2, 1e-2)
 
 
+def test_stream_copy_exact():
+    x = torch.randn(8191 * 3000, device=DEV).to(torch.bfloat16)
+    y = torch.empty_like(x)
+    ops.stream_copy(x, y, sync=True)
+    assert rt.module().last_kernel == "g950_stream_copy"
+    assert torch.equal(x, y)
+
+
 @pytest.mark.parametrize("case", golden_cases("softmax"))
 def test_softmax_reference_fixture(case):
     b = load(case)
