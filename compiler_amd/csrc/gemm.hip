@@ -8,41 +8,43 @@
 // (per-column scale), here with the per-row A scale as well:
 // Y[m,n] = bf16(float(acc[m,n]) * sa[m] * sb[n]).
 //
-// Fast kernel (g950_gemm_*_256x256): both operands K-contiguous (A row-major
+// MFMA kernel (g950_gemm_*_256x256): both operands K-contiguous (A row-major
 // [M,K]; B stored as Bt[N,K], i.e. column-major [K,N]).
-//   * workgroup tile 256x256, 8 waves (4 x 2), wave tile 64 x 128
-//   * K slab of 128 bytes per row (64 bf16 / 128 int8) per stage, two LDS
-//     stages (2 x 64 KiB), filled by direct global->LDS 16-byte DMA loads
-//     (global_load_lds_dwordx4), so the next slab streams in while MFMAs run
-//     on the current one
-//   * LDS rows are 128 B; the eight 16-byte chunks of a row are XOR-swizzled
-//     with (row>>1)&7 so the 32 rows an MFMA operand read touches spread over
-//     all 64 banks
-//   * MFMA v_mfma_f32_32x32x16_{bf16,f16} / v_mfma_i32_32x32x32_i8; the B tile
-//     feeds the MFMA A port so each lane ends with four consecutive output
-//     columns of one output row (8-byte bf16 stores)
+//   * workgroup tile 256x256, 8 waves (4 x 2, two per SIMD), wave tile
+//     64 x 128 = 2 x 4 fragments of v_mfma_f32_32x32x16_{bf16,f16} /
+//     v_mfma_i32_32x32x32_i8; the B tile feeds the MFMA A port so each lane
+//     ends with four consecutive output columns of one output row
+//   * K in slabs of 64 bytes per row (32 bf16 / 64 int8); a ring of five LDS
+//     stages of 32 KiB (A rows then B rows, 64-byte rows), filled by direct
+//     global->LDS 16-byte DMA (global_load_lds_dwordx4): a slab's load is
+//     issued about three slabs of compute before it is read
+//   * the four 16-byte chunks of a 64-byte LDS row are XOR-swizzled with
+//     (row >> 2) & 3, so the 16 rows one phase of an MFMA operand read
+//     touches cover all 64 banks
+//   * per slab: two k-steps; each k-step's MFMAs run with the next k-step's
+//     fragment reads (second register set) and half of a later slab's DMA
+//     spread between them (sched_group_barrier), so no wave stalls issuing a
+//     burst of LDS reads or DMA while its MFMAs wait behind it; one workgroup
+//     barrier per slab, between its two k-steps
 //   * XCD-aware block order: consecutive tiles go to the same XCD (the
 //     hardware deals workgroups round-robin over 8 XCDs), grouped 8 tile-rows
 //     deep for L2 reuse
 //   * M/N edges: loads clamp the row index (the duplicated rows only feed
 //     output rows/cols that are never stored); stores are masked.  K must be a
-//     multiple of the slab (host checks), otherwise the general kernel runs.
+//     whole number of slabs (host checks), otherwise the general kernel runs.
 //
 // General kernel (g950_gemm_general): any strides, any K, fp32/fp16/bf16
 // inputs (fp32 FMA) or int8 (int32 exact); 64x64 tiles.  It serves the
-// reference's row-major-B fixtures and shapes the fast kernel refuses.
+// reference's row-major-B fixtures and shapes the MFMA kernel refuses.
 #include "g950_common.h"
 
 namespace g950 {
 
 enum GemmMode : int { GEMM_BF16 = 0, GEMM_F16 = 1, GEMM_I8 = 2 };
 
-
-
-constexpr int BM = 256, BN = 256, SLAB = 128;  // SLAB: bytes of K per row per stage
-constexpr int STAGE_BYTES = (BM + BN) * SLAB;    // 64 KiB
-
-__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+constexpr int BM = 256, BN = 256;  // workgroup tile
+constexpr int SLAB = 64;           // bytes of K per row per LDS stage
+constexpr int STAGES = 5;          // LDS ring depth (5 x 32 KiB)
 
 // Map the linear workgroup id to a (tile_m, tile_n): XCD-contiguous, then
 // grouped by 8 tile-rows.
@@ -59,155 +61,17 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& 
   tn = in / gsize;
 }
 
-// One wave-instruction of the slab load: 8 rows x 128 B = 1 KiB of LDS.
-__device__ __forceinline__ void dma_rows(const char* gbase, long long ld_bytes, int row0,
-                                         int row_limit, long long kbyte, char* lds_rows,
-                                         int lane) {
-  const int r = lane >> 3;
-  const int slot = lane & 7;
-  const int row = row0 + r;                       // row within the tile
-  const int grow = min(row, row_limit);           // clamped global row (relative)
-  const int chunk = slot ^ swz(row);
-  const char* src = gbase + (long long)grow * ld_bytes + kbyte + chunk * 16;
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                   (__attribute__((address_space(3))) void*)lds_rows, 16, 0, 0);
-}
-
-template <int MODE>
-__device__ __forceinline__ void mfma_step(const u32x4& bfrag, const u32x4& afrag, f32x16& accf,
-                                          i32x16& acci) {
-  if constexpr (MODE == GEMM_BF16) {
-    accf = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, bfrag),
-                                                   __builtin_bit_cast(bf16x8, afrag), accf, 0, 0, 0);
-  } else if constexpr (MODE == GEMM_F16) {
-    accf = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bfrag),
-                                                  __builtin_bit_cast(f16x8, afrag), accf, 0, 0, 0);
-  } else {
-    acci = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bfrag),
-                                                 __builtin_bit_cast(i32x4, afrag), acci, 0, 0, 0);
-  }
-}
-
-// WM x WN waves; wave tile (BM/WM) x (BN/WN) = FM x FN fragments of 32x32.
-// SCHED selects the in-slab instruction schedule:
-//   0  read a k-step's fragments, then its MFMAs
-//   1  fragments of k-step ks+1 read (second register set) before the MFMAs of ks
-//   2  as 1, with the LDS reads interleaved one-by-one between the MFMAs
-//   3  as 2, with the wave's issue priority raised while its MFMAs issue
-//   4  as 0, with the priority raise
-template <int MODE, int WM, int WN, int SCHED = 0>
-__device__ __forceinline__ void gemm_fast_body(const GemmArgs& p) {
-  constexpr int NW = WM * WN;
-  constexpr int FM = BM / WM / 32;
-  constexpr int FN = BN / WN / 32;
-  constexpr int GROUPS = (BM + BN) / 8 / NW;  // 8-row DMA groups per wave per slab
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE_BYTES];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / WN;
-  const int wn = wave % WN;
-  int tm, tn;
-  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
-  const int m0 = tm * BM;
-  const int n0 = tn * BN;
-  constexpr int ES = (MODE == GEMM_I8) ? 1 : 2;  // element bytes
-  const long long lda_b = p.a_s0 * ES;
-  const long long ldb_b = p.b_s0 * ES;  // Bt row stride (n) in bytes
-  const char* abase = (const char*)p.a + (long long)m0 * lda_b;
-  const char* bbase = (const char*)p.b + (long long)n0 * ldb_b;
-  const int a_lim = p.M - 1 - m0;
-  const int b_lim = p.N - 1 - n0;
-  const int kslabs = (p.K * ES) / SLAB;
-
-  f32x16 accf[FM][FN];
-  i32x16 acci[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      if constexpr (MODE == GEMM_I8) acci[i][j] = (i32x16){};
-      else accf[i][j] = (f32x16){};
-    }
-
-  // slab loads: row groups 0..31 are A rows, 32..63 are B rows
-  auto issue = [&](int stage, int slab) {
-    char* sa = lds + stage * STAGE_BYTES;
-    const long long kb = (long long)slab * SLAB;
-#pragma unroll
-    for (int t = 0; t < GROUPS; ++t) {
-      const int rg = wave * GROUPS + t;
-      if (rg < BM / 8) dma_rows(abase, lda_b, rg * 8, a_lim, kb, sa + rg * 1024, lane);
-      else dma_rows(bbase, ldb_b, (rg - BM / 8) * 8, b_lim, kb, sa + rg * 1024, lane);
-    }
-  };
-
-  const int g = lane >> 5;
-  const int r = lane & 31;
-  u32x4 af[2][FM], bfr[2][FN];
-  auto frags = [&](const char* sa, int ks, int buf) {
-    const char* sb = sa + BM * SLAB;
-    const int chunk = ks * 2 + g;
-#pragma unroll
-    for (int mi = 0; mi < FM; ++mi) {
-      const int row = wm * (BM / WM) + mi * 32 + r;
-      af[buf][mi] = *(const u32x4*)(sa + row * SLAB + ((chunk ^ swz(row)) << 4));
-    }
-#pragma unroll
-    for (int ni = 0; ni < FN; ++ni) {
-      const int row = wn * (BN / WN) + ni * 32 + r;
-      bfr[buf][ni] = *(const u32x4*)(sb + row * SLAB + ((chunk ^ swz(row)) << 4));
-    }
-  };
-
-  issue(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-
-  constexpr bool DB = (SCHED == 1 || SCHED == 2 || SCHED == 3);
-  constexpr bool PRIO = (SCHED == 3 || SCHED == 4);
-  for (int kt = 0; kt < kslabs; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < kslabs) issue(cur ^ 1, kt + 1);
-    const char* sa = lds + cur * STAGE_BYTES;
-    if constexpr (DB) frags(sa, 0, 0);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int buf = DB ? (ks & 1) : 0;
-      if constexpr (DB) {
-        // fragments of the next k-step are read while this step's MFMAs run
-        if (ks + 1 < 4) frags(sa, ks + 1, (ks + 1) & 1);
-      } else {
-        frags(sa, ks, 0);
-      }
-      if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int mi = 0; mi < FM; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < FN; ++ni)
-          mfma_step<MODE>(bfr[buf][ni], af[buf][mi], accf[mi][ni], acci[mi][ni]);
-      if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
-      if constexpr (SCHED == 2 || SCHED == 3) {
-        if (ks + 1 < 4) {
-#pragma unroll
-          for (int i = 0; i < FM + FN; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-          }
-          __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + FN), 0);
-        }
-      }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-  }
-
-  // Epilogue: lane holds C[m][n..n+3] for m = row r of each 32-row fragment,
-  // n = 8q + 4g + {0..3} of each 32-column fragment.
+// Epilogue: lane holds C[m][n..n+3] for m = row r of each 32-row fragment,
+// n = 8q + 4g + {0..3} of each 32-column fragment; (wm0, wn0) is the first
+// output row / column of the wave's tile.
+template <int MODE, int FM, int FN>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&accf)[FM][FN],
+                                              const i32x16 (&acci)[FM][FN], int wm0, int wn0,
+                                              int r, int g) {
   const bool vec_ok = ((p.c_s0 & 3) == 0);
 #pragma unroll
   for (int mi = 0; mi < FM; ++mi) {
-    const int m = m0 + wm * (BM / WM) + mi * 32 + r;
+    const int m = wm0 + mi * 32 + r;
     if (m >= p.M) continue;
     float rs = 1.0f;
     if constexpr (MODE == GEMM_I8) rs = p.sa ? p.sa[m] : 1.0f;
@@ -215,7 +79,7 @@ __device__ __forceinline__ void gemm_fast_body(const GemmArgs& p) {
     for (int ni = 0; ni < FN; ++ni) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * (BN / WN) + ni * 32 + q * 8 + g * 4;
+        const int n = wn0 + ni * 32 + q * 8 + g * 4;
         float v[4];
         if constexpr (MODE == GEMM_I8) {
           int iv[4];
@@ -268,6 +132,163 @@ __device__ __forceinline__ void gemm_fast_body(const GemmArgs& p) {
       }
     }
   }
+}
+
+template <int MODE>
+__device__ __forceinline__ void mfma_step(const u32x4& bfrag, const u32x4& afrag, f32x16& accf,
+                                          i32x16& acci) {
+  if constexpr (MODE == GEMM_BF16) {
+    accf = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, bfrag),
+                                                   __builtin_bit_cast(bf16x8, afrag), accf, 0, 0, 0);
+  } else if constexpr (MODE == GEMM_F16) {
+    accf = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, bfrag),
+                                                  __builtin_bit_cast(f16x8, afrag), accf, 0, 0, 0);
+  } else {
+    acci = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, bfrag),
+                                                 __builtin_bit_cast(i32x4, afrag), acci, 0, 0, 0);
+  }
+}
+
+// WM x WN waves; wave tile (BM/WM) x (BN/WN) = FM x FN fragments of 32x32.
+template <int MODE, int WM, int WN>
+__device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
+  constexpr int NW = WM * WN;
+  constexpr int FM = BM / WM / 32;
+  constexpr int FN = BN / WN / 32;
+  constexpr int STAGE = (BM + BN) * SLAB;      // 32 KiB
+  constexpr int GROUPS = (BM + BN) / 16 / NW;  // 16-row DMA groups per wave per slab
+  static_assert(GROUPS * 16 * NW == BM + BN && GROUPS % 2 == 0, "DMA split over waves and halves");
+  __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+  constexpr int ES = (MODE == GEMM_I8) ? 1 : 2;  // element bytes
+  const long long lda_b = p.a_s0 * ES;
+  const long long ldb_b = p.b_s0 * ES;  // Bt row stride (n) in bytes
+  const char* abase = (const char*)p.a + (long long)m0 * lda_b;
+  const char* bbase = (const char*)p.b + (long long)n0 * ldb_b;
+  const int a_lim = p.M - 1 - m0;
+  const int b_lim = p.N - 1 - n0;
+  const int kslabs = (p.K * ES) / SLAB;
+  const int last = kslabs - 1;
+
+  f32x16 accf[FM][FN];
+  i32x16 acci[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (MODE == GEMM_I8) acci[i][j] = (i32x16){};
+      else accf[i][j] = (f32x16){};
+    }
+
+  // DMA: one wave instruction moves 16 rows x 64 bytes (lane: row lane / 4,
+  // 16-byte slot lane % 4, which holds the swizzled chunk).  Row groups
+  // 0..BM/16-1 are A rows, the rest B rows; wave w owns groups
+  // w*GROUPS .. w*GROUPS+GROUPS-1, issued in two halves.
+  const int dr = lane >> 2;
+  const int dslot = lane & 3;
+  auto issue = [&](int stage, int slab, int t0, int t1) {
+    char* st = lds + stage * STAGE;
+    const long long kb = (long long)slab * SLAB;
+#pragma unroll
+    for (int t = t0; t < t1; ++t) {
+      const int rg = wave * GROUPS + t;
+      const bool is_a = rg < BM / 16;
+      const int row = (is_a ? rg : rg - BM / 16) * 16 + dr;
+      const int grow = min(row, is_a ? a_lim : b_lim);
+      const int chunk = dslot ^ ((row >> 2) & 3);
+      const char* src = (is_a ? abase : bbase) + (long long)grow * (is_a ? lda_b : ldb_b) + kb +
+                        chunk * 16;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(st + rg * 1024),
+                                       16, 0, 0);
+    }
+  };
+
+  // Fragments of k-step ks (16 bf16 / 32 int8 of K) of one stage: lane
+  // (g, r) reads 16 bytes of row r of each 32-row fragment, chunk 2 ks + g.
+  const int g = lane >> 5;
+  const int r = lane & 31;
+  u32x4 af[2][FM], bfr[2][FN];
+  auto frags = [&](const char* st, int ks, int buf) {
+    const char* sb = st + BM * SLAB;
+    const int chunk = ks * 2 + g;
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi) {
+      const int row = wm * (BM / WM) + mi * 32 + r;
+      af[buf][mi] = *(const u32x4*)(st + row * SLAB + ((chunk ^ ((row >> 2) & 3)) << 4));
+    }
+#pragma unroll
+    for (int ni = 0; ni < FN; ++ni) {
+      const int row = wn * (BN / WN) + ni * 32 + r;
+      bfr[buf][ni] = *(const u32x4*)(sb + row * SLAB + ((chunk ^ ((row >> 2) & 3)) << 4));
+    }
+  };
+  auto mfmas = [&](int buf) {
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < FN; ++ni)
+        mfma_step<MODE>(bfr[buf][ni], af[buf][mi], accf[mi][ni], acci[mi][ni]);
+  };
+  // one MFMA, then one LDS read (FM + FN of them), then one DMA (GROUPS / 2)
+  auto interleave = [&]() {
+#pragma unroll
+    for (int i = 0; i < FM * FN; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i < FM + FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i < GROUPS / 2) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+    }
+  };
+
+  // Ring protocol.  Iteration kt consumes slab kt from stage kt % STAGES and
+  // refills the stage slab kt - 1 left (every wave finished reading it before
+  // the barrier of iteration kt - 1) with slab kt + STAGES - 1, half before and
+  // half after its barrier.  At that barrier slab kt + 1 must have landed:
+  // each wave then has slabs kt + 2 .. kt + STAGES - 2 and the first half of
+  // slab kt + STAGES - 1 in flight.  Past the end of K the DMA re-reads the
+  // last slab into a stage nobody reads again, so the counts never change and
+  // the loop body has no branch.  The compiler cannot count LDS reads issued
+  // behind a DMA, so every LDS-read wait it must see is an explicit
+  // lgkmcnt(0) at a point where the reads are long done.
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) issue(s, min(s, last), 0, GROUPS);
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((STAGES - 2) * GROUPS) : "memory");
+  frags(lds, 0, 0);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  int cur = 0;
+  for (int kt = 0; kt < kslabs; ++kt) {
+    const char* st = lds + cur * STAGE;
+    const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
+    const int prv = cur == 0 ? STAGES - 1 : cur - 1;
+    const int fill = min(kt + STAGES - 1, last);
+    issue(prv, fill, 0, GROUPS / 2);
+    frags(st, 1, 1);
+    mfmas(0);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // this slab's reads done
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((STAGES - 3) * GROUPS + GROUPS / 2)
+                 : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    issue(prv, fill, GROUPS / 2, GROUPS);
+    frags(lds + nxt * STAGE, 0, 0);  // (after the last slab: a stale stage, never used)
+    mfmas(1);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    cur = nxt;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  gemm_epilogue<MODE, FM, FN>(p, accf, acci, m0 + wm * (BM / WM), n0 + wn * (BN / WN), r, g);
 }
 
 // ------------------------------------------------------------ general GEMM
@@ -336,15 +357,13 @@ __device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
 
 }  // namespace g950
 
-#define G950_GEMM_FAST(NAME, MODE, WM, WN, SCHED)                                           \
+#define G950_GEMM_MFMA(NAME, MODE, WM, WN)                                                   \
   extern "C" __global__ __launch_bounds__(WM * WN * 64) void NAME(const g950::GemmArgs p) {  \
-    g950::gemm_fast_body<MODE, WM, WN, SCHED>(p);                                          \
+    g950::gemm_mfma_body<MODE, WM, WN>(p);                                                 \
   }
-// measured on MI355X (8192^3 bf16, 4096x8192x8192 int8): 4 x 2 waves of
-// 64 x 128 tiles; interleaved fragment reads for the 16-bit kernels
-G950_GEMM_FAST(g950_gemm_bf16_256x256, g950::GEMM_BF16, 4, 2, 2)
-G950_GEMM_FAST(g950_gemm_f16_256x256, g950::GEMM_F16, 4, 2, 2)
-G950_GEMM_FAST(g950_gemm_i8_256x256, g950::GEMM_I8, 4, 2, 0)
+G950_GEMM_MFMA(g950_gemm_bf16_256x256, g950::GEMM_BF16, 4, 2)
+G950_GEMM_MFMA(g950_gemm_f16_256x256, g950::GEMM_F16, 4, 2)
+G950_GEMM_MFMA(g950_gemm_i8_256x256, g950::GEMM_I8, 4, 2)
 extern "C" __global__ __launch_bounds__(256) void g950_gemm_general(const g950::GemmArgs p) {
   g950::gemm_general_body<false>(p);
 }
