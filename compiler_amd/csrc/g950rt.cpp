@@ -356,9 +356,9 @@ int gemm_tiles(GemmArgs& g) {
 }
 
 // A[M,K] and B[K,N] both K-contiguous, 16-byte rows, K a whole number of
-// 64-byte slabs: the MFMA kernel applies.
+// 128-byte slabs: the MFMA kernel applies.
 bool gemm_fast_ok(const View& a, const View& b, int K, int esz) {
-  return a.stride[1] == 1 && b.stride[0] == 1 && (K * esz) % 64 == 0 && K > 0 &&
+  return a.stride[1] == 1 && b.stride[0] == 1 && (K * esz) % 128 == 0 && K > 0 &&
          aligned16(a.addr()) && aligned16(b.addr()) && (a.stride[0] * esz) % 16 == 0 &&
          (b.stride[1] * esz) % 16 == 0 && a.shape[0] > 0 && b.shape[1] > 0;
 }

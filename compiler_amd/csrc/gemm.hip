@@ -14,21 +14,22 @@
 //     64 x 128 = 2 x 4 fragments of v_mfma_f32_32x32x16_{bf16,f16} /
 //     v_mfma_i32_32x32x32_i8; the B tile feeds the MFMA A port so each lane
 //     ends with four consecutive output columns of one output row
-//   * K in slabs of 64 bytes per row (32 bf16 / 64 int8); a ring of five LDS
-//     stages of 32 KiB (A rows then B rows, 64-byte rows), filled by direct
-//     global->LDS 16-byte DMA (global_load_lds_dwordx4): a slab's load is
-//     issued about three slabs of compute before it is read
-//   * the four 16-byte chunks of a 64-byte LDS row are XOR-swizzled with
-//     (row >> 2) & 3, so the 16 rows one phase of an MFMA operand read
-//     touches cover all 64 banks
-//   * per slab: two k-steps; each k-step's MFMAs run with the next k-step's
-//     fragment reads (second register set) and half of a later slab's DMA
-//     spread between them (sched_group_barrier), so no wave stalls issuing a
-//     burst of LDS reads or DMA while its MFMAs wait behind it; one workgroup
-//     barrier per slab, between its two k-steps
+//   * K in slabs of 128 bytes per row (64 bf16 / 128 int8); two LDS stages
+//     of 64 KiB (A rows then B rows, 128-byte rows), filled by direct
+//     global->LDS 16-byte DMA (global_load_lds_dwordx4) of whole 128-byte
+//     lines (measured on MI355X: 64-byte row pieces cost the load path 1.5x
+//     per byte)
+//   * the eight 16-byte chunks of a 128-byte LDS row are XOR-swizzled with
+//     (row >> 1) & 7, so the 32 rows an MFMA operand read touches spread over
+//     all 64 banks
+//   * per slab: four k-steps; each k-step's MFMAs run with the next k-step's
+//     fragment reads (second register set) spread between them, and the
+//     slab's DMA is spread over k-step 3 of the previous slab and k-step 0
+//     (sched_group_barrier), so no wave stalls issuing a burst of loads while
+//     its MFMAs wait behind it; one workgroup barrier per slab, before k-step 3
 //   * XCD-aware block order: consecutive tiles go to the same XCD (the
-//     hardware deals workgroups round-robin over 8 XCDs), grouped 8 tile-rows
-//     deep for L2 reuse
+//     hardware deals workgroups round-robin over 8 XCDs), grouped 4 tile-rows
+//     deep for L2 reuse (4 beat 2, 8, 16 and 32 at 8192^3)
 //   * M/N edges: loads clamp the row index (the duplicated rows only feed
 //     output rows/cols that are never stored); stores are masked.  K must be a
 //     whole number of slabs (host checks), otherwise the general kernel runs.
@@ -43,15 +44,14 @@ namespace g950 {
 enum GemmMode : int { GEMM_BF16 = 0, GEMM_F16 = 1, GEMM_I8 = 2 };
 
 constexpr int BM = 256, BN = 256;  // workgroup tile
-constexpr int SLAB = 64;           // bytes of K per row per LDS stage
-constexpr int STAGES = 5;          // LDS ring depth (5 x 32 KiB)
+constexpr int SLAB = 128;          // bytes of K per row per LDS stage (two stages)
 
 // Map the linear workgroup id to a (tile_m, tile_n): XCD-contiguous, then
-// grouped by 8 tile-rows.
+// grouped by 4 tile-rows.
 __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
   if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
-  const int group = 8;
+  const int group = 4;
   const int per_group = group * tiles_n;
   const int gid = pid / per_group;
   const int first = gid * group;
@@ -155,10 +155,11 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   constexpr int NW = WM * WN;
   constexpr int FM = BM / WM / 32;
   constexpr int FN = BN / WN / 32;
-  constexpr int STAGE = (BM + BN) * SLAB;      // 32 KiB
-  constexpr int GROUPS = (BM + BN) / 16 / NW;  // 16-row DMA groups per wave per slab
-  static_assert(GROUPS * 16 * NW == BM + BN && GROUPS % 2 == 0, "DMA split over waves and halves");
-  __shared__ __attribute__((aligned(1024))) char lds[STAGES * STAGE];
+  constexpr int STAGE = (BM + BN) * SLAB;     // 64 KiB
+  constexpr int GROUPS = (BM + BN) / 8 / NW;  // 8-row DMA groups per wave per slab
+  constexpr int H = GROUPS / 2;
+  static_assert(GROUPS * 8 * NW == BM + BN && GROUPS % 2 == 0, "DMA split over waves and halves");
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -188,22 +189,22 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
       else accf[i][j] = (f32x16){};
     }
 
-  // DMA: one wave instruction moves 16 rows x 64 bytes (lane: row lane / 4,
-  // 16-byte slot lane % 4, which holds the swizzled chunk).  Row groups
-  // 0..BM/16-1 are A rows, the rest B rows; wave w owns groups
+  // DMA: one wave instruction moves 8 rows x 128 bytes (lane: row lane / 8,
+  // 16-byte slot lane % 8, which holds the swizzled chunk).  Row groups
+  // 0..BM/8-1 are A rows, the rest B rows; wave w owns groups
   // w*GROUPS .. w*GROUPS+GROUPS-1, issued in two halves.
-  const int dr = lane >> 2;
-  const int dslot = lane & 3;
+  const int dr = lane >> 3;
+  const int dslot = lane & 7;
   auto issue = [&](int stage, int slab, int t0, int t1) {
     char* st = lds + stage * STAGE;
     const long long kb = (long long)slab * SLAB;
 #pragma unroll
     for (int t = t0; t < t1; ++t) {
       const int rg = wave * GROUPS + t;
-      const bool is_a = rg < BM / 16;
-      const int row = (is_a ? rg : rg - BM / 16) * 16 + dr;
+      const bool is_a = rg < BM / 8;
+      const int row = (is_a ? rg : rg - BM / 8) * 8 + dr;
       const int grow = min(row, is_a ? a_lim : b_lim);
-      const int chunk = dslot ^ ((row >> 2) & 3);
+      const int chunk = dslot ^ ((row >> 1) & 7);
       const char* src = (is_a ? abase : bbase) + (long long)grow * (is_a ? lda_b : ldb_b) + kb +
                         chunk * 16;
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
@@ -223,12 +224,12 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
 #pragma unroll
     for (int mi = 0; mi < FM; ++mi) {
       const int row = wm * (BM / WM) + mi * 32 + r;
-      af[buf][mi] = *(const u32x4*)(st + row * SLAB + ((chunk ^ ((row >> 2) & 3)) << 4));
+      af[buf][mi] = *(const u32x4*)(st + row * SLAB + ((chunk ^ ((row >> 1) & 7)) << 4));
     }
 #pragma unroll
     for (int ni = 0; ni < FN; ++ni) {
       const int row = wn * (BN / WN) + ni * 32 + r;
-      bfr[buf][ni] = *(const u32x4*)(sb + row * SLAB + ((chunk ^ ((row >> 2) & 3)) << 4));
+      bfr[buf][ni] = *(const u32x4*)(sb + row * SLAB + ((chunk ^ ((row >> 1) & 7)) << 4));
     }
   };
   auto mfmas = [&](int buf) {
@@ -238,52 +239,53 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
       for (int ni = 0; ni < FN; ++ni)
         mfma_step<MODE>(bfr[buf][ni], af[buf][mi], accf[mi][ni], acci[mi][ni]);
   };
-  // one MFMA, then one LDS read (FM + FN of them), then one DMA (GROUPS / 2)
-  auto interleave = [&]() {
+  // One MFMA per slot; the next k-step's LDS reads in the first FM + FN
+  // slots; ndma DMA instructions spread evenly over the slots.  The compiler
+  // cannot count LDS reads issued behind a DMA, so each k-step ends with an
+  // explicit lgkmcnt(0), by when its reads are long done.
+  auto kstep = [&](int buf, int ndma) {
+    mfmas(buf);
 #pragma unroll
     for (int i = 0; i < FM * FN; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       if (i < FM + FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (i < GROUPS / 2) __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+      if (ndma && i % ((FM * FN) / ndma) == 0 && i / ((FM * FN) / ndma) < ndma)
+        __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
   };
 
-  // Ring protocol.  Iteration kt consumes slab kt from stage kt % STAGES and
-  // refills the stage slab kt - 1 left (every wave finished reading it before
-  // the barrier of iteration kt - 1) with slab kt + STAGES - 1, half before and
-  // half after its barrier.  At that barrier slab kt + 1 must have landed:
-  // each wave then has slabs kt + 2 .. kt + STAGES - 2 and the first half of
-  // slab kt + STAGES - 1 in flight.  Past the end of K the DMA re-reads the
-  // last slab into a stage nobody reads again, so the counts never change and
-  // the loop body has no branch.  The compiler cannot count LDS reads issued
-  // behind a DMA, so every LDS-read wait it must see is an explicit
-  // lgkmcnt(0) at a point where the reads are long done.
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) issue(s, min(s, last), 0, GROUPS);
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((STAGES - 2) * GROUPS) : "memory");
+  // Two-stage protocol.  Iteration kt consumes slab kt from stage kt % 2.
+  // Slab kt + 1 goes to the other stage: its first DMA half in k-step 3 of
+  // iteration kt - 1, its second half in k-step 0 of iteration kt, both past
+  // the barrier after which nobody reads slab kt - 1 again.  The barrier
+  // before k-step 3 comes after every read of slab kt (the k-step 3
+  // fragments are read during k-step 2) and after this wave's DMAs of slab
+  // kt + 1 have landed; k-step 3 then reads slab kt + 1's first fragments.
+  // Past the end of K the DMA re-reads the last slab into a stage nobody
+  // reads again, so the loop body has no branch.
+  issue(0, 0, 0, GROUPS);
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   frags(lds, 0, 0);
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  issue(1, min(1, last), 0, H);
+  __builtin_amdgcn_s_waitcnt(0xc07f);
   int cur = 0;
   for (int kt = 0; kt < kslabs; ++kt) {
     const char* st = lds + cur * STAGE;
-    const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
-    const int prv = cur == 0 ? STAGES - 1 : cur - 1;
-    const int fill = min(kt + STAGES - 1, last);
-    issue(prv, fill, 0, GROUPS / 2);
+    const int nxt = cur ^ 1;
+    issue(nxt, min(kt + 1, last), H, GROUPS);
     frags(st, 1, 1);
-    mfmas(0);
-    interleave();
+    kstep(0, H);
+    frags(st, 2, 0);
+    kstep(1, 0);
+    frags(st, 3, 1);
+    kstep(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // this slab's reads done
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((STAGES - 3) * GROUPS + GROUPS / 2)
-                 : "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    issue(prv, fill, GROUPS / 2, GROUPS);
+    issue(cur, min(kt + 2, last), 0, H);
     frags(lds + nxt * STAGE, 0, 0);  // (after the last slab: a stale stage, never used)
-    mfmas(1);
-    interleave();
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xc07f);
+    kstep(1, H);
     cur = nxt;
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

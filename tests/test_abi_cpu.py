@@ -160,8 +160,8 @@ def gemm_args(m, n, k, dtype, col_major_b=True, out=rt.DT_BF16):
     (8192, 8192, 8192, True, "g950_gemm_bf16_256x256"),
     (4097, 11008, 4096, True, "g950_gemm_bf16_256x256"),
     (128, 128, 128, False, "g950_gemm_general"),   # row-major B (the corpus fixtures)
-    (64, 64, 72, True, "g950_gemm_general"),       # K not a whole 32-element (64-byte) slab
-    (33, 65, 32, True, "g950_gemm_bf16_256x256"),  # a single slab
+    (64, 64, 96, True, "g950_gemm_general"),       # K not a whole 64-element (128-byte) slab
+    (33, 65, 64, True, "g950_gemm_bf16_256x256"),  # a single slab
 ])
 def test_matmul_selection(m, n, k, colb, kernel):
     rc, name, err = validate(rt.OP_MATMUL, gemm_args(m, n, k, rt.DT_BF16, colb), [k, m, n])

@@ -128,7 +128,7 @@ def test_rms_fixture_shapes_all_dtypes():
 
 # ------------------------------------------------------------------ GEMM
 @pytest.mark.parametrize("m,n,k", [(256, 256, 64), (300, 260, 256), (513, 1000, 1024), (1, 7, 64),
-                                   (33, 65, 32), (257, 129, 96)])
+                                   (33, 65, 64), (257, 129, 192)])
 def test_gemm_bf16_mfma(m, n, k):
     c = inputs.config3(m, n, k)
     y = ops.matmul(dev(c["a"], "bfloat16"), dev(c["bt"], "bfloat16").t(), sync=True)
@@ -185,8 +185,8 @@ def test_matmul_reference_fixture(case):
 
 
 # ------------------------------------------------------------------ int8
-@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (300, 200, 384), (4096, 8192, 8192), (64, 64, 64),
-                                   (300, 200, 192)])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (300, 200, 384), (4096, 8192, 8192), (64, 64, 128),
+                                   (300, 200, 256), (65, 33, 640)])
 def test_int8_gemm_exact_and_dequant(m, n, k):
     c = inputs.config5(m, n, k)
     a = torch.from_numpy(c["a"]).to(DEV)
