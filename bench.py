@@ -41,11 +41,28 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def event_time(torch, launch, iters, warmup):
+def warm(torch, launch, seconds):
+    """Launch repeatedly for about ``seconds`` of wall time: MI355X engine
+    clocks ramp over the first few hundred milliseconds of sustained load
+    (measured: 1.46 -> 1.86 GHz across four back-to-back 1 ms kernels), so a
+    handful of warmup launches under-reports a kernel's steady rate."""
+    import time
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(4):
+            launch(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
+def event_time(torch, launch, iters, warmup, warm_s=0.0):
     """Average ms per launch of ``launch(i)``: HIP events on the launch stream
     around a batch of back-to-back launches of prepared calls (whose host cost
     is well below the kernel time, so the queue never drains and the average
     is the kernel's own duration plus the inter-dispatch gap)."""
+    if warm_s > 0:
+        warm(torch, launch, warm_s)
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
@@ -94,7 +111,7 @@ def headline(torch, ops, args):
         sm(i)
 
     # per-kernel launch times (events around many launches of one kernel)
-    ln_ms = event_time(torch, ln, 200, 10)
+    ln_ms = event_time(torch, ln, 200, 10, warm_s=0.3)
     ln_kernel = ln_calls[0].kernel
     sm_ms = event_time(torch, sm, 200, 10)
     sm_kernel = sm_calls[0].kernel
@@ -192,7 +209,7 @@ def suite(torch, ops):
 
     for name, calls, nbytes in (("C1a rmsnorm fp32 [4096,4096]", rms_calls, rb),
                                 ("C1b softmax fp32 [4096,4096]", smx_calls, sb)):
-        ms = event_time(torch, lambda i: calls[i % ROTATE](), 200, 10)
+        ms = event_time(torch, lambda i: calls[i % ROTATE](), 200, 10, warm_s=0.3)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out.append({"config": name, "kernel": calls[0].kernel, "us": round(ms * 1e3, 2),
                     "value": round(gbs, 1), "unit": "GB/s", "bound": "hbm",
@@ -208,7 +225,7 @@ def suite(torch, ops):
         del c
         y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         call = ops.matmul_kernel(a, bt.t(), y, m, n, k, prepare=True)
-        ms = event_time(torch, lambda i: call(), 20, 3)
+        ms = event_time(torch, lambda i: call(), 20, 3, warm_s=0.5)
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         out.append({"config": f"C3 gemm bf16 {m}x{n}x{k}", "kernel": call.kernel,
                     "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
@@ -225,7 +242,7 @@ def suite(torch, ops):
     lse = torch.empty((4, 32, 4096), dtype=torch.float32, device=dev)
     call = ops.attn_fwd_causal_kernel(q, k, v, o, 4, 32, 4096, 1 / math.sqrt(128), *q.stride(), *k.stride(),
                                       *v.stride(), *o.stride(), CAUSAL=True, lse_ptr=lse, prepare=True)
-    ms = event_time(torch, lambda i: call(), 10, 2)
+    ms = event_time(torch, lambda i: call(), 10, 2, warm_s=0.5)
     flops = 4.0 * 4 * 32 * 128 * 4096 * 4096 / 2
     tf = flops / (ms * 1e-3) / 1e12
     out.append({"config": "C4 causal GQA attention bf16 (4,32/8,4096,128)", "kernel": call.kernel,
@@ -243,7 +260,7 @@ def suite(torch, ops):
     del c
     y = torch.empty((4096, 8192), dtype=torch.bfloat16, device=dev)
     call = ops.matmul_i8_dequant_kernel(a, bt.t(), sa, sbv, y, 4096, 8192, 8192, prepare=True)
-    ms = event_time(torch, lambda i: call(), 20, 3)
+    ms = event_time(torch, lambda i: call(), 20, 3, warm_s=0.5)
     tops = 2.0 * 4096 * 8192 * 8192 / (ms * 1e-3) / 1e12
     out.append({"config": "C5 int8 gemm 4096x8192x8192 + dequant", "kernel": call.kernel,
                 "us": round(ms * 1e3, 1), "value": round(tops, 1), "unit": "TOP/s", "bound": "mfma",
