@@ -271,6 +271,27 @@ int op_softmax(g950_module* m, const g950_view* views, uint32_t nviews, const g9
   return launch_rows(m, "softmax", a, x.v->dtype, x, y, nullptr, nullptr, stream);
 }
 
+int op_logsumexp(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+                 uint32_t nsc, void* stream) {
+  if (nviews != 2 || nsc != 1) return fail(G950_USAGE, "logsumexp: needs views (x_ptr, y_ptr), scalars (n_cols)");
+  View x, y;
+  if (int rc = check_view(views, 0, "x_ptr", 2, x, false)) return rc;
+  if (int rc = check_view(views, 1, "y_ptr", 1, y, true)) return rc;
+  if (!is_float(x.v->dtype) || !is_float(y.v->dtype))
+    return fail(G950_USAGE, "logsumexp: x/y dtypes %s/%s unsupported (float32, bfloat16, float16)",
+                dtname(x.v->dtype), dtname(y.v->dtype));
+  if (y.shape[0] != x.shape[0]) return fail(G950_USAGE, "logsumexp: y needs one entry per row");
+  if (int rc = expect_int(sc, 0, "n_cols", x.shape[1])) return rc;
+  RowArgs a{};
+  a.x = x.v->data;
+  a.x_row = x.stride[0]; a.y_row = x.stride[0];
+  a.stat0 = y.v->data; a.stat0_stride = y.stride[0]; a.stat_dtype = (int)y.v->dtype;
+  a.rows = (int)x.shape[0]; a.cols = (int)x.shape[1];
+  if (a.cols == 0) return fail(G950_USAGE, "logsumexp: empty row");
+  // no row output: x stands in for y in the vector-path alignment checks
+  return launch_rows(m, "logsumexp", a, x.v->dtype, x, x, nullptr, nullptr, stream);
+}
+
 int stat_view(const View& s, const View& x, const char* what) {
   if (!is_float(s.v->dtype)) return fail(G950_USAGE, "%s: dtype %s unsupported", what, dtname(s.v->dtype));
   if (s.shape[0] != x.shape[0]) return fail(G950_USAGE, "%s: needs one entry per row", what);
@@ -613,6 +634,7 @@ int dispatch(g950_module* m, uint32_t op, const g950_view* views, uint32_t nview
       case G950_OP_SOFTMAX: return op_softmax(m, views, nviews, scalars, nscalars, stream);
       case G950_OP_RMS_LAYERNORM: return op_rms(m, views, nviews, scalars, nscalars, stream);
       case G950_OP_LAYERNORM: return op_layernorm(m, views, nviews, scalars, nscalars, stream);
+      case G950_OP_LOGSUMEXP: return op_logsumexp(m, views, nviews, scalars, nscalars, stream);
       case G950_OP_MATMUL: return op_matmul(m, views, nviews, scalars, nscalars, stream);
       case G950_OP_MATMUL_I8: return op_matmul_i8(m, views, nviews, scalars, nscalars, false, stream);
       case G950_OP_MATMUL_I8_DEQUANT:

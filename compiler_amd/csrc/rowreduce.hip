@@ -27,7 +27,7 @@
 
 namespace g950 {
 
-enum RowOp : int { ROW_SOFTMAX = 0, ROW_RMSNORM = 1, ROW_LAYERNORM = 2 };
+enum RowOp : int { ROW_SOFTMAX = 0, ROW_RMSNORM = 1, ROW_LAYERNORM = 2, ROW_LOGSUMEXP = 3 };
 
 
 
@@ -182,6 +182,15 @@ __device__ __forceinline__ float row_exp(float x) {
   else return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
+// logsumexp of one row from its NaN-ignoring max m, sum s = sum(exp(x - m))
+// and NaN flag (ops/suite/perf/logsumexp.py kernel: a row with any NaN gives
+// NaN; an infinite max is returned as is; else m + log(s)).
+__device__ __forceinline__ float lse_finish(float m, float s, bool nan) {
+  if (nan) return __builtin_nanf("");
+  if (__builtin_fabsf(m) == __builtin_huge_valf()) return m;
+  return m + logf(s);
+}
+
 // Persistent register-resident row kernel.  Workgroup g handles rows
 // g, g + G, g + 2G, ... (the reference's persistent form
 // tl.range(pid, n_rows, num_progs), ops/suite/dev/layer_norm_forward_row.py);
@@ -199,7 +208,7 @@ __device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
 
   // parameters stay packed in registers (16-bit types: half the VGPRs)
   R wr[ITEMS], br[ITEMS];
-  if constexpr (OP != ROW_SOFTMAX) {
+  if constexpr (OP == ROW_RMSNORM || OP == ROW_LAYERNORM) {
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
       const int j = tid + i * BLOCK;
@@ -230,7 +239,7 @@ __device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
         if (j < nvec) nxt[i] = IO::load(xrow, (long long)j * VEC);
       }
     }
-    if constexpr (OP != ROW_SOFTMAX) {
+    if constexpr (OP == ROW_RMSNORM || OP == ROW_LAYERNORM) {
       // keep the decode of the packed parameters inside the loop: hoisting it
       // would hold them as fp32 for the whole kernel (twice the VGPRs)
 #pragma unroll
@@ -248,11 +257,34 @@ __device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
         IO::unpack(cur[i], v[i]);
       } else {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) v[i][e] = (OP == ROW_SOFTMAX) ? -__builtin_huge_valf() : 0.0f;
+        for (int e = 0; e < VEC; ++e)
+          v[i][e] = (OP == ROW_SOFTMAX || OP == ROW_LOGSUMEXP) ? -__builtin_huge_valf() : 0.0f;
       }
     }
 
-    if constexpr (OP == ROW_SOFTMAX) {
+    if constexpr (OP == ROW_LOGSUMEXP) {
+      // max ignores NaN (fmaxf), a separate flag carries it
+      float m = -__builtin_huge_valf(), nan = 0.0f;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          m = fmaxf(m, v[i][e]);
+          nan = (v[i][e] != v[i][e]) ? 1.0f : nan;
+        }
+      m = block_reduce<OpMax, BLOCK>(m, scratch);
+      nan = block_reduce<OpMax, BLOCK>(nan, scratch);
+      float s = 0.0f;
+      if (__builtin_fabsf(m) != __builtin_huge_valf()) {
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) s += row_exp<T>(v[i][e] - m);  // tail: exp(-inf) = 0
+      }
+      s = block_reduce<OpSum, BLOCK>(s, scratch);
+      if (tid == 0)
+        store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, lse_finish(m, s, nan != 0.0f));
+    } else if constexpr (OP == ROW_SOFTMAX) {
       float m = -__builtin_huge_valf();
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i)
@@ -353,7 +385,27 @@ __device__ __forceinline__ void rr_loop_body(const RowArgs& a) {
   const void* xrow = (const char*)a.x + (long long)row * a.x_row * (long long)sizeof(T);
   void* yrow = (char*)a.y + (long long)row * a.y_row * (long long)sizeof(T);
   float xv;
-  if constexpr (OP == ROW_SOFTMAX) {
+  if constexpr (OP == ROW_LOGSUMEXP) {
+    float m = -__builtin_huge_valf(), z = 0.0f, nan = 0.0f;
+    for (int j = tid; j < n; j += BLOCK) {
+      load_vec<T, 1>(xrow, j, &xv);
+      if (xv != xv) {
+        nan = 1.0f;
+        continue;
+      }
+      const float mn = fmaxf(m, xv);
+      if (mn != -__builtin_huge_valf() && mn != __builtin_huge_valf())
+        z = z * expf(m - mn) + expf(xv - mn);
+      m = mn;
+    }
+    const float mrow = block_reduce<OpMax, BLOCK>(m, scratch);
+    nan = block_reduce<OpMax, BLOCK>(nan, scratch);
+    const bool finite = __builtin_fabsf(mrow) != __builtin_huge_valf();
+    z = (finite && m != -__builtin_huge_valf()) ? z * expf(m - mrow) : 0.0f;
+    const float zrow = block_reduce<OpSum, BLOCK>(z, scratch);
+    if (tid == 0)
+      store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, lse_finish(mrow, zrow, nan != 0.0f));
+  } else if constexpr (OP == ROW_SOFTMAX) {
     // online max/sum (softmax_kernel_inner.py:12-72): z is rescaled whenever
     // the running max grows
     float m = -__builtin_huge_valf(), z = 0.0f;
@@ -462,6 +514,7 @@ __device__ __forceinline__ void rr_loop_body(const RowArgs& a) {
 G950_RR_ALL(softmax, g950::ROW_SOFTMAX)
 G950_RR_ALL(rmsnorm, g950::ROW_RMSNORM)
 G950_RR_ALL(layernorm, g950::ROW_LAYERNORM)
+G950_RR_ALL(logsumexp, g950::ROW_LOGSUMEXP)
 
 // ------------------------------------------------------------- stream copy
 // y = x for n 16-byte vectors, grid-stride, nontemporal loads and stores --

@@ -67,6 +67,10 @@ def _softmax(a):
     ops.softmax_kernel(a["x_ptr"], a["y_ptr"], a["n_cols"], sync=True)
 
 
+def _logsumexp(a):
+    ops.logsumexp_kernel(a["x_ptr"], a["y_ptr"], a["n_cols"], sync=True)
+
+
 def _rms(a):
     ops.rms_layernorm_forward_kernel(a["Y"], a["Y_row_stride"], a["X"], a["X_row_stride"], a["W"],
                                      a["W_row_stride"], a["r"], a["r_row_stride"], a["n_cols"],
@@ -94,6 +98,7 @@ def _attention(a, causal_default):
 # reference kernel name -> operator (hot path only)
 KERNELS = {
     "softmax_kernel": _softmax,
+    "logsumexp_kernel": _logsumexp,
     "rms_layernorm_forward_kernel": _rms,
     "layernorm_kernel": _layernorm,
     "matmul_kernel": _matmul,

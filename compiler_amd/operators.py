@@ -38,6 +38,15 @@ def softmax_kernel(x_ptr, y_ptr, n_cols, *, stream=None, sync=False, prepare=Fal
                    {"n_cols": n_cols}, stream, sync, prepare)
 
 
+def logsumexp_kernel(x_ptr, y_ptr, n_cols, *, stream=None, sync=False, prepare=False):
+    """Row logsumexp (ops/suite/perf/logsumexp.py:16-38).  x: [rows, n_cols],
+    y: [rows] (float32 in the reference): max over non-NaN entries plus
+    log(sum(exp(x - max))); NaN for a row holding a NaN; an infinite max is
+    returned as is."""
+    return _launch(rt.OP_LOGSUMEXP, {"x_ptr": x_ptr, "y_ptr": y_ptr}, {"y_ptr"},
+                   {"n_cols": n_cols}, stream, sync, prepare)
+
+
 def rms_layernorm_forward_kernel(Y, Y_row_stride, X, X_row_stride, W, W_row_stride, r,
                                  r_row_stride, n_cols, eps, *, stream=None, sync=False, prepare=False):
     """RMSNorm forward (ops/suite/perf/fast_rms_layernorm.py:20-42)."""
@@ -118,6 +127,13 @@ def softmax(x, out=None, **kw):
     import torch
     y = torch.empty_like(x) if out is None else out
     softmax_kernel(x, y, x.shape[-1], **kw)
+    return y
+
+
+def logsumexp(x, out=None, **kw):
+    import torch
+    y = torch.empty(x.shape[0], dtype=torch.float32, device=x.device) if out is None else out
+    logsumexp_kernel(x, y, x.shape[-1], **kw)
     return y
 
 

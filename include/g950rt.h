@@ -112,6 +112,12 @@ typedef struct g950_scalar {
  *                      the HBM traffic counters; same load/store path as the
  *                      row kernels)
  *   views   x, y
+ * G950_OP_LOGSUMEXP    logsumexp_kernel (ops/suite/perf/logsumexp.py:16-38):
+ *                      y[r] = max + log(sum(exp(x - max))) with the max taken
+ *                      over non-NaN entries; NaN if the row holds a NaN, the
+ *                      max itself if it is infinite
+ *   views   x_ptr[R,C] f32 | bf16 | f16, y_ptr[R] (f32 in the reference)
+ *   scalars n_cols
  */
 enum g950_op {
   G950_OP_SOFTMAX = 1,
@@ -122,7 +128,8 @@ enum g950_op {
   G950_OP_MATMUL_I8_DEQUANT = 6,
   G950_OP_ATTENTION = 7,
   G950_OP_ATTENTION_LSE = 8,
-  G950_OP_COPY = 9
+  G950_OP_COPY = 9,
+  G950_OP_LOGSUMEXP = 10
 };
 
 typedef struct g950_module g950_module;

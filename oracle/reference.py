@@ -37,6 +37,7 @@ __all__ = [
     "bf16_round", "bf16_bits", "bf16_from_bits", "softmax", "rms_layernorm",
     "layernorm", "matmul", "matmul_i8", "dequant", "attention", "isclose_verdict",
     "TOLERANCES",
+    "logsumexp",
 ]
 
 # Shared value tolerances per dtype (ops/harness/opslib/case.py:153-157) and the
@@ -83,6 +84,26 @@ def softmax(x) -> np.ndarray:
     x64 = np.asarray(x, dtype=np.float64)
     e = np.exp(x64 - x64.max(axis=-1, keepdims=True))
     return e / e.sum(axis=-1, keepdims=True)
+
+
+def logsumexp(x) -> np.ndarray:
+    """Row logsumexp over the last axis in float64 (ops/suite/perf/logsumexp.py).
+
+    ref (:52-56) is ``np.logaddexp.reduce`` in float64; the kernel (:16-38)
+    takes the max over non-NaN entries, returns NaN for a row holding a NaN,
+    the max itself when it is infinite, else ``max + log(sum(exp(x - max)))``.
+    Both agree on every row: a NaN row reduces to NaN in logaddexp, a +inf
+    entry to +inf, an all -inf row to -inf.
+    """
+    x64 = np.asarray(x, dtype=np.float64)
+    nan = np.isnan(x64).any(axis=-1)
+    finite_or_inf = np.where(np.isnan(x64), -np.inf, x64)
+    mx = finite_or_inf.max(axis=-1)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        safe = np.where(np.isfinite(mx), mx, 0.0)
+        s = np.exp(finite_or_inf - safe[..., None]).sum(axis=-1)
+        out = np.where(np.isfinite(mx), safe + np.log(s), mx)
+    return np.where(nan, np.nan, out)
 
 
 def rms_layernorm(x, w, eps):

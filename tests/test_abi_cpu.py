@@ -121,6 +121,32 @@ def test_softmax_refusals():
     assert validate(rt.OP_SOFTMAX, softmax_args(4, 97, rt.DT_F32), [97, 1])[0] == rt.USAGE
 
 
+@pytest.mark.parametrize("rows,cols,dtype,ydt,kernel", [
+    (4, 16, rt.DT_F32, rt.DT_F32, "g950_rr_logsumexp_f32_v4_i1_b64"),
+    (64, 1024, rt.DT_BF16, rt.DT_F32, "g950_rr_logsumexp_bf16_v8_i2_b64"),
+    (4, 97, rt.DT_F16, rt.DT_F16, "g950_rr_logsumexp_f16_v1_i2_b64"),
+    (2, 100000, rt.DT_F32, rt.DT_F32, "g950_rr_loop_logsumexp_f32"),
+])
+def test_logsumexp_contract(rows, cols, dtype, ydt, kernel):
+    a = Args().view([rows, cols], dtype).view([rows], ydt, output=True)
+    rc, name, err = validate(rt.OP_LOGSUMEXP, a, [cols])
+    assert rc == 0, err
+    assert name == kernel
+
+
+def test_logsumexp_refusals():
+    ok = Args().view([4, 97], rt.DT_F32).view([4], rt.DT_F32, output=True)
+    assert validate(rt.OP_LOGSUMEXP, ok, [96])[0] == rt.USAGE
+    assert validate(rt.OP_LOGSUMEXP, ok, [97, 1])[0] == rt.USAGE
+    short = Args().view([4, 97], rt.DT_F32).view([3], rt.DT_F32, output=True)
+    rc, _, err = validate(rt.OP_LOGSUMEXP, short, [97])
+    assert rc == rt.USAGE and "per row" in err
+    ints = Args().view([4, 97], rt.DT_F32).view([4], rt.DT_INT32, output=True)
+    assert validate(rt.OP_LOGSUMEXP, ints, [97])[0] == rt.USAGE
+    unflagged = Args().view([4, 97], rt.DT_F32).view([4], rt.DT_F32, output=False)
+    assert validate(rt.OP_LOGSUMEXP, unflagged, [97])[0] == rt.REJECTED
+
+
 def test_view_reach_outside_storage_is_rejected():
     a = softmax_args(4, 97, rt.DT_F32)
     shape, strides, dtype, out, data, storage, size = a.specs[0]

@@ -1,0 +1,68 @@
+"""The harness Device protocol (ops/harness/opslib/device.py:79-118) driven the
+way the reference's case loop drives it: alloc / upload, a launch with the
+kernel object and positional arguments bound by its signature, download.
+
+The kernel objects here are plain functions carrying the reference kernels'
+names and parameter lists (ops/suite/perf/softmax.py, logsumexp.py); the
+device dispatches on the name, so these stand in for the Triton JIT objects.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from compiler_amd import runtime as rt  # noqa: E402
+from compiler_amd.device import G950Device  # noqa: E402
+from oracle import reference as ref  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def softmax_kernel(x_ptr, y_ptr, n_cols, BLOCK_SIZE):  # noqa: N803 - reference names
+    raise AssertionError("dispatched by name, never called")
+
+
+def logsumexp_kernel(x_ptr, y_ptr, n_cols, BLOCK_N):  # noqa: N803
+    raise AssertionError("dispatched by name, never called")
+
+
+def gelu_kernel(x_ptr, y_ptr, n):
+    raise AssertionError("not a hot-path operator")
+
+
+def test_device_softmax_float32_and_bf16_duality():
+    d = G950Device()
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((37, 97)).astype(np.float32)
+    for dt in ("float32", "bfloat16"):
+        xb = d.upload(x, dt)
+        yb = d.alloc(x.shape, dt)
+        d.launch(softmax_kernel, (37,), (xb, yb, 97), {"BLOCK_SIZE": 128})
+        y = d.download(yb)
+        assert y.dtype == np.float32 and y.shape == x.shape
+        xin = ref.bf16_round(x) if dt == "bfloat16" else x
+        rtol, atol = ref.TOLERANCES[dt]
+        ok, err = ref.isclose_verdict(y, ref.softmax(xin), rtol, atol)
+        assert ok, err
+    # uint16 host array = raw bf16 bits
+    bits = (ref.bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+    xb = d.upload(bits, "bfloat16")
+    assert np.array_equal(d.download(xb), ref.bf16_round(x))
+
+
+def test_device_logsumexp_reference_case_shape():
+    d = G950Device()
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((64, 1024)) * 3.0).astype(np.float32)
+    xb, yb = d.upload(x), d.alloc((64,), np.float32)
+    d.launch(logsumexp_kernel, (64,), (xb, yb, 1024), {"BLOCK_N": 1024})
+    assert rt.module().last_kernel.startswith("g950_rr_logsumexp_f32")
+    ok, err = ref.isclose_verdict(d.download(yb), ref.logsumexp(x), 3e-5, 3e-6)
+    assert ok, err
+
+
+def test_device_refuses_other_kernels():
+    d = G950Device()
+    xb, yb = d.upload(np.zeros(8, np.float32)), d.alloc((8,), np.float32)
+    with pytest.raises(NotImplementedError):
+        d.launch(gelu_kernel, (1,), (xb, yb, 8), {})

@@ -76,6 +76,51 @@ def test_layernorm_softmax_bf16_masked_tail(rows, cols):
     assert np.allclose(host(s).sum(axis=1), 1.0, atol=2e-2)
 
 
+@pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("rows,cols", [(4, 16), (4, 97), (64, 1024), (8191, 3000), (2, 100000)])
+def test_logsumexp(rows, cols, dt):
+    """ops/suite/perf/logsumexp.py: x ~ 3 N(0,1), expected from the inputs as
+    the kernel sees them (rounded to dt); y in float32 to the reference's own
+    bar (rtol 3e-5, atol 3e-6, :66), y in dt to the dtype's shared bar."""
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = (rng.standard_normal((rows, cols)) * 3.0).astype(np.float32)
+    xd = dev(x, dt)
+    xr = host(xd)
+    expect = ref.logsumexp(xr)
+    y = ops.logsumexp(xd, sync=True)
+    name = rt.module().last_kernel
+    assert name.startswith("g950_rr_") and "logsumexp" in name
+    assert ("_loop_" in name) == (cols == 100000)
+    close(host(y), expect, 3e-5, 3e-6)
+    yd = torch.zeros(rows, dtype=TD[dt], device=DEV)
+    ops.logsumexp_kernel(xd, yd, cols, sync=True)
+    rtol, atol = ref.TOLERANCES[dt]
+    close(host(yd), expect, rtol, atol)
+
+
+@pytest.mark.parametrize("cols", [97, 3000, 100000])
+def test_logsumexp_special_rows(cols):
+    """NaN anywhere -> NaN (also beside +inf), +inf -> +inf, all -inf -> -inf,
+    partial -inf -> lse of the finite part; a huge-magnitude row stays finite."""
+    rng = np.random.default_rng(cols)
+    x = rng.standard_normal((7, cols)).astype(np.float32)
+    x[0, cols // 2] = np.nan
+    x[1, cols - 1] = np.inf
+    x[2, :] = -np.inf
+    x[3, : cols // 3] = -np.inf
+    x[4, 0] = np.nan
+    x[4, cols - 1] = np.inf
+    x[5, :] = 3.0e38
+    x[6, :] = -3.0e38
+    y = host(ops.logsumexp(dev(x), sync=True))
+    e = ref.logsumexp(x)
+    assert np.array_equal(np.isnan(y), np.isnan(e)) and np.isnan(y[[0, 4]]).all()
+    assert y[1] == np.inf and y[2] == -np.inf
+    fin = np.isfinite(e)
+    assert np.isfinite(y[fin]).all()
+    close(y[fin], e[fin], 3e-5, 3e-6)
+
+
 def test_reduction_tail_guard_untouched():
     """Outputs are written only inside the view: a poisoned guard behind each
     row stays intact (the masked-tail witness idea of tools/check_masked_tails.py)."""

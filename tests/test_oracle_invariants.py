@@ -45,6 +45,44 @@ def test_softmax_constant_row_and_shift_invariance():
     assert np.allclose(ref.softmax(y)[0], bf, atol=1e-15)
 
 
+# ------------------------------------------------------------- logsumexp
+def test_logsumexp_closed_forms_and_library():
+    # constant row c of n entries: c + ln n
+    for c, n in ((2.5, 97), (-40.0, 16), (0.0, 1)):
+        assert np.allclose(ref.logsumexp(np.full((2, n), c)), c + math.log(n), rtol=0, atol=1e-13)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((6, 97)) * 3.0
+    scipy_special = pytest.importorskip("scipy.special")
+    assert np.allclose(ref.logsumexp(x), scipy_special.logsumexp(x, axis=-1), rtol=1e-14, atol=0)
+    # the reference's own ref() form (ops/suite/perf/logsumexp.py:52-56)
+    assert np.allclose(ref.logsumexp(x), np.logaddexp.reduce(x, axis=-1), rtol=1e-13, atol=0)
+    # shift invariance and brute force on one row
+    assert np.allclose(ref.logsumexp(x + 1000.0), ref.logsumexp(x) + 1000.0, rtol=1e-14)
+    assert math.isclose(ref.logsumexp(x)[0], math.log(sum(math.exp(v) for v in x[0])), rel_tol=1e-13)
+    # bounds: max <= lse <= max + ln n
+    assert np.all(ref.logsumexp(x) >= x.max(axis=1))
+    assert np.all(ref.logsumexp(x) <= x.max(axis=1) + math.log(97) + 1e-12)
+
+
+def test_logsumexp_special_values():
+    x = np.zeros((5, 8))
+    x[0, 3] = np.nan                       # NaN anywhere -> NaN
+    x[1, 5] = np.inf                       # +inf entry -> +inf
+    x[2, :] = -np.inf                      # all -inf -> -inf
+    x[3, :4] = -np.inf                     # some -inf -> ln of the finite part
+    x[4, 2] = np.nan
+    x[4, 6] = np.inf                       # NaN wins over +inf
+    y = ref.logsumexp(x)
+    assert math.isnan(y[0]) and math.isnan(y[4])
+    assert y[1] == np.inf and y[2] == -np.inf
+    assert math.isclose(y[3], math.log(4), rel_tol=1e-15)
+    # np.logaddexp.reduce (the reference's ref) agrees on every special row
+    with np.errstate(invalid="ignore"):
+        lib = np.logaddexp.reduce(x, axis=-1)
+    assert np.array_equal(np.isnan(lib), np.isnan(y))
+    assert np.array_equal(lib[~np.isnan(y)], y[~np.isnan(y)])
+
+
 # ---------------------------------------------------------------- norms
 def test_rmsnorm_closed_forms():
     w = np.linspace(0.5, 1.5, 64)
