@@ -186,29 +186,40 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
   // ---- DMA of one K+V tile: wave-instruction d (0..2*DMAS-1) fills 1 KiB,
   // dealt round-robin over the waves.  K instruction d = (slab ks, key half
   // kh): 32 keys x 32 B; V instruction (block b, key quarter kq): 16 keys x 64 B.
+  // Per-lane tile-relative source offsets are computed once: instruction u
+  // of a wave is a K instruction for u < DMA_PER_WAVE / 2, a V one after.
+  // Interior tiles then cost one 64-bit add per instruction; only a tile that
+  // runs past Sk clamps key indices.
+  static_assert(C::DMAS % NW == 0 && C::DMA_PER_WAVE * NW == 2 * C::DMAS, "DMA deal");
+  const long long kstride = 2 * (long long)p.k_ss, vstride = 2 * (long long)p.v_ss;
+  int dkey[C::DMA_PER_WAVE], dcol[C::DMA_PER_WAVE];
+#pragma unroll
+  for (int u = 0; u < C::DMA_PER_WAVE; ++u) {
+    const int d = wave + u * NW;
+    if (u < C::DMA_PER_WAVE / 2) {
+      const int ks = d >> 1, key = (d & 1) * 32 + (lane >> 1);
+      dkey[u] = key;
+      dcol[u] = ks * 32 + (((lane & 1) ^ ((key >> 3) & 1)) * 16);
+    } else {
+      const int dv = d - C::DMAS;
+      dkey[u] = (dv & 3) * 16 + (lane >> 2);
+      dcol[u] = (dv >> 2) * 64 + (lane & 3) * 16;
+    }
+  }
   auto dma_tile = [&](int t) {
     char* stage = lds + (t % ATT_STAGES) * C::STAGE;
     const int kv0 = t * ATT_BK;
+    const bool tail = kv0 + ATT_BK > p.Sk;
 #pragma unroll
     for (int u = 0; u < C::DMA_PER_WAVE; ++u) {
-      const int d = wave + u * NW;
-      if (d < 2 * C::DMAS) {
-        const char* src;
-        if (d < C::DMAS) {
-          const int ks = d >> 1, key = (d & 1) * 32 + (lane >> 1);
-          const int half = (lane & 1) ^ ((key >> 3) & 1);
-          const int gk = min(kv0 + key, p.Sk - 1);
-          src = kbase + 2 * (long long)gk * p.k_ss + ks * 32 + half * 16;
-        } else {
-          const int dv = d - C::DMAS;
-          const int b = dv >> 2, key = (dv & 3) * 16 + (lane >> 2);
-          const int gk = min(kv0 + key, p.Sk - 1);
-          src = vbase + 2 * (long long)gk * p.v_ss + b * 64 + (lane & 3) * 16;
-        }
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                         (__attribute__((address_space(3))) void*)(stage + d * 1024),
-                                         16, 0, 0);
-      }
+      const bool is_k = u < C::DMA_PER_WAVE / 2;
+      const char* base = is_k ? kbase : vbase;
+      const long long stride = is_k ? kstride : vstride;
+      const int key = tail ? min(kv0 + dkey[u], p.Sk - 1) : kv0 + dkey[u];
+      const char* src = base + key * stride + dcol[u];
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(stage + (wave + u * NW) * 1024),
+                                       16, 0, 0);
     }
   };
   auto active = [&](int t) { return !(p.causal && t * ATT_BK > qw + 31) && (qw < p.Sq); };
