@@ -217,6 +217,29 @@ def suite(torch, ops):
     del sets
     torch.cuda.empty_cache()
 
+    # next-row operators at their BASELINE-sized shapes, 4 rotating sets each:
+    # row logsumexp bf16 [8191, 3000] -> fp32, int8 weight dequant [8192, 8192] -> bf16
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    lse_sets = [(torch.randn((8191, 3000), device=dev, generator=g).mul_(3.0).to(torch.bfloat16),
+                 torch.empty(8191, device=dev)) for _ in range(ROTATE)]
+    lse_calls = [ops.logsumexp_kernel(x, y, 3000, prepare=True) for x, y in lse_sets]
+    dq_sets = [(torch.randint(-127, 127, (8192, 8192), device=dev, generator=g, dtype=torch.int8),
+                torch.rand(8192, device=dev, generator=g).to(torch.bfloat16),
+                torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)) for _ in range(ROTATE)]
+    dq_calls = [ops.dequantize_kernel(b, sc, y, 8192, 8192, 8192, 1, 8192, 1, prepare=True)
+                for b, sc, y in dq_sets]
+    for name, calls, nbytes, iters in (
+            ("F logsumexp bf16 [8191,3000] -> fp32", lse_calls, 8191 * 3000 * 2 + 8191 * 4, 200),
+            ("F dequantize int8 [8192,8192] -> bf16", dq_calls, 8192 * 8192 * 3 + 8192 * 2, 50)):
+        ms = event_time(torch, lambda i: calls[i % ROTATE](), iters, 10, warm_s=0.3)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"config": name, "kernel": calls[0].kernel, "us": round(ms * 1e3, 2),
+                    "value": round(gbs, 1), "unit": "GB/s", "bound": "hbm",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    del lse_sets, dq_sets, lse_calls, dq_calls
+    torch.cuda.empty_cache()
+
     # C3: bf16 GEMM, A row-major, B column-major
     for m, n, k in ((8192, 8192, 8192), (4097, 11008, 4096)):
         c = inputs.config3(m, n, k)

@@ -61,6 +61,18 @@ struct CopyArgs {
   long long n16;  // 16-byte vectors
 };
 
+struct DequantArgs {
+  const void* b;      // int8 [k, n]
+  const void* scale;  // [n], same dtype as y
+  void* y;            // [k, n]
+  long long b_sk, b_sn;  // element strides
+  long long y_sk, y_sn;
+  long long s_sn;
+  long long k, n;
+  long long work;     // vector kernel: row groups x column vectors
+  int y_dtype;
+};
+
 struct AttnGenArgs {
   AttnArgs a;
   int D;

@@ -4,3 +4,4 @@
 #include "rowreduce.hip"
 #include "gemm.hip"
 #include "attention.hip"
+#include "dequant.hip"

@@ -487,6 +487,68 @@ int op_matmul_i8(g950_module* m, const g950_view* views, uint32_t nviews, const 
   return launch(m, "g950_gemm_general_i8", (unsigned)blocks, 256u, g, stream);
 }
 
+// ---------------------------------------------------------- dequantisation
+// The reference passes the strides as scalars; they must name the same
+// elements as the views (checked wherever the extent makes them matter).
+int stride_agrees(const g950_scalar* sc, uint32_t idx, const char* name, const View& v, int dim) {
+  long long got;
+  if (int rc = scalar_int(&sc[idx], name, got)) return rc;
+  if (v.shape[dim] > 1 && got != v.stride[dim])
+    return fail(G950_USAGE, "scalar %s = %lld disagrees with view %s (stride %lld)", name, got, v.name,
+                (long long)v.stride[dim]);
+  return G950_OK;
+}
+
+int op_dequantize(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+                  uint32_t nsc, void* stream) {
+  if (nviews != 3 || nsc != 6)
+    return fail(G950_USAGE, "dequantize: needs views (b_ptr, b_scale_ptr, fpb_ptr), scalars "
+                "(K, N, stride_bk, stride_bn, stride_fpbk, stride_fpbn)");
+  View b, s, y;
+  if (int rc = check_view(views, 0, "b_ptr", 2, b, false)) return rc;
+  if (int rc = check_view(views, 1, "b_scale_ptr", 1, s, false)) return rc;
+  if (int rc = check_view(views, 2, "fpb_ptr", 2, y, true)) return rc;
+  if (b.v->dtype != G950_DTYPE_INT8) return fail(G950_USAGE, "dequantize: b_ptr must be int8");
+  if (!is_float(y.v->dtype) || s.v->dtype != y.v->dtype)
+    return fail(G950_USAGE, "dequantize: b_scale_ptr/fpb_ptr dtypes %s/%s (one of float32, bfloat16, float16)",
+                dtname(s.v->dtype), dtname(y.v->dtype));
+  const long long K = b.shape[0], N = b.shape[1];
+  if (y.shape[0] != K || y.shape[1] != N) return fail(G950_USAGE, "dequantize: fpb_ptr must be [K, N]");
+  if (s.shape[0] != N) return fail(G950_USAGE, "dequantize: b_scale_ptr needs one entry per column");
+  if (int rc = expect_int(sc, 0, "K", K)) return rc;
+  if (int rc = expect_int(sc, 1, "N", N)) return rc;
+  if (int rc = stride_agrees(sc, 2, "stride_bk", b, 0)) return rc;
+  if (int rc = stride_agrees(sc, 3, "stride_bn", b, 1)) return rc;
+  if (int rc = stride_agrees(sc, 4, "stride_fpbk", y, 0)) return rc;
+  if (int rc = stride_agrees(sc, 5, "stride_fpbn", y, 1)) return rc;
+  DequantArgs a{};
+  a.b = b.v->data; a.scale = s.v->data; a.y = y.v->data;
+  a.b_sk = b.stride[0]; a.b_sn = b.stride[1];
+  a.y_sk = y.stride[0]; a.y_sn = y.stride[1];
+  a.s_sn = s.stride[0];
+  a.k = K; a.n = N;
+  a.y_dtype = (int)y.v->dtype;
+  if (K == 0 || N == 0) return launch(m, "g950_dequant_i8_general", 0, 256u, a, stream);
+  const int ysz = y.isz;
+  const bool unit = (N == 1) || (b.stride[1] == 1 && y.stride[1] == 1 && s.stride[0] == 1);
+  const int cols = 16 / ysz;  // one 16-byte y vector (4 fp32 / 8 16-bit) per lane and row
+  const bool vec = unit && N % cols == 0 && (b.addr() % cols) == 0 && aligned16(y.addr()) &&
+                   aligned16(s.addr()) && (K == 1 || ((b.stride[0] % cols) == 0 && (y.stride[0] * ysz) % 16 == 0));
+  const unsigned cap = m ? (unsigned)m->cus * 8u : 2048u;
+  if (vec) {
+    const long long groups = (K + 3) / 4;  // DQ_ROWS rows per lane
+    a.work = groups * (N / cols);
+    if (a.work < 0x7FFFFFFF) {
+      const long long blocks = (a.work + 255) / 256;
+      const char* name = y.v->dtype == G950_DTYPE_FLOAT32 ? "g950_dequant_i8_f32"
+                         : y.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_dequant_i8_bf16" : "g950_dequant_i8_f16";
+      return launch(m, name, (unsigned)(blocks < cap ? blocks : cap), 256u, a, stream);
+    }
+  }
+  const long long blocks = (K * N + 255) / 256;
+  return launch(m, "g950_dequant_i8_general", (unsigned)(blocks < cap ? blocks : cap), 256u, a, stream);
+}
+
 // ---------------------------------------------------------------- attention
 int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
                  uint32_t nsc, bool with_lse, void* stream) {
@@ -642,6 +704,7 @@ int dispatch(g950_module* m, uint32_t op, const g950_view* views, uint32_t nview
       case G950_OP_ATTENTION: return op_attention(m, views, nviews, scalars, nscalars, false, stream);
       case G950_OP_ATTENTION_LSE: return op_attention(m, views, nviews, scalars, nscalars, true, stream);
       case G950_OP_COPY: return op_copy(m, views, nviews, nscalars, stream);
+      case G950_OP_DEQUANTIZE: return op_dequantize(m, views, nviews, scalars, nscalars, stream);
       default: return fail(G950_USAGE, "g950_launch: unknown operator contract %u", op);
     }
   } catch (...) {

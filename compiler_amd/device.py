@@ -57,10 +57,14 @@ def _kernel_name(kernel) -> str:
 
 
 def _kernel_params(kernel):
+    """Parameter names in the order ``bind_arguments`` emits positional values:
+    constexprs an autotuner supplies are skipped (device.py:241-252)."""
+    configs = getattr(kernel, "configs", None)
+    tuned = set((getattr(configs[0], "kwargs", {}) or {}).keys()) if configs else set()
     target = kernel
     for attr in ("fn", "fn"):
         target = getattr(target, attr, target)
-    return list(inspect.signature(target).parameters)
+    return [p for p in inspect.signature(target).parameters if p not in tuned]
 
 
 def _softmax(a):
@@ -69,6 +73,11 @@ def _softmax(a):
 
 def _logsumexp(a):
     ops.logsumexp_kernel(a["x_ptr"], a["y_ptr"], a["n_cols"], sync=True)
+
+
+def _dequantize(a):
+    ops.dequantize_kernel(a["b_ptr"], a["b_scale_ptr"], a["fpb_ptr"], a["K"], a["N"], a["stride_bk"],
+                          a["stride_bn"], a["stride_fpbk"], a["stride_fpbn"], sync=True)
 
 
 def _rms(a):
@@ -99,6 +108,7 @@ def _attention(a, causal_default):
 KERNELS = {
     "softmax_kernel": _softmax,
     "logsumexp_kernel": _logsumexp,
+    "dequantize_kernel": _dequantize,
     "rms_layernorm_forward_kernel": _rms,
     "layernorm_kernel": _layernorm,
     "matmul_kernel": _matmul,

@@ -47,6 +47,18 @@ def logsumexp_kernel(x_ptr, y_ptr, n_cols, *, stream=None, sync=False, prepare=F
                    {"n_cols": n_cols}, stream, sync, prepare)
 
 
+def dequantize_kernel(b_ptr, b_scale_ptr, fpb_ptr, K, N, stride_bk, stride_bn, stride_fpbk, stride_fpbn,
+                      *, stream=None, sync=False, prepare=False):
+    """int8 weight dequantisation fpb = b * b_scale[None, :]
+    (ops/suite/perf/dequantize_matmul.py:28-43).  b: int8 [K, N]; b_scale [N]
+    and fpb [K, N] share one float dtype; the stride scalars are element
+    strides and must match the tensors'."""
+    return _launch(rt.OP_DEQUANTIZE, {"b_ptr": b_ptr, "b_scale_ptr": b_scale_ptr, "fpb_ptr": fpb_ptr},
+                   {"fpb_ptr"}, {"K": K, "N": N, "stride_bk": stride_bk, "stride_bn": stride_bn,
+                                 "stride_fpbk": stride_fpbk, "stride_fpbn": stride_fpbn},
+                   stream, sync, prepare)
+
+
 def rms_layernorm_forward_kernel(Y, Y_row_stride, X, X_row_stride, W, W_row_stride, r,
                                  r_row_stride, n_cols, eps, *, stream=None, sync=False, prepare=False):
     """RMSNorm forward (ops/suite/perf/fast_rms_layernorm.py:20-42)."""
@@ -134,6 +146,15 @@ def logsumexp(x, out=None, **kw):
     import torch
     y = torch.empty(x.shape[0], dtype=torch.float32, device=x.device) if out is None else out
     logsumexp_kernel(x, y, x.shape[-1], **kw)
+    return y
+
+
+def dequantize(b, scale, out=None, **kw):
+    """b: int8 [K, N] tensor, scale: [N] float tensor -> b * scale in scale's dtype."""
+    import torch
+    y = torch.empty(b.shape, dtype=scale.dtype, device=b.device) if out is None else out
+    dequantize_kernel(b, scale, y, b.shape[0], b.shape[1], b.stride(0), b.stride(1), y.stride(0),
+                      y.stride(1), **kw)
     return y
 
 

@@ -118,6 +118,13 @@ typedef struct g950_scalar {
  *                      max itself if it is infinite
  *   views   x_ptr[R,C] f32 | bf16 | f16, y_ptr[R] (f32 in the reference)
  *   scalars n_cols
+ * G950_OP_DEQUANTIZE   dequantize_kernel (ops/suite/perf/dequantize_matmul.py:28-43):
+ *                      fpb[k,n] = float(b[k,n]) * b_scale[n], rounded once to
+ *                      fpb's dtype (exact product: bit-equal to float64 then round)
+ *   views   b_ptr i8[K,N], b_scale_ptr[N], fpb_ptr[K,N]; b_scale_ptr and fpb_ptr
+ *           share one dtype (f32 | bf16 | f16)
+ *   scalars K, N, stride_bk, stride_bn, stride_fpbk, stride_fpbn (element
+ *           strides; must agree with the views wherever the extent exceeds 1)
  */
 enum g950_op {
   G950_OP_SOFTMAX = 1,
@@ -129,7 +136,8 @@ enum g950_op {
   G950_OP_ATTENTION = 7,
   G950_OP_ATTENTION_LSE = 8,
   G950_OP_COPY = 9,
-  G950_OP_LOGSUMEXP = 10
+  G950_OP_LOGSUMEXP = 10,
+  G950_OP_DEQUANTIZE = 11
 };
 
 typedef struct g950_module g950_module;

@@ -38,6 +38,7 @@ __all__ = [
     "layernorm", "matmul", "matmul_i8", "dequant", "attention", "isclose_verdict",
     "TOLERANCES",
     "logsumexp",
+    "dequantize",
 ]
 
 # Shared value tolerances per dtype (ops/harness/opslib/case.py:153-157) and the
@@ -104,6 +105,15 @@ def logsumexp(x) -> np.ndarray:
         s = np.exp(finite_or_inf - safe[..., None]).sum(axis=-1)
         out = np.where(np.isfinite(mx), safe + np.log(s), mx)
     return np.where(nan, np.nan, out)
+
+
+def dequantize(b, scale) -> np.ndarray:
+    """int8 weight dequantisation in float64 (ops/suite/perf/dequantize_matmul.py):
+    ``ref`` (:47-50) is ``b * s[None, :]`` in float64, cast to fpb's dtype;
+    the kernel (:28-43) widens b and s to fp32 and multiplies.  The product of
+    an int8 and a float32/bf16/fp16 value is exact in float64, so rounding it
+    to the output dtype is the single rounding both forms perform."""
+    return np.asarray(b, dtype=np.float64) * np.asarray(scale, dtype=np.float64)[None, :]
 
 
 def rms_layernorm(x, w, eps):

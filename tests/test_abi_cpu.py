@@ -48,7 +48,7 @@ def test_strerror_codes():
 class Args:
     """Builds fake views (host shape/stride arrays, fake device addresses)."""
 
-    ITEM = {rt.DT_F32: 4, rt.DT_BF16: 2, rt.DT_F16: 2, rt.DT_INT8: 1, rt.DT_INT32: 4}
+    ITEM = {rt.DT_F32: 4, rt.DT_BF16: 2, rt.DT_F16: 2, rt.DT_INT8: 1, rt.DT_UINT8: 1, rt.DT_INT32: 4}
 
     def __init__(self):
         self.specs = []
@@ -145,6 +145,43 @@ def test_logsumexp_refusals():
     assert validate(rt.OP_LOGSUMEXP, ints, [97])[0] == rt.USAGE
     unflagged = Args().view([4, 97], rt.DT_F32).view([4], rt.DT_F32, output=False)
     assert validate(rt.OP_LOGSUMEXP, unflagged, [97])[0] == rt.REJECTED
+
+
+def dq_args(k, n, ydt, b_strides=None):
+    return (Args().view([k, n], rt.DT_INT8, strides=b_strides).view([n], ydt)
+            .view([k, n], ydt, output=True))
+
+
+@pytest.mark.parametrize("k,n,ydt,kernel", [
+    (32, 32, rt.DT_F32, "g950_dequant_i8_f32"),
+    (8192, 8192, rt.DT_BF16, "g950_dequant_i8_bf16"),
+    (256, 32, rt.DT_F16, "g950_dequant_i8_f16"),
+    (33, 33, rt.DT_F32, "g950_dequant_i8_general"),
+])
+def test_dequantize_contract(k, n, ydt, kernel):
+    rc, name, err = validate(rt.OP_DEQUANTIZE, dq_args(k, n, ydt), [np.int32(k), np.int32(n), np.int32(n),
+                                                                     np.int32(1), np.int32(n), np.int32(1)])
+    assert rc == 0, err
+    assert name == kernel
+
+
+def test_dequantize_refusals():
+    good = [np.int32(32), np.int32(32), np.int32(32), np.int32(1), np.int32(32), np.int32(1)]
+    # a stride scalar that disagrees with its view
+    bad = list(good)
+    bad[2] = np.int32(31)
+    rc, _, err = validate(rt.OP_DEQUANTIZE, dq_args(32, 32, rt.DT_F32), bad)
+    assert rc == rt.USAGE and "stride_bk" in err
+    assert validate(rt.OP_DEQUANTIZE, dq_args(32, 32, rt.DT_F32), good[:5])[0] == rt.USAGE
+    # scale and output dtypes must agree; b must be int8
+    a = Args().view([32, 32], rt.DT_INT8).view([32], rt.DT_F32).view([32, 32], rt.DT_BF16, output=True)
+    assert validate(rt.OP_DEQUANTIZE, a, good)[0] == rt.USAGE
+    a = Args().view([32, 32], rt.DT_UINT8).view([32], rt.DT_F32).view([32, 32], rt.DT_F32, output=True)
+    assert validate(rt.OP_DEQUANTIZE, a, good)[0] == rt.USAGE
+    # a column-major b takes the general kernel
+    rc, name, err = validate(rt.OP_DEQUANTIZE, dq_args(32, 32, rt.DT_F32, b_strides=[1, 32]),
+                             [np.int32(32), np.int32(32), np.int32(1), np.int32(32), np.int32(32), np.int32(1)])
+    assert rc == 0 and name == "g950_dequant_i8_general", err
 
 
 def test_view_reach_outside_storage_is_rejected():

@@ -26,6 +26,25 @@ def logsumexp_kernel(x_ptr, y_ptr, n_cols, BLOCK_N):  # noqa: N803
     raise AssertionError("dispatched by name, never called")
 
 
+def _dequantize_kernel(b_ptr, b_scale_ptr, fpb_ptr, K, N, stride_bk, stride_bn, stride_fpbk,  # noqa: N803
+                       stride_fpbn, BLOCK_K, BLOCK_N):
+    raise AssertionError("dispatched by name, never called")
+
+
+class _Config:
+    kwargs = {"BLOCK_K": 32, "BLOCK_N": 32}
+
+
+class _Autotuned:
+    """The shape of a triton Autotuner: .fn is the kernel, .configs its tuning
+    space; bind_arguments leaves the tuned constexprs out of the positionals."""
+    fn = staticmethod(_dequantize_kernel)
+    configs = [_Config()]
+
+
+_dequantize_kernel.__name__ = "dequantize_kernel"
+
+
 def gelu_kernel(x_ptr, y_ptr, n):
     raise AssertionError("not a hot-path operator")
 
@@ -59,6 +78,20 @@ def test_device_logsumexp_reference_case_shape():
     assert rt.module().last_kernel.startswith("g950_rr_logsumexp_f32")
     ok, err = ref.isclose_verdict(d.download(yb), ref.logsumexp(x), 3e-5, 3e-6)
     assert ok, err
+
+
+def test_device_dequantize_autotuned_kernel():
+    """dequantize_matmul.py case (33, 33) in bf16: the autotuned constexprs
+    are absent from the positionals, the scalars are numpy int32."""
+    d = G950Device()
+    rng = np.random.default_rng(13)
+    b = rng.integers(-127, 128, (33, 33)).astype(np.int8)
+    s = ref.bf16_round(rng.random(33).astype(np.float32))
+    bb, sb, yb = d.upload(b), d.upload(s, "bfloat16"), d.alloc((33, 33), "bfloat16")
+    i32 = np.int32
+    d.launch(_Autotuned(), None, (bb, sb, yb, i32(33), i32(33), i32(33), i32(1), i32(33), i32(1)), {})
+    expect = ref.bf16_round(ref.dequantize(b, s).astype(np.float32))
+    assert np.array_equal(d.download(yb), expect)
 
 
 def test_device_refuses_other_kernels():

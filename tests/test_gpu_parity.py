@@ -121,6 +121,52 @@ def test_logsumexp_special_rows(cols):
     close(y[fin], e[fin], 3e-5, 3e-6)
 
 
+def _dq_expect(b, s, dt):
+    p = ref.dequantize(b, s)
+    if dt == "bfloat16":
+        return ref.bf16_round(p.astype(np.float32))
+    if dt == "float16":
+        return p.astype(np.float16).astype(np.float32)
+    return p.astype(np.float32)
+
+
+@pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("k,n", [(32, 32), (33, 33), (256, 32), (5, 48), (8192, 8192)])
+def test_dequantize_bit_exact(k, n, dt):
+    """ops/suite/perf/dequantize_matmul.py: b ~ U{-127..127}, scale ~ U[0,1)
+    in dt (make_case :57-60); bit-exact against the float64 product rounded
+    once to dt."""
+    rng = np.random.default_rng(k * 31 + n)
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    sd = dev(rng.random(n).astype(np.float32), dt)
+    y = ops.dequantize(torch.from_numpy(b).to(DEV), sd, sync=True)
+    vec = n % (4 if dt == "float32" else 8) == 0
+    assert rt.module().last_kernel == ("g950_dequant_i8_" + {"float32": "f32", "bfloat16": "bf16",
+                                                            "float16": "f16"}[dt] if vec
+                                       else "g950_dequant_i8_general")
+    assert np.array_equal(host(y), _dq_expect(b, host(sd), dt))
+
+
+def test_dequantize_strided_views_and_guard():
+    """Column-major b (general kernel) and an output with padded rows: the
+    pad stays untouched, the values stay exact."""
+    rng = np.random.default_rng(44)
+    k, n = 64, 96
+    b = rng.integers(-128, 128, (k, n)).astype(np.int8)
+    bt = torch.from_numpy(np.ascontiguousarray(b.T)).to(DEV).t()  # strides (1, k)
+    s = dev(rng.random(n).astype(np.float32), "bfloat16")
+    buf = torch.full((k, n + 16), 5.0, dtype=torch.bfloat16, device=DEV)
+    y = buf[:, :n]
+    ops.dequantize(bt, s, out=y, sync=True)
+    assert rt.module().last_kernel == "g950_dequant_i8_general"
+    assert np.array_equal(host(y), _dq_expect(b, host(s), "bfloat16"))
+    bc = torch.from_numpy(b).to(DEV)
+    ops.dequantize(bc, s, out=y, sync=True)
+    assert rt.module().last_kernel == "g950_dequant_i8_bf16"
+    assert np.array_equal(host(y), _dq_expect(b, host(s), "bfloat16"))
+    assert torch.all(buf[:, n:] == 5.0)
+
+
 def test_reduction_tail_guard_untouched():
     """Outputs are written only inside the view: a poisoned guard behind each
     row stays intact (the masked-tail witness idea of tools/check_masked_tails.py)."""

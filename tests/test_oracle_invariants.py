@@ -83,6 +83,28 @@ def test_logsumexp_special_values():
     assert np.array_equal(lib[~np.isnan(y)], y[~np.isnan(y)])
 
 
+# ------------------------------------------------------------ dequantize
+def test_dequantize_orientation_brute_force_and_exactness():
+    rng = np.random.default_rng(6)
+    k, n = 5, 7
+    b = rng.integers(-128, 128, (k, n)).astype(np.int8)
+    s = rng.random(n).astype(np.float32)
+    y = ref.dequantize(b, s)
+    # brute force; the scale belongs to the column (a per-row scale fails)
+    for i in range(k):
+        for j in range(n):
+            assert y[i, j] == float(int(b[i, j])) * float(s[j])
+    assert not np.allclose(y, np.asarray(b, np.float64) * np.asarray(s[:k], np.float64)[:, None])
+    # unit scale is the widened int8; a power-of-two scale is exact scaling
+    assert np.array_equal(ref.dequantize(b, np.ones(n)), b.astype(np.float64))
+    assert np.array_equal(ref.dequantize(b, np.full(n, 0.125)), b.astype(np.float64) / 8)
+    # int8 x bf16/fp16 products fit fp32 exactly: the kernel's fp32 product
+    # rounds only once, at the output dtype
+    for scale in (ref.bf16_round(s), s.astype(np.float16).astype(np.float32)):
+        p = ref.dequantize(b, scale)
+        assert np.array_equal(p.astype(np.float32).astype(np.float64), p)
+
+
 # ---------------------------------------------------------------- norms
 def test_rmsnorm_closed_forms():
     w = np.linspace(0.5, 1.5, 64)
