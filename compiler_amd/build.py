@@ -2,6 +2,7 @@
 
   compiler_amd/lib/g950.hsaco     every hot-path kernel (hipcc --genco, gfx950)
   compiler_amd/lib/libg950rt.so   the C-ABI module loader/launcher (include/g950rt.h)
+  compiler_amd/lib/g950_exec      the bundle-driven command-line runner
 
 Both are written next to the package so they travel with the source tree; the
 Python runtime loads exactly these two files.
@@ -19,6 +20,7 @@ CSRC = PKG / "csrc"
 LIB = PKG / "lib"
 HSACO = LIB / "g950.hsaco"
 RTLIB = LIB / "libg950rt.so"
+EXEC = LIB / "g950_exec"
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -48,14 +50,24 @@ def build_runtime() -> Path:
     LIB.mkdir(exist_ok=True)
     tmp = RTLIB.with_name(RTLIB.name + ".tmp")
     _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-I{ROOT / 'include'}",
-          f"-I{CSRC}", "-o", str(tmp), str(CSRC / "g950rt.cpp")])
+          f"-I{CSRC}", "-o", str(tmp), str(CSRC / "g950rt.cpp"), str(CSRC / "g950_bundle.cpp")])
     os.replace(tmp, RTLIB)
     return RTLIB
+
+
+def build_exec() -> Path:
+    """g950_exec: the bundle-driven command-line runner (links libg950rt.so)."""
+    tmp = EXEC.with_name(EXEC.name + ".tmp")
+    _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{ROOT / 'include'}", "-o", str(tmp),
+          str(CSRC / "g950_exec.cpp"), f"-L{LIB}", "-lg950rt", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, EXEC)
+    return EXEC
 
 
 def build_all() -> None:
     build_code_object()
     build_runtime()
+    build_exec()
 
 
 if __name__ == "__main__":

@@ -118,7 +118,11 @@ def _reach(shape, strides, itemsize):
 
 
 def parse(image: bytes | bytearray, names: dict | None = None) -> Bundle:
-    """Validate and decode a whole image (mirrors a100c/runtime/bundle.c:111-339)."""
+    """Validate and decode a whole image (mirrors a100c/runtime/bundle.c:111-339).
+
+    The checks run in the reference reader's order, so the first rule an image
+    breaks is the reason reported (the native reader, ``g950_bundle_check``,
+    follows the same order and the tests hold the two to the same verdicts)."""
     image = bytearray(image)
     size = len(image)
     if size < HEADER.size:
@@ -132,65 +136,73 @@ def parse(image: bytes | bytearray, names: dict | None = None) -> Bundle:
         raise BundleRejected("reserved")
     cursor = HEADER.size
     if nstorage * STORAGE.size > size - cursor:
-        raise BundleRejected("count-bounds")
+        raise BundleRejected("storage-bounds", "storage table")
     storages = []
     for i in range(nstorage):
         off, ln = STORAGE.unpack_from(image, cursor + i * STORAGE.size)
         if off > size or ln > size - off:
             raise BundleRejected("storage-bounds", f"storage {i}")
         storages.append((off, ln))
+    if nviews > size // 24 or nscalars > size // 16 or nreloc > size // 24:
+        raise BundleRejected("count-bounds")
     cursor += nstorage * STORAGE.size
     views = []
     for i in range(nviews):
         if cursor + VIEW.size > size:
             raise BundleRejected("view-truncated")
         storage, dtype, ndim, flags, offset = VIEW.unpack_from(image, cursor)
-        cursor += VIEW.size
-        if ndim > 16 or cursor + 16 * ndim > size:
-            raise BundleRejected("view-dim" if ndim > 16 else "view-truncated")
-        dims = struct.unpack_from("<" + "q" * (2 * ndim), image, cursor)
-        cursor += 16 * ndim
-        shape, strides = tuple(dims[:ndim]), tuple(dims[ndim:])
         if storage >= nstorage:
             raise BundleRejected("view-storage", f"view {i}")
         if dtype not in ITEMSIZE:
             raise BundleRejected("view-dtype", f"view {i}")
         if flags & ~1:
             raise BundleRejected("view-flags", f"view {i}")
-        if any(n < 0 for n in shape):
-            raise BundleRejected("view-dim", f"view {i}")
+        cursor += VIEW.size
+        if 16 * ndim > size - cursor:
+            raise BundleRejected("view-truncated")
         s_off, s_len = storages[storage]
-        lo, hi = _reach(shape, strides, ITEMSIZE[dtype])
         if offset < 0 or offset > s_len:
             raise BundleRejected("view-offset", f"view {i}")
+        dims = struct.unpack_from("<" + "q" * (2 * ndim), image, cursor)
+        cursor += 16 * ndim
+        shape, strides = tuple(dims[:ndim]), tuple(dims[ndim:])
+        if any(n < 0 for n in shape):
+            raise BundleRejected("view-dim", f"view {i}")
+        lo, hi = _reach(shape, strides, ITEMSIZE[dtype])
         if offset + lo < 0 or offset + hi > s_len:
             raise BundleRejected("view-reach", f"view {i}")
         views.append(ViewRecord(storage, dtype, shape, strides, offset, bool(flags & 1)))
+    if SCALAR.size * nscalars > size - cursor:
+        raise BundleRejected("scalar-truncated")
     scalars = []
     for i in range(nscalars):
-        if cursor + SCALAR.size > size:
-            raise BundleRejected("scalar-truncated")
         dtype, width, bits = SCALAR.unpack_from(image, cursor)
         cursor += SCALAR.size
         if dtype not in ITEMSIZE or width != ITEMSIZE[dtype]:
             raise BundleRejected("scalar-width", f"scalar {i}")
         scalars.append(ScalarRecord(dtype, width, bits))
+    if RELOCATION.size * nreloc > size - cursor:
+        raise BundleRejected("reloc-truncated")
+    metadata_end = cursor + RELOCATION.size * nreloc
+    for i, (off, _ln) in enumerate(storages):
+        if off < metadata_end:
+            raise BundleRejected("storage-overlaps-metadata", f"storage {i}")
     relocations = []
     for i in range(nreloc):
-        if cursor + RELOCATION.size > size:
-            raise BundleRejected("reloc-truncated")
         table, target, entry, byte_offset = RELOCATION.unpack_from(image, cursor)
         cursor += RELOCATION.size
         if table >= nviews or target >= nviews:
             raise BundleRejected("reloc-view")
-        if views[table].dtype not in (8, 9):
+        t, d = views[table], views[target]
+        if t.dtype not in (8, 9):
             raise BundleRejected("reloc-table-width")
-        if views[table].output:
+        if t.output:
             raise BundleRejected("reloc-table-output")
+        if entry > (2**64 - 1) // 8 or t.offset + entry * 8 + 8 > storages[t.storage][1]:
+            raise BundleRejected("reloc-entry")
+        if byte_offset < 0 or byte_offset > storages[d.storage][1] - d.offset:
+            raise BundleRejected("reloc-offset")
         relocations.append((table, target, entry, byte_offset))
-    for i, (off, ln) in enumerate(storages):
-        if ln and off < cursor:
-            raise BundleRejected("storage-overlaps-metadata", f"storage {i}")
     bundle = Bundle(image, storages, views, scalars, relocations)
     if names:
         for rec, name in zip(views, names.get("view_order", [])):

@@ -668,6 +668,11 @@ int op_copy(g950_module* m, const g950_view* views, uint32_t nviews, uint32_t ns
 
 }  // namespace
 
+// Shared with g950_bundle.cpp (same library; not part of the C ABI).
+__attribute__((visibility("hidden"))) int g950rt_fail(int code, const std::string& msg) {
+  return fail(code, "%s", msg.c_str());
+}
+
 extern "C" {
 
 int g950_open(const char* path, g950_module** out) {

@@ -37,7 +37,9 @@ DT_BOOL, DT_INT8, DT_UINT8, DT_INT16, DT_UINT16, DT_INT32 = 1, 2, 3, 4, 5, 6
 DT_UINT32, DT_INT64, DT_UINT64, DT_F16, DT_BF16, DT_F32, DT_F64 = 7, 8, 9, 10, 11, 12, 13
 
 EXPORTS = ("g950_open", "g950_launch", "g950_validate", "g950_last_kernel", "g950_sync", "g950_strerror",
-           "g950_last_error", "g950_close")
+           "g950_last_error", "g950_close", "g950_bundle_open", "g950_bundle_check", "g950_bundle_reason",
+           "g950_bundle_count", "g950_bundle_view", "g950_bundle_scalar", "g950_bundle_exec",
+           "g950_bundle_close")
 
 
 class G950Error(RuntimeError):
@@ -89,8 +91,28 @@ def load_library():
         lib.g950_last_error.restype = ctypes.c_char_p
         lib.g950_close.argtypes = [ctypes.c_void_p]
         lib.g950_close.restype = None
+        vp, u32, i32p = ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_int)
+        lib.g950_bundle_open.argtypes = [ctypes.c_char_p, u32, ctypes.POINTER(vp), i32p]
+        lib.g950_bundle_check.argtypes = [ctypes.c_char_p, ctypes.c_uint64, i32p]
+        lib.g950_bundle_reason.argtypes = [ctypes.c_int]
+        lib.g950_bundle_reason.restype = ctypes.c_char_p
+        lib.g950_bundle_count.argtypes = [vp, ctypes.c_int]
+        lib.g950_bundle_count.restype = u32
+        lib.g950_bundle_view.argtypes = [vp, u32, ctypes.POINTER(View)]
+        lib.g950_bundle_scalar.argtypes = [vp, u32, ctypes.POINTER(Scalar)]
+        lib.g950_bundle_exec.argtypes = [vp, vp, u32, ctypes.POINTER(Scalar), u32, u32, vp, i32p]
+        lib.g950_bundle_close.argtypes = [vp]
         _lib = lib
         return lib
+
+
+def bundle_check(image: bytes) -> str | None:
+    """Native a100-native-io/v1 validation of an in-memory image: None if the
+    image is valid, else the reference reader's reason name."""
+    lib = load_library()
+    reason = ctypes.c_int(0)
+    rc = lib.g950_bundle_check(bytes(image), len(image), ctypes.byref(reason))
+    return None if rc == OK else lib.g950_bundle_reason(reason.value).decode()
 
 
 def _torch_dtype_code(t) -> int:

@@ -177,6 +177,65 @@ const char *g950_last_error(void);
 /* Unload the code object. */
 void g950_close(g950_module *module);
 
+/* ---------------------------------------------------------------------------
+ * a100-native-io/v1 bundles: the reference's host<->native argument image
+ * (writer a100_support/native_io.py:49-150, reader a100c/runtime/bundle.c).
+ * These calls replace the reference's bundle reader and the repeat loop of its
+ * single-operator executable (a100c/runtime/main.c:50-177); the
+ * `g950_exec` program (compiler_amd/csrc/g950_exec.cpp) is the command-line
+ * counterpart of `operator_exec --bundle`.
+ * ------------------------------------------------------------------------- */
+typedef struct g950_bundle g950_bundle;
+
+/* Map the file shared and write outputs back on close (the reference's
+ * behaviour); without it the mapping is private and the file never changes. */
+#define G950_BUNDLE_WRITE_BACK 1u
+
+/* Rejection reasons: the reference reader's codes and names, same values
+ * (a100c/runtime/bundle.c:31-88). */
+enum g950_bundle_reason {
+  G950_R_OPEN = 1, G950_R_SIZE, G950_R_MAGIC, G950_R_VERSION, G950_R_RESERVED, G950_R_MAP,
+  G950_R_STORAGE_BOUNDS, G950_R_COUNT_BOUNDS, G950_R_ALLOC, G950_R_VIEW_TRUNCATED,
+  G950_R_VIEW_STORAGE, G950_R_VIEW_DTYPE, G950_R_VIEW_OFFSET, G950_R_VIEW_DIM, G950_R_VIEW_REACH,
+  G950_R_VIEW_FLAGS, G950_R_SCALAR_TRUNCATED, G950_R_SCALAR_WIDTH, G950_R_RELOC_TRUNCATED,
+  G950_R_RELOC_VIEW, G950_R_RELOC_TABLE_WIDTH, G950_R_RELOC_TABLE_OUTPUT, G950_R_RELOC_ENTRY,
+  G950_R_RELOC_OFFSET, G950_R_STORAGE_OVERLAPS_METADATA
+};
+
+/* Open, map and validate a bundle image (replaces a100rt_bundle_open,
+ * a100c/runtime/bundle.c:111-339).  Every record is checked, in the
+ * reference's order, before anything is returned: a violation returns
+ * G950_REJECTED with *reason set and leaves the file untouched.  Host only. */
+int g950_bundle_open(const char *path, uint32_t flags, g950_bundle **out, int *reason);
+
+/* The same validation on an in-memory image (no file, nothing written). */
+int g950_bundle_check(const void *image, uint64_t size, int *reason);
+
+/* Name of a rejection reason (replaces a100rt_reject_reason,
+ * a100c/runtime/bundle.c:59-88). */
+const char *g950_bundle_reason(int reason);
+
+/* Record counts: what = 0 storages, 1 views, 2 scalars, 3 relocations. */
+uint32_t g950_bundle_count(const g950_bundle *bundle, int what);
+
+/* View i over the mapped (host) image, and scalar i, in the image's order. */
+int g950_bundle_view(const g950_bundle *bundle, uint32_t i, g950_view *out);
+int g950_bundle_scalar(const g950_bundle *bundle, uint32_t i, g950_scalar *out);
+
+/* Run operator `op` on the bundle `repeats` times on the current device
+ * (replaces main.c:96-150 and the pool call): every storage is staged into its
+ * own device allocation (pointer tables patched with device addresses), each
+ * repeat restores all storages from the image first, outputs are compared
+ * with the first repeat's byte for byte (*repeats_equal), and the first
+ * repeat's outputs are written into the mapped image.  `lead` scalars are
+ * prepended to the bundle's own (for constexprs with semantics that the image
+ * does not carry, e.g. attention's CAUSAL).  Returns the launcher's code. */
+int g950_bundle_exec(g950_module *module, g950_bundle *bundle, uint32_t op, const g950_scalar *lead,
+                     uint32_t nlead, uint32_t repeats, void *stream, int *repeats_equal);
+
+/* Unmap (syncing a write-back mapping to its file: G950_SYNC on failure). */
+int g950_bundle_close(g950_bundle *bundle);
+
 #ifdef __cplusplus
 }
 #endif
