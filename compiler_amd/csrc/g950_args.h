@@ -20,6 +20,8 @@ struct RowArgs {
   int cols;
   float eps;
   int stat_dtype;     // dtype code of stat0/stat1
+  void* part;         // split rows: [rows * splits] partial records of 4 floats
+  int splits;         // split rows: chunks per row
 };
 
 struct GemmArgs {

@@ -36,6 +36,10 @@ struct g950_module {
   int cus = 256;  // compute units of the device (persistent grid sizing)
   std::mutex mu;
   std::unordered_map<std::string, hipFunction_t> fns;
+  // per-stream device workspace (split-row partials); launches on one stream
+  // are ordered, so each stream owns one buffer, grown on demand
+  std::mutex ws_mu;
+  std::unordered_map<void*, std::pair<void*, size_t>> ws;
 };
 
 namespace {
@@ -216,6 +220,51 @@ const char* rr_dtype(uint32_t dt) {
   return dt == G950_DTYPE_FLOAT32 ? "f32" : dt == G950_DTYPE_BFLOAT16 ? "bf16" : "f16";
 }
 
+// Device workspace of at least `bytes` for launches on `stream`.  Growing it
+// waits for the stream (the old buffer may still be read by queued work).
+int workspace(g950_module* m, void* stream, size_t bytes, void** out) {
+  std::lock_guard<std::mutex> lock(m->ws_mu);
+  auto& w = m->ws[stream];
+  if (w.second < bytes) {
+    if (w.first) {
+      if (hipError_t e = hipStreamSynchronize((hipStream_t)stream))
+        return fail(G950_SYNC, "workspace: %s", hipGetErrorString(e));
+      (void)hipFree(w.first);
+      w = {nullptr, 0};
+    }
+    const size_t n = (bytes < (size_t)65536 ? (size_t)65536 : bytes * 2 + 255) & ~(size_t)255;
+    if (hipError_t e = hipMalloc(&w.first, n)) {
+      w = {nullptr, 0};
+      return fail(G950_RESOURCE, "workspace: hipMalloc(%zu): %s", n, hipGetErrorString(e));
+    }
+    w.second = n;
+  }
+  *out = w.first;
+  return G950_OK;
+}
+
+// Split rows (rowreduce.hip, rs_*): chunks of 1024 vectors (RS_BLOCK 256 x
+// RS_ITEMS 4), one workgroup per (row, chunk), two launches.
+constexpr long long kRsChunkVecs = 1024;
+
+int launch_split_rows(g950_module* m, const char* op, RowArgs& a, uint32_t dt, int v, void* stream) {
+  const long long nvec = a.cols / v;
+  const long long splits = (nvec + kRsChunkVecs - 1) / kRsChunkVecs;
+  const long long blocks = (long long)a.rows * splits;
+  if (blocks > 0x7FFFFFFF) return fail(G950_USAGE, "%s: too many row chunks", op);
+  a.splits = (int)splits;
+  a.part = nullptr;
+  if (m && blocks) {
+    if (int rc = workspace(m, stream, (size_t)blocks * 16, &a.part)) return rc;
+  }
+  char name[128];
+  snprintf(name, sizeof name, "g950_rs_part_%s_%s_v%d", op, rr_dtype(dt), v);
+  if (int rc = launch(m, name, (unsigned)blocks, 256u, a, stream)) return rc;
+  snprintf(name, sizeof name, "g950_rs_final_%s_%s_v%d", op, rr_dtype(dt), v);
+  const bool lse = strcmp(op, "logsumexp") == 0;
+  return launch(m, name, (unsigned)(lse ? a.rows : blocks), 256u, a, stream);
+}
+
 // Pick and launch the row kernel.  `params` are the per-column parameter
 // views (W, B) whose alignment the vector form also needs.
 int launch_rows(g950_module* m, const char* op, RowArgs& a, uint32_t dt, const View& x,
@@ -232,14 +281,17 @@ int launch_rows(g950_module* m, const char* op, RowArgs& a, uint32_t dt, const V
   const RowCfg* pick = nullptr;
   for (const RowCfg& c : kRowCfgs)
     if (c.items * c.block >= nvec) { pick = &c; break; }
-  if (pick) {
+  // one workgroup per row leaves most of the chip idle when rows are few and
+  // long: split them (two or more chunks each) instead
+  const long long cus = m ? m->cus : 256;
+  const bool few = (long long)a.rows * 2 < cus && nvec > kRsChunkVecs;
+  if (pick && !few) {
     snprintf(name, sizeof name, "g950_rr_%s_%s_v%d_i%d_b%d", op, rr_dtype(dt), v, pick->items,
              pick->block);
     return launch(m, name, row_grid(m, a.rows, pick->block, pick->waves), (unsigned)pick->block, a,
                   stream);
   }
-  snprintf(name, sizeof name, "g950_rr_loop_%s_%s", op, rr_dtype(dt));
-  return launch(m, name, (unsigned)a.rows, 256u, a, stream);
+  return launch_split_rows(m, op, a, dt, v, stream);
 }
 
 int row_common(const View& x, const View& y) {
@@ -752,6 +804,11 @@ const char* g950_last_error(void) { return t_error.c_str(); }
 
 void g950_close(g950_module* m) {
   if (!m) return;
+  for (auto& kv : m->ws)
+    if (kv.second.first) {
+      (void)hipStreamSynchronize((hipStream_t)kv.first);
+      (void)hipFree(kv.second.first);
+    }
   if (m->mod) hipModuleUnload(m->mod);
   delete m;
 }

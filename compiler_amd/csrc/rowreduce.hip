@@ -1,9 +1,10 @@
-// Row-reduction family on gfx950: softmax, RMSNorm, LayerNorm.
+// Row-reduction family on gfx950: softmax, logsumexp, RMSNorm, LayerNorm.
 //
 // Operator semantics (reference, per row of the last axis):
 //   softmax   ops/suite/perf/softmax.py:21-32 (masked tail reads -inf,
-//             contributes exp(-inf)=0), online form for long rows
-//             ops/suite/dev/softmax_kernel_inner.py:12-72
+//             contributes exp(-inf)=0)
+//   logsumexp ops/suite/perf/logsumexp.py:16-38 (NaN-ignoring max plus a NaN
+//             flag; an infinite max is the result)
 //   RMSNorm   ops/suite/perf/fast_rms_layernorm.py:20-42:
 //             inv = 1/sqrt(sum(x^2)/n + eps); r[row] = inv; Y = (x*inv)*w
 //   LayerNorm ops/suite/dev/fused_layernorm_triton.py:27-42: mean; centered
@@ -20,9 +21,10 @@
 //               next row's loads are in flight while the current row is
 //               reduced.  The tail of a non-power-of-two row is a per-vector
 //               predicate; x is read from HBM once and y written once.
-//   rr_loop  -- rows longer than the register budget: scalar strided passes
-//               (softmax: online max/sum then output; norms: statistics then
-//               output), reading x two (three for LayerNorm) times.
+//   rs       -- rows longer than the register budget, or too few rows to
+//               fill the chip: each row is cut into register-resident chunks,
+//               one workgroup per chunk, partial statistics go through a small
+//               workspace and a second launch merges them and writes y.
 #include "g950_common.h"
 
 namespace g950 {
@@ -375,97 +377,210 @@ __device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
   }
 }
 
-// Long rows: strided scalar passes over global memory.
-template <int OP, typename T, int BLOCK>
-__device__ __forceinline__ void rr_loop_body(const RowArgs& a) {
-  __shared__ float scratch[BLOCK / 64];
-  const int row = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int n = a.cols;
-  const void* xrow = (const char*)a.x + (long long)row * a.x_row * (long long)sizeof(T);
-  void* yrow = (char*)a.y + (long long)row * a.y_row * (long long)sizeof(T);
-  float xv;
-  if constexpr (OP == ROW_LOGSUMEXP) {
-    float m = -__builtin_huge_valf(), z = 0.0f, nan = 0.0f;
-    for (int j = tid; j < n; j += BLOCK) {
-      load_vec<T, 1>(xrow, j, &xv);
-      if (xv != xv) {
-        nan = 1.0f;
-        continue;
+// ------------------------------------------------------------- split rows
+// Rows longer than one workgroup's registers hold, or too few rows to fill
+// the chip, are cut into chunks of RS_CHUNK_VECS vectors; one RS_BLOCK-thread
+// workgroup per (row, chunk).  Two launches, the reference's two-phase
+// split with the merge in the second (a100c/plan/stages.py:668-752):
+//   part   each workgroup reduces its register-resident chunk to a partial
+//          record in the workspace: softmax/logsumexp (max, sum of
+//          exp(x - max), NaN flag), RMSNorm (sum of squares), LayerNorm
+//          (count, chunk mean, centered M2);
+//   final  each workgroup merges its row's partials (max then rescaled sums;
+//          Chan's pairwise moments for LayerNorm, exact in the count and
+//          robust to offsets), re-reads its chunk and writes y; chunk 0 writes
+//          the row statistics.  Logsumexp's final step is one workgroup per
+//          row that only merges.
+// x is read twice (the second read mostly from the MALL for the few-row
+// shapes this path serves) and y written once.
+constexpr int RS_BLOCK = 256;
+constexpr int RS_ITEMS = 4;
+
+template <int OP, typename T, int VEC>
+__device__ __forceinline__ void rs_load(const RowArgs& a, int row, int split, float (&v)[RS_ITEMS][VEC],
+                                        bool (&ok)[RS_ITEMS]) {
+  using IO = RawIO<T, VEC>;
+  const char* xrow = (const char*)a.x + (long long)row * a.x_row * (long long)sizeof(T);
+  const int nvec = a.cols / VEC;
+  const int base = split * (RS_BLOCK * RS_ITEMS);
+  typename IO::type raw[RS_ITEMS];
+#pragma unroll
+  for (int i = 0; i < RS_ITEMS; ++i) {
+    const int j = base + threadIdx.x + i * RS_BLOCK;
+    ok[i] = j < nvec;
+    if (ok[i]) raw[i] = IO::load(xrow, (long long)j * VEC);
+  }
+#pragma unroll
+  for (int i = 0; i < RS_ITEMS; ++i) {
+    if (ok[i]) {
+      IO::unpack(raw[i], v[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        v[i][e] = (OP == ROW_SOFTMAX || OP == ROW_LOGSUMEXP) ? -__builtin_huge_valf() : 0.0f;
+    }
+  }
+}
+
+template <int OP, typename T, int VEC>
+__device__ __forceinline__ void rs_part_body(const RowArgs& a) {
+  __shared__ float scratch[RS_BLOCK / 64];
+  const int row = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+  float v[RS_ITEMS][VEC];
+  bool ok[RS_ITEMS];
+  rs_load<OP, T, VEC>(a, row, split, v, ok);
+  f32x4 p = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (OP == ROW_SOFTMAX || OP == ROW_LOGSUMEXP) {
+    float m = -__builtin_huge_valf(), nan = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RS_ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        m = fmaxf(m, v[i][e]);
+        if constexpr (OP == ROW_LOGSUMEXP) nan = (v[i][e] != v[i][e]) ? 1.0f : nan;
       }
-      const float mn = fmaxf(m, xv);
-      if (mn != -__builtin_huge_valf() && mn != __builtin_huge_valf())
-        z = z * expf(m - mn) + expf(xv - mn);
-      m = mn;
+    m = block_reduce<OpMax, RS_BLOCK>(m, scratch);
+    if constexpr (OP == ROW_LOGSUMEXP) nan = block_reduce<OpMax, RS_BLOCK>(nan, scratch);
+    // a chunk without a finite max contributes nothing to a finite row max
+    // (and must not form inf - inf); an infinite row max is handled at merge
+    float z = 0.0f;
+    if (__builtin_fabsf(m) != __builtin_huge_valf()) {
+#pragma unroll
+      for (int i = 0; i < RS_ITEMS; ++i)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) z += row_exp<T>(v[i][e] - m);
     }
-    const float mrow = block_reduce<OpMax, BLOCK>(m, scratch);
-    nan = block_reduce<OpMax, BLOCK>(nan, scratch);
-    const bool finite = __builtin_fabsf(mrow) != __builtin_huge_valf();
-    z = (finite && m != -__builtin_huge_valf()) ? z * expf(m - mrow) : 0.0f;
-    const float zrow = block_reduce<OpSum, BLOCK>(z, scratch);
-    if (tid == 0)
-      store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, lse_finish(mrow, zrow, nan != 0.0f));
-  } else if constexpr (OP == ROW_SOFTMAX) {
-    // online max/sum (softmax_kernel_inner.py:12-72): z is rescaled whenever
-    // the running max grows
-    float m = -__builtin_huge_valf(), z = 0.0f;
-    for (int j = tid; j < n; j += BLOCK) {
-      load_vec<T, 1>(xrow, j, &xv);
-      const float mn = fmaxf(m, xv);
-      z = z * expf(m - mn) + expf(xv - mn);
-      m = mn;
-    }
-    const float mrow = block_reduce<OpMax, BLOCK>(m, scratch);
-    z = (m == -__builtin_huge_valf()) ? 0.0f : z * expf(m - mrow);
-    const float zrow = block_reduce<OpSum, BLOCK>(z, scratch);
-    const float inv = 1.0f / zrow;
-    for (int j = tid; j < n; j += BLOCK) {
-      load_vec<T, 1>(xrow, j, &xv);
-      float o = expf(xv - mrow) * inv;
-      store_vec<T, 1>(yrow, j, &o);
-    }
+    z = block_reduce<OpSum, RS_BLOCK>(z, scratch);
+    p[0] = m; p[1] = z; p[2] = nan;
   } else if constexpr (OP == ROW_RMSNORM) {
     float ss = 0.0f;
-    for (int j = tid; j < n; j += BLOCK) {
-      load_vec<T, 1>(xrow, j, &xv);
-      ss = fmaf(xv, xv, ss);
-    }
-    ss = block_reduce<OpSum, BLOCK>(ss, scratch);
-    const float inv = 1.0f / sqrtf(ss / (float)n + a.eps);
-    if (tid == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, inv);
-    for (int j = tid; j < n; j += BLOCK) {
-      float w;
-      load_vec<T, 1>(xrow, j, &xv);
-      load_param<T, 1>(a.w, j, &w);
-      float o = (xv * inv) * w;
-      store_vec<T, 1>(yrow, j, &o);
-    }
+#pragma unroll
+    for (int i = 0; i < RS_ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ss = fmaf(v[i][e], v[i][e], ss);
+    p[0] = block_reduce<OpSum, RS_BLOCK>(ss, scratch);
   } else {
+    const int first = split * (RS_BLOCK * RS_ITEMS * VEC);
+    const float n = (float)min(RS_BLOCK * RS_ITEMS * VEC, a.cols - first);
     float s = 0.0f;
-    for (int j = tid; j < n; j += BLOCK) {
-      load_vec<T, 1>(xrow, j, &xv);
-      s += xv;
-    }
-    const float mean = block_reduce<OpSum, BLOCK>(s, scratch) / (float)n;
+#pragma unroll
+    for (int i = 0; i < RS_ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += v[i][e];
+    const float mean = block_reduce<OpSum, RS_BLOCK>(s, scratch) / n;
     float q = 0.0f;
-    for (int j = tid; j < n; j += BLOCK) {
-      load_vec<T, 1>(xrow, j, &xv);
-      const float c = xv - mean;
-      q = fmaf(c, c, q);
+#pragma unroll
+    for (int i = 0; i < RS_ITEMS; ++i)
+      if (ok[i]) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float c = v[i][e] - mean;
+          q = fmaf(c, c, q);
+        }
+      }
+    p[0] = n; p[1] = mean; p[2] = block_reduce<OpSum, RS_BLOCK>(q, scratch);
+  }
+  if (threadIdx.x == 0) ((f32x4*)a.part)[blockIdx.x] = p;
+}
+
+// Merge the partial records of one row (all RS_BLOCK threads take part).
+// softmax / logsumexp: (max, sum at that max, NaN); norms: (statistic 0, 1).
+template <int OP>
+__device__ __forceinline__ f32x4 rs_merge(const RowArgs& a, int row, float* scratch) {
+  const f32x4* part = (const f32x4*)a.part + (long long)row * a.splits;
+  f32x4 r = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (OP == ROW_SOFTMAX || OP == ROW_LOGSUMEXP) {
+    float m = -__builtin_huge_valf(), nan = 0.0f;
+    for (int k = threadIdx.x; k < a.splits; k += RS_BLOCK) {
+      m = fmaxf(m, part[k][0]);
+      nan = fmaxf(nan, part[k][2]);
     }
-    q = block_reduce<OpSum, BLOCK>(q, scratch);
-    const float rstd = 1.0f / sqrtf(q / (float)n + a.eps);
-    if (tid == 0) {
-      store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mean);
-      store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, rstd);
+    m = block_reduce<OpMax, RS_BLOCK>(m, scratch);
+    nan = block_reduce<OpMax, RS_BLOCK>(nan, scratch);
+    float z = 0.0f;
+    for (int k = threadIdx.x; k < a.splits; k += RS_BLOCK) {
+      const f32x4 q = part[k];
+      if constexpr (OP == ROW_LOGSUMEXP) {
+        if (__builtin_fabsf(m) != __builtin_huge_valf() && q[0] != -__builtin_huge_valf())
+          z += q[1] * expf(q[0] - m);
+      } else {
+        // the reference's single-pass arithmetic: an all -inf or +inf row
+        // ends in NaN, a finite row ignores its all -inf chunks
+        z += (q[0] == -__builtin_huge_valf() && m != -__builtin_huge_valf()) ? 0.0f : q[1] * expf(q[0] - m);
+      }
     }
-    for (int j = tid; j < n; j += BLOCK) {
-      float w, bb;
-      load_vec<T, 1>(xrow, j, &xv);
-      load_param<T, 1>(a.w, j, &w);
-      load_param<T, 1>(a.b, j, &bb);
-      float o = (xv - mean) * rstd * w + bb;
-      store_vec<T, 1>(yrow, j, &o);
+    r[0] = m; r[1] = block_reduce<OpSum, RS_BLOCK>(z, scratch); r[2] = nan;
+  } else if constexpr (OP == ROW_RMSNORM) {
+    float ss = 0.0f;
+    for (int k = threadIdx.x; k < a.splits; k += RS_BLOCK) ss += part[k][0];
+    r[0] = block_reduce<OpSum, RS_BLOCK>(ss, scratch);
+  } else {
+    // Chan et al.: mean = sum(n_k mean_k) / n; M2 = sum(M2_k + n_k (mean_k - mean)^2)
+    float s = 0.0f;
+    for (int k = threadIdx.x; k < a.splits; k += RS_BLOCK) s += part[k][0] * part[k][1];
+    const float mean = block_reduce<OpSum, RS_BLOCK>(s, scratch) / (float)a.cols;
+    float q = 0.0f;
+    for (int k = threadIdx.x; k < a.splits; k += RS_BLOCK) {
+      const float d = part[k][1] - mean;
+      q += part[k][2] + part[k][0] * d * d;
+    }
+    r[0] = mean; r[1] = block_reduce<OpSum, RS_BLOCK>(q, scratch);
+  }
+  return r;
+}
+
+template <int OP, typename T, int VEC>
+__device__ __forceinline__ void rs_final_body(const RowArgs& a) {
+  __shared__ float scratch[RS_BLOCK / 64];
+  if constexpr (OP == ROW_LOGSUMEXP) {
+    const int row = blockIdx.x;
+    const f32x4 r = rs_merge<OP>(a, row, scratch);
+    if (threadIdx.x == 0)
+      store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, lse_finish(r[0], r[1], r[2] != 0.0f));
+  } else {
+    const int row = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+    float v[RS_ITEMS][VEC];
+    bool ok[RS_ITEMS];
+    rs_load<OP, T, VEC>(a, row, split, v, ok);  // in flight during the merge
+    const f32x4 r = rs_merge<OP>(a, row, scratch);
+    void* yrow = (char*)a.y + (long long)row * a.y_row * (long long)sizeof(T);
+    const int base = split * (RS_BLOCK * RS_ITEMS);
+    float mul = 1.0f, sub = 0.0f;
+    if constexpr (OP == ROW_SOFTMAX) {
+      sub = r[0];
+      mul = 1.0f / r[1];
+    } else if constexpr (OP == ROW_RMSNORM) {
+      mul = 1.0f / sqrtf(r[0] / (float)a.cols + a.eps);
+      if (split == 0 && threadIdx.x == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mul);
+    } else {
+      sub = r[0];
+      mul = 1.0f / sqrtf(r[1] / (float)a.cols + a.eps);
+      if (split == 0 && threadIdx.x == 0) {
+        store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, sub);
+        store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, mul);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RS_ITEMS; ++i) {
+      if (!ok[i]) continue;
+      const int j = base + threadIdx.x + i * RS_BLOCK;
+      float o[VEC];
+      if constexpr (OP == ROW_SOFTMAX) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = row_exp<T>(v[i][e] - sub) * mul;
+      } else if constexpr (OP == ROW_RMSNORM) {
+        float w[VEC];
+        load_param<T, VEC>(a.w, (long long)j * VEC, w);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] * mul) * w[e];
+      } else {
+        float w[VEC], bb[VEC];
+        load_param<T, VEC>(a.w, (long long)j * VEC, w);
+        load_param<T, VEC>(a.b, (long long)j * VEC, bb);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] - sub) * mul * w[e] + bb[e];
+      }
+      store_vec<T, VEC>(yrow, (long long)j * VEC, o);
     }
   }
 }
@@ -473,19 +588,24 @@ __device__ __forceinline__ void rr_loop_body(const RowArgs& a) {
 }  // namespace g950
 
 // ------------------------------------------------------------------ symbols
-// Kernel names: g950_rr_<op>_<dtype>_v<VEC>_i<ITEMS>_b<BLOCK> and
-// g950_rr_loop_<op>_<dtype>.  The launcher (g950rt.cpp) picks the smallest
-// register configuration whose BLOCK*ITEMS*VEC covers the row.
+// Kernel names: g950_rr_<op>_<dtype>_v<VEC>_i<ITEMS>_b<BLOCK> and the split
+// pair g950_rs_{part,final}_<op>_<dtype>_v<VEC>.  The launcher (g950rt.cpp)
+// picks the smallest register configuration whose BLOCK*ITEMS*VEC covers the
+// row, or the split pair for long rows and for too few rows.
 #define G950_RR_REGS(OPNAME, OP, TNAME, T, VEC, ITEMS, BLOCK)                              \
   extern "C" __global__ __launch_bounds__(BLOCK) void                                    \
       g950_rr_##OPNAME##_##TNAME##_v##VEC##_i##ITEMS##_b##BLOCK(const g950::RowArgs a) { \
     g950::rr_regs_body<OP, T, VEC, ITEMS, BLOCK>(a);                                     \
   }
 
-#define G950_RR_LOOP(OPNAME, OP, TNAME, T)                                                 \
-  extern "C" __global__ __launch_bounds__(256) void g950_rr_loop_##OPNAME##_##TNAME(       \
-      const g950::RowArgs a) {                                                             \
-    g950::rr_loop_body<OP, T, 256>(a);                                                     \
+#define G950_RS(OPNAME, OP, TNAME, T, VEC)                                                       \
+  extern "C" __global__ __launch_bounds__(g950::RS_BLOCK) void                                      \
+      g950_rs_part_##OPNAME##_##TNAME##_v##VEC(const g950::RowArgs a) {                             \
+    g950::rs_part_body<OP, T, VEC>(a);                                                              \
+  }                                                                                                 \
+  extern "C" __global__ __launch_bounds__(g950::RS_BLOCK) void                                      \
+      g950_rs_final_##OPNAME##_##TNAME##_v##VEC(const g950::RowArgs a) {                            \
+    g950::rs_final_body<OP, T, VEC>(a);                                                             \
   }
 
 // register configurations: (VEC, ITEMS, BLOCK).  Vector forms need
@@ -507,9 +627,12 @@ __device__ __forceinline__ void rr_loop_body(const RowArgs& a) {
   G950_RR_SET(OPNAME, OP, bf16, g950::bf16_t, 1)                         \
   G950_RR_SET(OPNAME, OP, f16, g950::f16_t, 8)                           \
   G950_RR_SET(OPNAME, OP, f16, g950::f16_t, 1)                           \
-  G950_RR_LOOP(OPNAME, OP, f32, float)                                   \
-  G950_RR_LOOP(OPNAME, OP, bf16, g950::bf16_t)                           \
-  G950_RR_LOOP(OPNAME, OP, f16, g950::f16_t)
+  G950_RS(OPNAME, OP, f32, float, 4)                                     \
+  G950_RS(OPNAME, OP, f32, float, 1)                                     \
+  G950_RS(OPNAME, OP, bf16, g950::bf16_t, 8)                             \
+  G950_RS(OPNAME, OP, bf16, g950::bf16_t, 1)                             \
+  G950_RS(OPNAME, OP, f16, g950::f16_t, 8)                               \
+  G950_RS(OPNAME, OP, f16, g950::f16_t, 1)
 
 G950_RR_ALL(softmax, g950::ROW_SOFTMAX)
 G950_RR_ALL(rmsnorm, g950::ROW_RMSNORM)

@@ -100,7 +100,12 @@ def softmax_args(rows, cols, dtype):
     (8191, 3000, rt.DT_BF16, "g950_rr_softmax_bf16_v8_i6_b64"),
     (4, 97, rt.DT_F32, "g950_rr_softmax_f32_v1_i2_b64"),
     (4, 16, rt.DT_F16, "g950_rr_softmax_f16_v8_i1_b64"),
-    (2, 100000, rt.DT_F32, "g950_rr_loop_softmax_f32"),
+    (2, 100000, rt.DT_F32, "g950_rs_final_softmax_f32_v4"),
+    (3, 70001, rt.DT_F32, "g950_rs_final_softmax_f32_v1"),
+    (1, 1 << 20, rt.DT_BF16, "g950_rs_final_softmax_bf16_v8"),
+    (4, 16384, rt.DT_F32, "g950_rs_final_softmax_f32_v4"),     # few rows: split
+    (4, 4096, rt.DT_F32, "g950_rr_softmax_f32_v4_i16_b64"),    # one chunk: no split
+    (200, 16384, rt.DT_F32, "g950_rr_softmax_f32_v4_i16_b256"),  # enough rows
 ])
 def test_softmax_kernel_selection(rows, cols, dtype, kernel):
     rc, name, err = validate(rt.OP_SOFTMAX, softmax_args(rows, cols, dtype), [cols])
@@ -125,7 +130,7 @@ def test_softmax_refusals():
     (4, 16, rt.DT_F32, rt.DT_F32, "g950_rr_logsumexp_f32_v4_i1_b64"),
     (64, 1024, rt.DT_BF16, rt.DT_F32, "g950_rr_logsumexp_bf16_v8_i2_b64"),
     (4, 97, rt.DT_F16, rt.DT_F16, "g950_rr_logsumexp_f16_v1_i2_b64"),
-    (2, 100000, rt.DT_F32, rt.DT_F32, "g950_rr_loop_logsumexp_f32"),
+    (2, 100000, rt.DT_F32, rt.DT_F32, "g950_rs_final_logsumexp_f32_v4"),
 ])
 def test_logsumexp_contract(rows, cols, dtype, ydt, kernel):
     a = Args().view([rows, cols], dtype).view([rows], ydt, output=True)
