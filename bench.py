@@ -274,6 +274,61 @@ def suite(torch, ops):
     del q, k, v, o, lse
     torch.cuda.empty_cache()
 
+    # varlen attention (flash_varlen_fwd_kernel): 8 sequences of 4096 - 256 i
+    # tokens (q = k lengths, causal), 32 query / 8 KV heads, d 128, bf16;
+    # contiguous and paged (64-token pages, shuffled) K/V
+    lens = [4096 - 256 * i for i in range(8)]
+    tq = sum(lens)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    qv = torch.randn((tq, 32, 128), device=dev, generator=g).mul_(0.5).to(torch.bfloat16)
+    kv = torch.randn((tq, 8, 128), device=dev, generator=g).mul_(0.5).to(torch.bfloat16)
+    vv = torch.randn((tq, 8, 128), device=dev, generator=g).to(torch.bfloat16)
+    ov = torch.empty_like(qv)
+    lsev = torch.empty((32, tq), device=dev)
+    pages = [(n + 63) // 64 for n in lens]
+    perm = torch.randperm(sum(pages), device=dev, generator=g)
+    table = torch.zeros((8, max(pages)), dtype=torch.int32, device=dev)
+    kp = torch.empty((sum(pages) * 64, 8, 128), dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    nxt = 0
+    for b, n in enumerate(lens):
+        for pg in range(pages[b]):
+            ph = int(perm[nxt]); nxt += 1
+            table[b, pg] = ph
+            lo, hi = pg * 64, min(n, pg * 64 + 64)
+            kp[ph * 64:ph * 64 + hi - lo] = kv[int(cu[b]) + lo:int(cu[b]) + hi]
+            vp[ph * 64:ph * 64 + hi - lo] = vv[int(cu[b]) + lo:int(cu[b]) + hi]
+    used = torch.tensor(lens, dtype=torch.int32, device=dev)
+    zero1 = torch.zeros(1, device=dev)
+    philox = torch.zeros(2, dtype=torch.int64, device=dev)
+    scal = dict(q_row_stride=32 * 128, k_row_stride=8 * 128, v_row_stride=8 * 128, q_head_stride=128,
+                k_head_stride=128, v_head_stride=128, o_row_stride=32 * 128, o_head_stride=128, q_batch_stride=0,
+                k_batch_stride=0, v_batch_stride=0, o_batch_stride=0, is_cu_seqlens_q=True,
+                is_cu_seqlens_k=True, is_seqused_k=False, b=8, bk=8, h=32, hk=8, h_hk_ratio=4, seqlen_q=4096,
+                seqlen_k=4096, seqlen_q_rounded=4096, seqlen_k_rounded=4096, d=128, is_softcap=False,
+                softcap=0.0, scale_softmax=1 / math.sqrt(128), scale_softmax_log2=math.log2(math.e) / math.sqrt(128),
+                is_dropout=False, p_dropout=1.0, rp_dropout=1.0, p_dropout_in_uint8_t=255, return_softmax=False,
+                is_causal=True, is_local=False, window_size_left=-1, window_size_right=0,
+                seqlenq_ngroups_swapped=False, is_paged=False, is_alibi=False, alibi_slopes_batch_stride=0,
+                total_q=tq, page_table_batch_stride=0, block_size=1, k_page_stride=0)
+    ptrs = dict(q_ptr=qv, k_ptr=kv, v_ptr=vv, o_ptr=ov, p_ptr=zero1, softmax_lse_ptr=lsev, cu_seqlens_q_ptr=cu,
+                cu_seqlens_k_ptr=cu, seqused_k_ptr=used, philox_args=philox, alibi_slopes_ptr=zero1,
+                page_table_ptr=table)
+    flops = sum(4.0 * 32 * 128 * n * (n + 1) / 2 for n in lens)
+    for name, extra in (("F varlen causal GQA bf16 (8 seqs 4096..2304, 32/8, d128)", {}),
+                        ("F varlen paged(64) causal GQA bf16 (same)",
+                         dict(k_ptr=kp, v_ptr=vp, is_paged=True, is_cu_seqlens_k=False, is_seqused_k=True,
+                              page_table_batch_stride=max(pages), block_size=64, k_page_stride=64 * 8 * 128))):
+        call = ops.flash_varlen_fwd_kernel(**{**ptrs, **scal, **extra}, prepare=True)
+        ms = event_time(torch, lambda i: call(), 10, 2, warm_s=0.5)
+        tf = flops / (ms * 1e-3) / 1e12
+        out.append({"config": name, "kernel": call.kernel, "us": round(ms * 1e3, 1), "value": round(tf, 1),
+                    "unit": "TFLOP/s", "bound": "mfma", "frac": round(tf / BF16_PEAK_TFS, 4)})
+    del qv, kv, vv, ov, lsev, kp, vp
+    torch.cuda.empty_cache()
+
     # C5: int8 GEMM 4096x8192x8192 + dequant
     c = inputs.config5()
     a = torch.from_numpy(c["a"]).to(dev)

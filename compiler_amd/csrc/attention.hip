@@ -124,12 +124,70 @@ __device__ __forceinline__ void read_tr8(uint32_t base, u32x2 (&v)[8]) {
       : "memory");
 }
 
+// Rows of sequence z of a variable-length batch (flash_varlen_fwd_kernel.py:
+// 24-52): cu_seqlens row starts or fixed lengths with batch strides, and
+// seqused_k overriding the key count; paged K/V carries no key offset (the
+// page table addresses the keys, :99-117).  Device-held values that would
+// address outside the views make the sequence empty (no rows, no keys).
+struct SeqGeom {
+  long long q_off, k_off, v_off, o_off, lse_off;  // elements
+  int q_len, k_len;
+};
+
+__device__ __forceinline__ SeqGeom varlen_geom(const AttnArgs& p, const VarlenArgs& vl, int z) {
+  SeqGeom g;
+  if (vl.cu_q) {
+    const int b0 = vl.cu_q[z], b1 = vl.cu_q[z + 1];
+    g.q_len = b1 - b0;
+    if (b0 < 0 || g.q_len < 0 || (long long)b1 > vl.q_rows || b1 > vl.total_q) g.q_len = 0;
+    g.q_off = (long long)b0 * p.q_ss;
+    g.o_off = (long long)b0 * p.o_ss;
+    g.lse_off = b0;
+  } else {
+    g.q_len = p.Sq;
+    g.q_off = z * vl.q_bs;
+    g.o_off = z * vl.o_bs;
+    g.lse_off = (long long)z * p.Sq;
+  }
+  int kcache, kbos = 0;
+  if (vl.cu_k) {
+    kbos = vl.cu_k[z];
+    kcache = vl.cu_k[z + 1] - kbos;
+    g.k_off = (long long)kbos * p.k_ss;
+    g.v_off = (long long)kbos * p.v_ss;
+  } else {
+    kcache = p.Sk;
+    g.k_off = z * vl.k_bs;
+    g.v_off = z * vl.v_bs;
+  }
+  g.k_len = vl.used_k ? vl.used_k[z] : kcache;
+  if (vl.page_table) {
+    g.k_off = g.v_off = 0;
+    if (g.k_len < 0) g.k_len = 0;
+  } else if (vl.cu_k ? (kbos < 0 || g.k_len < 0 || (long long)kbos + g.k_len > vl.k_rows)
+                     : (g.k_len < 0 || g.k_len > p.Sk)) {
+    g.k_len = 0;
+  }
+  return g;
+}
+
+// Offset (elements, past the head offset) of key j's row in K (and, with
+// pages, in V): the page table entry of its page with K's page and row
+// strides for both (flash_varlen_fwd_kernel.py:101-104); entries outside the
+// table or the pool read page 0.
+__device__ __forceinline__ long long paged_row(const VarlenArgs& vl, int z, int j, long long row_stride) {
+  const long long e = (long long)z * vl.pt_stride + j / vl.block_size;
+  int ph = e < vl.pt_elems ? vl.page_table[e] : 0;
+  if (ph < 0 || ph >= vl.pages) ph = 0;
+  return (long long)ph * vl.page_stride + (long long)(j % vl.block_size) * row_stride;
+}
+
 // NW waves x 32 queries of one (z, q-head); key tiles of 64 in a 3-stage LDS
 // ring.  Iteration j: wait for this wave's DMA of tile j+1; barrier; issue
 // the DMA of tile j+2; issue the S^T MFMAs of tile j+1; online softmax of
 // tile j on the VALU while those MFMAs execute; O^T += V^T.P^T for tile j.
-template <int D, bool F16, int NW>
-__device__ __forceinline__ void attn_body(const AttnArgs& p) {
+template <int D, bool F16, int NW, bool VL>
+__device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* vl) {
   using C = AttnCfg<D, NW>;
   __shared__ __attribute__((aligned(1024))) char lds[ATT_STAGES * C::STAGE];
   if (blockDim.x != C::NT) return;  // launch shape must match the instantiation
@@ -161,27 +219,53 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
   }
   const int hk = h / G;
 
-  const char* qbase = (const char*)p.q + 2 * ((long long)z * p.q_sz + (long long)h * p.q_sh);
-  const char* kbase = (const char*)p.k + 2 * ((long long)z * p.k_sz + (long long)hk * p.k_sh);
-  const char* vbase = (const char*)p.v + 2 * ((long long)z * p.v_sz + (long long)hk * p.v_sh);
-
+  // ---- sequence geometry: element offsets of this (z, head)'s rows, lengths,
+  // and the key window of query row i: keys <= i + hi_off (has_hi) and
+  // >= i + lo_off (has_lo).  Fixed-length attention: causal is key <= query.
   const int q0 = qb * C::BQ;
+  long long q_off, k_off, v_off, o_off, lse_off;
+  int Sq = p.Sq, Sk = p.Sk;
+  bool has_hi = p.causal, has_lo = false;
+  int hi_off = 0, lo_off = 0;
+  if constexpr (VL) {
+    const SeqGeom sg = varlen_geom(p, *vl, z);
+    q_off = sg.q_off; k_off = sg.k_off; v_off = sg.v_off; o_off = sg.o_off; lse_off = sg.lse_off;
+    Sq = sg.q_len;
+    Sk = sg.k_len;
+    if (q0 >= Sq) return;  // whole workgroup past this sequence's queries
+    has_hi = p.causal || vl->local;
+    has_lo = vl->local;
+    hi_off = Sk - Sq + vl->wr;
+    lo_off = Sk - Sq - vl->wl;
+  } else {
+    q_off = (long long)z * p.q_sz;
+    k_off = (long long)z * p.k_sz;
+    v_off = (long long)z * p.v_sz;
+    o_off = (long long)z * p.o_sz;
+    lse_off = (long long)z * p.lse_sz;
+  }
+  const char* qbase = (const char*)p.q + 2 * (q_off + (long long)h * p.q_sh);
+  const char* kbase = (const char*)p.k + 2 * (k_off + (long long)hk * p.k_sh);
+  const char* vbase = (const char*)p.v + 2 * (v_off + (long long)hk * p.v_sh);
+
   const int qw = q0 + wave * 32;  // first query of this wave
   const int my_q = qw + r;        // this lane's query
-  const int q_last_block = min(q0 + C::BQ, p.Sq) - 1;
+  const int q_last_block = min(q0 + C::BQ, Sq) - 1;
 
   // ---- Q fragment (B port of S^T = K.Q^T): lane holds Q[my_q][16*ks + 8*g .. +8]
   u32x4 qf[C::DSTEPS];
   {
-    const int qrow = min(my_q, p.Sq - 1);
+    const int qrow = min(my_q, Sq - 1);
     const char* src = qbase + 2 * (long long)qrow * p.q_ss;
 #pragma unroll
     for (int ks = 0; ks < C::DSTEPS; ++ks) qf[ks] = *(const u32x4*)(src + (ks * 16 + g * 8) * 2);
   }
 
-  int kend = p.Sk;
-  if (p.causal) kend = min(kend, q_last_block + 1);
-  const int ntiles = (kend + ATT_BK - 1) / ATT_BK;
+  int kend = Sk;
+  if (has_hi) kend = min(kend, q_last_block + hi_off + 1);
+  // first key tile: 0, or the left window edge of the block's first query
+  const int kbeg = has_lo ? (max(0, q0 + lo_off) / ATT_BK) * ATT_BK : 0;
+  const int ntiles = kend > kbeg ? (kend - kbeg + ATT_BK - 1) / ATT_BK : 0;
 
   // ---- DMA of one K+V tile: wave-instruction d (0..2*DMAS-1) fills 1 KiB,
   // dealt round-robin over the waves.  K instruction d = (slab ks, key half
@@ -206,23 +290,52 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
       dcol[u] = (dv >> 2) * 64 + (lane & 3) * 16;
     }
   }
+  // Pages of a multiple of 64 keys hold whole tiles: one uniform page-table
+  // read per tile, issued one DMA round ahead so its latency is hidden.
+  const bool tile_pages = VL && vl->page_table && vl->tile_pages;
+  auto tile_page = [&](int t) -> long long {
+    if (!tile_pages || t >= ntiles) return 0;
+    const long long e = (long long)z * vl->pt_stride + (kbeg + t * ATT_BK) / vl->block_size;
+    int ph = e < vl->pt_elems ? vl->page_table[e] : 0;
+    if (ph < 0 || ph >= vl->pages) ph = 0;
+    return (long long)ph * vl->page_stride * 2 - (long long)((kbeg + t * ATT_BK) / vl->block_size) *
+                                                     vl->block_size * kstride;
+  };
+  long long page_next = tile_page(0);  // byte shift of tile 0's page
   auto dma_tile = [&](int t) {
     char* stage = lds + (t % ATT_STAGES) * C::STAGE;
-    const int kv0 = t * ATT_BK;
-    const bool tail = kv0 + ATT_BK > p.Sk;
+    const int kv0 = kbeg + t * ATT_BK;
+    const bool tail = kv0 + ATT_BK > Sk;
+    long long page_shift = 0;
+    if constexpr (VL) {
+      if (tile_pages) {
+        page_shift = page_next;
+        page_next = tile_page(t + 1);
+      }
+    }
 #pragma unroll
     for (int u = 0; u < C::DMA_PER_WAVE; ++u) {
       const bool is_k = u < C::DMA_PER_WAVE / 2;
       const char* base = is_k ? kbase : vbase;
       const long long stride = is_k ? kstride : vstride;
-      const int key = tail ? min(kv0 + dkey[u], p.Sk - 1) : kv0 + dkey[u];
+      const int key = tail ? min(kv0 + dkey[u], Sk - 1) : kv0 + dkey[u];
       const char* src = base + key * stride + dcol[u];
+      if constexpr (VL) {
+        // page rows use K's row stride for K and V (flash_varlen_fwd_kernel.py:101-104)
+        if (tile_pages) src = base + page_shift + key * kstride + dcol[u];
+        else if (vl->page_table) src = base + 2 * paged_row(*vl, z, key, p.k_ss) + dcol[u];
+      }
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                        (__attribute__((address_space(3))) void*)(stage + (wave + u * NW) * 1024),
                                        16, 0, 0);
     }
   };
-  auto active = [&](int t) { return !(p.causal && t * ATT_BK > qw + 31) && (qw < p.Sq); };
+  auto active = [&](int t) {
+    const int kv0 = kbeg + t * ATT_BK;
+    const int qlast = VL ? min(qw + 31, Sq - 1) : qw + 31;
+    if (qw >= Sq || (has_hi && kv0 > qlast + hi_off)) return false;
+    return !(has_lo && kv0 + ATT_BK - 1 < qw + lo_off);
+  };
   // S^T tile (2 blocks of 32 keys) from the K tile of tile t; lane (g, r)
   // reads 16 B of key kb*32 + r in slab ks at ks*2048 + kb*1024 + k_lane
   const int k_lane = r * 32 + ((g ^ ((r >> 3) & 1)) << 4);
@@ -281,8 +394,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
   };
 
   auto consume = [&](int t, f32x16* s) {
-    const int kv0 = t * ATT_BK;
-    const bool need_mask = (p.causal && kv0 + ATT_BK - 1 > qw) || (kv0 + ATT_BK > p.Sk);
+    const int kv0 = kbeg + t * ATT_BK;
+    const bool need_mask = (has_hi && kv0 + ATT_BK - 1 > qw + hi_off) || (has_lo && kv0 < qw + 31 + lo_off) ||
+                           (kv0 + ATT_BK > Sk);
     if (need_mask) {
       // key kv0 + 32kb + 8(vv>>2) + 4g + (vv&3) is kept iff its in-tile
       // offset 32kb + 8(vv>>2) + (vv&3) <= thr (one compare per score)
@@ -291,7 +405,8 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
 #pragma unroll
         for (int vv = 0; vv < 16; ++vv) {
           const int key = kv0 + kb * 32 + 8 * (vv >> 2) + 4 * g + (vv & 3);
-          if (key >= p.Sk || (p.causal && key > my_q)) s[kb][vv] = -__builtin_huge_valf();
+          if (key >= Sk || (has_hi && key > my_q + hi_off) || (has_lo && key < my_q + lo_off))
+            s[kb][vv] = -__builtin_huge_valf();
         }
     }
     float mt = fmaxf(s[0][0], s[0][1]);
@@ -304,7 +419,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
     const bool move = mt > ms + 8.0f;
     if (__any(move)) {
       const float ms_new = move ? mt : ms;
-      const float alpha = __builtin_amdgcn_exp2f(ms - ms_new);  // 0 on the first tile
+      // 0 on a row's first keys; 1 on rows that keep their reference (also a
+      // row with no visible key yet, ms = -inf, beside rows that moved)
+      const float alpha = move ? __builtin_amdgcn_exp2f(ms - ms_new) : 1.0f;
       l_run *= alpha;
 #pragma unroll
       for (int b = 0; b < C::DBLK; ++b) oacc[b] *= alpha;
@@ -399,8 +516,8 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
   };
   // interior tiles: below every wave's diagonal (causal) and inside Sk, with
   // a successor tile; rounded down to even so both loops start on sa
-  int full = (p.causal ? q0 : p.Sk) / ATT_BK;
-  full = min(min(full, p.Sk / ATT_BK), ntiles - 1);
+  int full = has_lo ? 0 : has_hi ? max(0, q0 + hi_off + 1) / ATT_BK : Sk / ATT_BK;
+  full = min(min(full, Sk / ATT_BK), ntiles - 1);
   const int nfast = full > 0 ? (full & ~1) : 0;
   int t = 0;
   for (; t < nfast; t += 2) {
@@ -416,10 +533,10 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
 
   // ---- epilogue: O = O / l ; lse = (ms + log2 l) * ln2
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (my_q < p.Sq) {
+  if (my_q < Sq) {
     const bool empty = !(l_tot > 0.0f);  // zero or NaN
     const float inv = empty ? 1.0f : 1.0f / l_tot;
-    char* orow = (char*)p.o + 2 * ((long long)z * p.o_sz + (long long)h * p.o_sh + (long long)my_q * p.o_ss);
+    char* orow = (char*)p.o + 2 * (o_off + (long long)h * p.o_sh + (long long)my_q * p.o_ss);
 #pragma unroll
     for (int b = 0; b < C::DBLK; ++b)
 #pragma unroll
@@ -436,7 +553,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p) {
       }
     if (p.lse && g == 0) {
       const float lse = empty ? __builtin_huge_valf() : (ms + __log2f(l_tot)) * 0.69314718055994530942f;
-      p.lse[(long long)z * p.lse_sz + (long long)h * p.lse_sh + (long long)my_q * p.lse_ss] = lse;
+      p.lse[lse_off + (long long)h * p.lse_sh + (long long)my_q * p.lse_ss] = lse;
     }
   }
 }
@@ -489,11 +606,68 @@ __device__ __forceinline__ void attn_general_body(const AttnGenArgs& g) {
   }
 }
 
+// Variable-length attention, any float dtype and head dim: one thread per
+// query row (grid over batch x heads x seqlen_q rows), two passes over the
+// row's key window.
+__device__ __forceinline__ void attn_varlen_general_body(const AttnVarArgs& g) {
+  const AttnArgs& p = g.a;
+  const VarlenArgs& vl = g.v;
+  const long long row = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= (long long)p.Z * p.Hq * p.Sq) return;
+  const int qi = row % p.Sq;
+  const int h = (row / p.Sq) % p.Hq;
+  const int z = row / ((long long)p.Sq * p.Hq);
+  const SeqGeom sg = varlen_geom(p, vl, z);
+  if (qi >= sg.q_len) return;
+  const int hk = h / (p.Hq / p.Hkv);
+  const int dg = sg.k_len - sg.q_len;
+  const int jlo = vl.local ? max(0, qi + dg - vl.wl) : 0;
+  const int jhi = (p.causal || vl.local) ? min(sg.k_len - 1, qi + dg + vl.wr) : sg.k_len - 1;
+  const long long qo = sg.q_off + (long long)h * p.q_sh + (long long)qi * p.q_ss;
+  auto krow = [&](int j) {
+    return vl.page_table ? paged_row(vl, z, j, p.k_ss) + (long long)hk * p.k_sh
+                         : sg.k_off + (long long)hk * p.k_sh + (long long)j * p.k_ss;
+  };
+  auto vrow = [&](int j) {
+    return vl.page_table ? paged_row(vl, z, j, p.k_ss) + (long long)hk * p.v_sh
+                         : sg.v_off + (long long)hk * p.v_sh + (long long)j * p.v_ss;
+  };
+  auto score = [&](int j) {
+    const long long kb = krow(j);
+    float s = 0.0f;
+    for (int d = 0; d < g.D; ++d)
+      s = fmaf(load_as_f32(p.q, qo + d, g.dtype), load_as_f32(p.k, kb + d, g.dtype), s);
+    return s * p.scale_log2;
+  };
+  float m = -__builtin_huge_valf();
+  for (int j = jlo; j <= jhi; ++j) m = fmaxf(m, score(j));
+  const long long oo = sg.o_off + (long long)h * p.o_sh + (long long)qi * p.o_ss;
+  float l = 0.0f;
+  for (int d = 0; d < g.D; ++d) {
+    float acc = 0.0f, ld = 0.0f;
+    for (int j = jlo; j <= jhi; ++j) {
+      const float w = exp2f(score(j) - m);
+      ld += w;
+      acc = fmaf(w, load_as_f32(p.v, vrow(j) + d, g.dtype), acc);
+    }
+    l = ld;
+    store_from_f32(p.o, oo + d, g.dtype, (l > 0.0f) ? acc / l : 0.0f);
+  }
+  if (g.D == 0) {
+    for (int j = jlo; j <= jhi; ++j) l += exp2f(score(j) - m);
+  }
+  const float lse = (l > 0.0f) ? (m + log2f(l)) * 0.69314718055994530942f : __builtin_huge_valf();
+  p.lse[sg.lse_off + (long long)h * p.lse_sh + qi] = lse;
+}
+
 }  // namespace g950
 
 #define G950_ATTN(NAME, D, F16, NW)                                                     \
   extern "C" __global__ __launch_bounds__(NW * 64) void NAME(const g950::AttnArgs p) {   \
-    g950::attn_body<D, F16, NW>(p);                                                    \
+    g950::attn_body<D, F16, NW, false>(p, nullptr);                                    \
+  }                                                                                     \
+  extern "C" __global__ __launch_bounds__(NW * 64) void NAME##_varlen(const g950::AttnVarArgs p) { \
+    g950::attn_body<D, F16, NW, true>(p.a, &p.v);                                      \
   }
 // 8 waves = 256 queries per workgroup (the launcher's grid assumes this)
 G950_ATTN(g950_attn_fwd_bf16_d128, 128, false, 8)
@@ -502,4 +676,7 @@ G950_ATTN(g950_attn_fwd_f16_d128, 128, true, 8)
 G950_ATTN(g950_attn_fwd_f16_d64, 64, true, 8)
 extern "C" __global__ __launch_bounds__(64) void g950_attn_fwd_general(const g950::AttnGenArgs p) {
   g950::attn_general_body(p);
+}
+extern "C" __global__ __launch_bounds__(64) void g950_attn_varlen_general(const g950::AttnVarArgs p) {
+  g950::attn_varlen_general_body(p);
 }

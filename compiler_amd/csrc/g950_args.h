@@ -81,4 +81,34 @@ struct AttnGenArgs {
   int dtype;
 };
 
+// Variable-length attention (flash_varlen_fwd_kernel): per-batch sequences.
+// With it, AttnArgs' *_ss are the row strides, *_sh the head strides, *_sz
+// unused; Z is the batch count, Sq / Sk the fixed lengths of the non-cu modes.
+// Values read from device memory (cu_seqlens, seqused_k, page table) are
+// checked against the extents below before they address anything.
+struct VarlenArgs {
+  const int* cu_q;          // [b + 1] query row starts, or null (fixed seqlen_q)
+  const int* cu_k;          // [b + 1] key row starts, or null (fixed seqlen_k)
+  const int* used_k;        // [b] keys used per batch, or null
+  const int* page_table;    // [b * pt_stride] physical page per key page, or null
+  long long pt_stride;      // page_table_batch_stride
+  long long pt_elems;       // entries of the page-table view
+  long long page_stride;    // k_page_stride (elements)
+  long long q_bs, k_bs, v_bs, o_bs;  // batch strides of the fixed-length modes
+  long long q_rows, k_rows; // rows the q/o and k/v views hold (cu modes)
+  long long pages;          // physical pages the k/v views hold (paged mode)
+  int total_q;              // lse head stride
+  int block_size;           // keys per page
+  int tile_pages;           // block_size is a multiple of the 64-key tile
+  int local;                // is_local
+  int wl, wr;               // window_size_left / window_size_right
+};
+
+struct AttnVarArgs {
+  AttnArgs a;
+  VarlenArgs v;
+  int D;       // general kernel: head dim
+  int dtype;   // general kernel: q/k/v/o dtype
+};
+
 }  // namespace g950

@@ -17,6 +17,7 @@
 // Nothing is launched unless every check passed.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -691,6 +692,173 @@ int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const 
   return launch(m, "g950_attn_fwd_general", (unsigned)((rows + 63) / 64), 64u, ga, stream);
 }
 
+// ------------------------------------------------------ varlen attention
+// flash_varlen_fwd_kernel (ops/suite/dev/flash_varlen_fwd_kernel.py:22-320):
+// 12 pointer views (all 1-D flat buffers) and the kernel's 46 non-pointer
+// arguments with semantics (runtime scalars and constexprs; the tile-shape
+// constexprs BLOCK_M/N/K, KERNEL_NUM_WARPS, PIPELINE_STAGES, d_rounded are
+// not part of the contract), both in sorted-name order.
+const char* const kVarlenScalars[] = {
+    "alibi_slopes_batch_stride", "b", "bk", "block_size", "d", "h", "h_hk_ratio", "hk", "is_alibi",
+    "is_causal", "is_cu_seqlens_k", "is_cu_seqlens_q", "is_dropout", "is_local", "is_paged",
+    "is_seqused_k", "is_softcap", "k_batch_stride", "k_head_stride", "k_page_stride", "k_row_stride",
+    "o_batch_stride", "o_head_stride", "o_row_stride", "p_dropout", "p_dropout_in_uint8_t",
+    "page_table_batch_stride", "q_batch_stride", "q_head_stride", "q_row_stride", "return_softmax",
+    "rp_dropout", "scale_softmax", "scale_softmax_log2", "seqlen_k", "seqlen_k_rounded", "seqlen_q",
+    "seqlen_q_rounded", "seqlenq_ngroups_swapped", "softcap", "total_q", "v_batch_stride", "v_head_stride",
+    "v_row_stride", "window_size_left", "window_size_right"};
+constexpr uint32_t kVarlenNsc = sizeof(kVarlenScalars) / sizeof(kVarlenScalars[0]);
+
+int varlen_index(const char* name) {
+  for (uint32_t i = 0; i < kVarlenNsc; ++i)
+    if (!strcmp(kVarlenScalars[i], name)) return (int)i;
+  return -1;
+}
+
+// Rows a flat buffer holds for (row stride rs, heads nh at head stride hs,
+// d contiguous elements): the largest R with (R-1)*rs + (nh-1)*hs + d <= n.
+long long rows_held(long long n, long long rs, long long nh, long long hs, long long d) {
+  const long long fixed = (nh - 1) * hs + d;
+  if (n < fixed) return 0;
+  return rs > 0 ? (n - fixed) / rs + 1 : 0x7FFFFFFF;
+}
+
+int op_flash_varlen(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+                    uint32_t nsc, void* stream) {
+  if (nviews != 12 || nsc != kVarlenNsc)
+    return fail(G950_USAGE, "flash_varlen: needs 12 views (alibi_slopes_ptr .. v_ptr) and %u scalars",
+                kVarlenNsc);
+  View alibi, cuk, cuq, k, o, pp, pt, philox, q, used, lse, v;
+  const struct { View* vw; const char* name; bool out; } vs[12] = {
+      {&alibi, "alibi_slopes_ptr", false}, {&cuk, "cu_seqlens_k_ptr", false}, {&cuq, "cu_seqlens_q_ptr", false},
+      {&k, "k_ptr", false}, {&o, "o_ptr", true}, {&pp, "p_ptr", false}, {&pt, "page_table_ptr", false},
+      {&philox, "philox_args", false}, {&q, "q_ptr", false}, {&used, "seqused_k_ptr", false},
+      {&lse, "softmax_lse_ptr", true}, {&v, "v_ptr", false}};
+  for (uint32_t i = 0; i < 12; ++i)
+    if (int rc = check_view(views, i, vs[i].name, 1, *vs[i].vw, vs[i].out)) return rc;
+  long long val[kVarlenNsc];
+  double fval[kVarlenNsc];
+  for (uint32_t i = 0; i < kVarlenNsc; ++i) {
+    if (int rc = scalar_float(&sc[i], kVarlenScalars[i], fval[i])) return rc;
+    val[i] = (long long)fval[i];
+    if (sc[i].dtype != G950_DTYPE_FLOAT32 && sc[i].dtype != G950_DTYPE_FLOAT64)
+      if (int rc = scalar_int(&sc[i], kVarlenScalars[i], val[i])) return rc;
+  }
+  auto I = [&](const char* n) { return val[varlen_index(n)]; };
+  auto F = [&](const char* n) { return fval[varlen_index(n)]; };
+  for (const char* flag : {"is_softcap", "is_dropout", "return_softmax", "seqlenq_ngroups_swapped", "is_alibi"})
+    if (I(flag)) return fail(G950_USAGE, "flash_varlen: %s is not supported by this build", flag);
+  const uint32_t dt = q.v->dtype;
+  if (!is_float(dt) || k.v->dtype != dt || v.v->dtype != dt || o.v->dtype != dt)
+    return fail(G950_USAGE, "flash_varlen: q/k/v/o must share one float dtype");
+  if (lse.v->dtype != G950_DTYPE_FLOAT32) return fail(G950_USAGE, "flash_varlen: softmax_lse_ptr must be float32");
+  const long long B = I("b"), H = I("h"), HK = I("hk"), D = I("d"), SQ = I("seqlen_q"), SK = I("seqlen_k");
+  const long long TQ = I("total_q");
+  if (B < 0 || H <= 0 || HK <= 0 || D <= 0 || SQ < 0 || SK < 0 || TQ < 0 || H % HK || I("h_hk_ratio") != H / HK)
+    return fail(G950_USAGE, "flash_varlen: b/h/hk/h_hk_ratio/d/seqlen/total_q inconsistent");
+  if (B > 0x7FFFFFF || H * B > 0x7FFFFFF || SQ > 0x7FFFFFF || SK > 0x7FFFFFF || TQ > 0x7FFFFFFF || D > 4096)
+    return fail(G950_USAGE, "flash_varlen: extent too large");
+  const double scale = F("scale_softmax"), scale_log2 = F("scale_softmax_log2");
+  if (!(std::fabs(scale * 1.4426950408889634 - scale_log2) <= 1e-6 * std::fabs(scale_log2) + 1e-30))
+    return fail(G950_USAGE, "flash_varlen: scale_softmax_log2 must equal scale_softmax * log2(e)");
+  const char* strides[] = {"q_row_stride", "k_row_stride", "v_row_stride", "o_row_stride", "q_head_stride",
+                           "k_head_stride", "v_head_stride", "o_head_stride", "q_batch_stride", "k_batch_stride",
+                           "v_batch_stride", "o_batch_stride", "k_page_stride", "page_table_batch_stride"};
+  for (const char* n : strides)
+    if (I(n) < 0) return fail(G950_USAGE, "flash_varlen: %s must be >= 0", n);
+  const bool cu_q = I("is_cu_seqlens_q") != 0, cu_k = I("is_cu_seqlens_k") != 0;
+  const bool seqused = I("is_seqused_k") != 0, paged = I("is_paged") != 0, local = I("is_local") != 0;
+  const long long bs = I("block_size");
+  auto int_view = [&](const View& w, const char* name, long long need) {
+    if (w.v->dtype != G950_DTYPE_INT32) return fail(G950_USAGE, "flash_varlen: %s must be int32", name);
+    if (w.shape[0] < need) return fail(G950_USAGE, "flash_varlen: %s needs %lld entries", name, need);
+    if (w.shape[0] > 1 && w.stride[0] != 1) return fail(G950_USAGE, "flash_varlen: %s must be contiguous", name);
+    return G950_OK;
+  };
+  if (cu_q) if (int rc = int_view(cuq, "cu_seqlens_q_ptr", B + 1)) return rc;
+  if (cu_k) if (int rc = int_view(cuk, "cu_seqlens_k_ptr", B + 1)) return rc;
+  if (seqused) if (int rc = int_view(used, "seqused_k_ptr", B)) return rc;
+  for (const View* w : {&q, &k, &v, &o, &lse})
+    if (w->shape[0] > 1 && w->stride[0] != 1) return fail(G950_USAGE, "flash_varlen: %s must be contiguous", w->name);
+  // every address the kernel can form stays inside the views: rows held by
+  // q/o and k/v bound the device-held lengths, the fixed-length modes are
+  // checked here in full
+  VarlenArgs vl{};
+  const long long qe = q.shape[0], oe = o.shape[0], ke = k.shape[0], ve = v.shape[0];
+  vl.q_rows = std::min(rows_held(qe, I("q_row_stride"), H, I("q_head_stride"), D),
+                       rows_held(oe, I("o_row_stride"), H, I("o_head_stride"), D));
+  if (!cu_q && B > 0 && SQ > 0) {
+    if ((B - 1) * I("q_batch_stride") + (SQ - 1) * I("q_row_stride") + (H - 1) * I("q_head_stride") + D > qe ||
+        (B - 1) * I("o_batch_stride") + (SQ - 1) * I("o_row_stride") + (H - 1) * I("o_head_stride") + D > oe)
+      return fail(G950_USAGE, "flash_varlen: b x seqlen_q rows exceed q_ptr/o_ptr");
+    if (B * SQ > TQ) return fail(G950_USAGE, "flash_varlen: b x seqlen_q exceeds total_q");
+  }
+  if (H * TQ > lse.shape[0]) return fail(G950_USAGE, "flash_varlen: softmax_lse_ptr needs h x total_q entries");
+  if (paged) {
+    if (bs <= 0) return fail(G950_USAGE, "flash_varlen: block_size must be positive");
+    if (int rc = int_view(pt, "page_table_ptr", 1)) return rc;
+    const long long ps = I("k_page_stride"), krs = I("k_row_stride");
+    const long long kfix = (bs - 1) * krs + (HK - 1) * I("k_head_stride") + D;
+    const long long vfix = (bs - 1) * krs + (HK - 1) * I("v_head_stride") + D;
+    long long pages = 0;
+    if (ke >= kfix && ve >= vfix)
+      pages = ps > 0 ? std::min((ke - kfix) / ps, (ve - vfix) / ps) + 1 : 1;
+    vl.pages = pages;
+    vl.pt_elems = pt.shape[0];
+    vl.pt_stride = I("page_table_batch_stride");
+    vl.page_stride = ps;
+    vl.block_size = (int)bs;
+    vl.tile_pages = bs % 64 == 0 ? 1 : 0;
+    vl.page_table = (const int*)pt.v->data;
+  } else {
+    vl.k_rows = std::min(rows_held(ke, I("k_row_stride"), HK, I("k_head_stride"), D),
+                         rows_held(ve, I("v_row_stride"), HK, I("v_head_stride"), D));
+    if (!cu_k && B > 0 && SK > 0 &&
+        ((B - 1) * I("k_batch_stride") + (SK - 1) * I("k_row_stride") + (HK - 1) * I("k_head_stride") + D > ke ||
+         (B - 1) * I("v_batch_stride") + (SK - 1) * I("v_row_stride") + (HK - 1) * I("v_head_stride") + D > ve))
+      return fail(G950_USAGE, "flash_varlen: b x seqlen_k rows exceed k_ptr/v_ptr");
+  }
+  vl.cu_q = cu_q ? (const int*)cuq.v->data : nullptr;
+  vl.cu_k = cu_k ? (const int*)cuk.v->data : nullptr;
+  vl.used_k = seqused ? (const int*)used.v->data : nullptr;
+  vl.q_bs = I("q_batch_stride"); vl.k_bs = I("k_batch_stride");
+  vl.v_bs = I("v_batch_stride"); vl.o_bs = I("o_batch_stride");
+  vl.total_q = (int)TQ;
+  vl.local = local ? 1 : 0;
+  vl.wl = (int)I("window_size_left");
+  vl.wr = (int)I("window_size_right");
+  AttnArgs a{};
+  a.q = q.v->data; a.k = k.v->data; a.v = v.v->data; a.o = o.v->data;
+  a.lse = (float*)lse.v->data;
+  a.q_ss = I("q_row_stride"); a.q_sh = I("q_head_stride");
+  a.k_ss = I("k_row_stride"); a.k_sh = I("k_head_stride");
+  a.v_ss = I("v_row_stride"); a.v_sh = I("v_head_stride");
+  a.o_ss = I("o_row_stride"); a.o_sh = I("o_head_stride");
+  a.lse_sh = TQ; a.lse_ss = 1;
+  a.Z = (int)B; a.Hq = (int)H; a.Hkv = (int)HK; a.Sq = (int)SQ; a.Sk = (int)SK;
+  a.scale_log2 = (float)scale_log2;
+  a.causal = I("is_causal") ? 1 : 0;
+  AttnVarArgs va{};
+  va.a = a; va.v = vl; va.D = (int)D; va.dtype = (int)dt;
+  if (B == 0 || SQ == 0) return launch(m, "g950_attn_varlen_general", 0, 64u, va, stream);
+  auto m8 = [](long long x) { return x % 8 == 0; };
+  const bool mfma = is_float16ish(dt) && (D == 64 || D == 128) && aligned16(q.addr()) && aligned16(k.addr()) &&
+                    aligned16(v.addr()) && (o.addr() & 7) == 0 && m8(a.q_ss) && m8(a.q_sh) && m8(a.k_ss) &&
+                    m8(a.k_sh) && m8(a.v_ss) && m8(a.v_sh) && a.o_ss % 4 == 0 && a.o_sh % 4 == 0 &&
+                    m8(vl.q_bs) && m8(vl.k_bs) && m8(vl.v_bs) && vl.o_bs % 4 == 0 && (!paged || m8(vl.page_stride));
+  if (mfma) {
+    va.a.nqb = (int)((SQ + 255) / 256);
+    const long long grid = (long long)va.a.nqb * B * H;
+    if (grid > 0x7FFFFFFF) return fail(G950_USAGE, "flash_varlen: grid too large");
+    char name[64];
+    snprintf(name, sizeof name, "g950_attn_fwd_%s_d%lld_varlen", dt == G950_DTYPE_BFLOAT16 ? "bf16" : "f16", D);
+    return launch(m, name, (unsigned)grid, 512u, va, stream);
+  }
+  const long long rows = B * H * SQ;
+  if ((rows + 63) / 64 > 0x7FFFFFFF) return fail(G950_USAGE, "flash_varlen: grid too large");
+  return launch(m, "g950_attn_varlen_general", (unsigned)((rows + 63) / 64), 64u, va, stream);
+}
+
 // ------------------------------------------------------------------- copy
 int op_copy(g950_module* m, const g950_view* views, uint32_t nviews, uint32_t nsc, void* stream) {
   if (nviews != 2 || nsc != 0) return fail(G950_USAGE, "copy: needs views (x, y) and no scalars");
@@ -762,6 +930,7 @@ int dispatch(g950_module* m, uint32_t op, const g950_view* views, uint32_t nview
       case G950_OP_ATTENTION_LSE: return op_attention(m, views, nviews, scalars, nscalars, true, stream);
       case G950_OP_COPY: return op_copy(m, views, nviews, nscalars, stream);
       case G950_OP_DEQUANTIZE: return op_dequantize(m, views, nviews, scalars, nscalars, stream);
+      case G950_OP_FLASH_VARLEN: return op_flash_varlen(m, views, nviews, scalars, nscalars, stream);
       default: return fail(G950_USAGE, "g950_launch: unknown operator contract %u", op);
     }
   } catch (...) {

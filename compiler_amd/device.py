@@ -80,6 +80,11 @@ def _dequantize(a):
                           a["stride_bn"], a["stride_fpbk"], a["stride_fpbn"], sync=True)
 
 
+def _flash_varlen(a):
+    from .operators import _VARLEN_SCALARS, _VARLEN_VIEWS
+    ops.flash_varlen_fwd_kernel(**{n: a[n] for n in _VARLEN_VIEWS + _VARLEN_SCALARS}, sync=True)
+
+
 def _rms(a):
     ops.rms_layernorm_forward_kernel(a["Y"], a["Y_row_stride"], a["X"], a["X_row_stride"], a["W"],
                                      a["W_row_stride"], a["r"], a["r_row_stride"], a["n_cols"],
@@ -109,6 +114,7 @@ KERNELS = {
     "softmax_kernel": _softmax,
     "logsumexp_kernel": _logsumexp,
     "dequantize_kernel": _dequantize,
+    "flash_varlen_fwd_kernel": _flash_varlen,
     "rms_layernorm_forward_kernel": _rms,
     "layernorm_kernel": _layernorm,
     "matmul_kernel": _matmul,

@@ -59,6 +59,38 @@ def dequantize_kernel(b_ptr, b_scale_ptr, fpb_ptr, K, N, stride_bk, stride_bn, s
                    stream, sync, prepare)
 
 
+_VARLEN_VIEWS = ("q_ptr", "k_ptr", "v_ptr", "o_ptr", "p_ptr", "softmax_lse_ptr", "cu_seqlens_q_ptr",
+                 "cu_seqlens_k_ptr", "seqused_k_ptr", "philox_args", "alibi_slopes_ptr", "page_table_ptr")
+_VARLEN_SCALARS = ("q_row_stride", "k_row_stride", "v_row_stride", "q_head_stride", "k_head_stride",
+                   "v_head_stride", "o_row_stride", "o_head_stride", "q_batch_stride", "k_batch_stride",
+                   "v_batch_stride", "o_batch_stride", "is_cu_seqlens_q", "is_cu_seqlens_k", "is_seqused_k",
+                   "b", "bk", "h", "hk", "h_hk_ratio", "seqlen_q", "seqlen_k", "seqlen_q_rounded",
+                   "seqlen_k_rounded", "d", "is_softcap", "softcap", "scale_softmax", "scale_softmax_log2",
+                   "is_dropout", "p_dropout", "rp_dropout", "p_dropout_in_uint8_t", "return_softmax",
+                   "is_causal", "is_local", "window_size_left", "window_size_right", "seqlenq_ngroups_swapped",
+                   "is_paged", "is_alibi", "alibi_slopes_batch_stride", "total_q", "page_table_batch_stride",
+                   "block_size", "k_page_stride")
+# tile-shape constexprs of the reference kernel: accepted, no semantics here
+_VARLEN_TILE = ("BLOCK_M", "BLOCK_N", "BLOCK_K", "KERNEL_NUM_WARPS", "PIPELINE_STAGES", "d_rounded")
+
+
+def flash_varlen_fwd_kernel(*, stream=None, sync=False, prepare=False, **args):
+    """Variable-length attention forward (ops/suite/dev/flash_varlen_fwd_kernel.py:22-320),
+    called with the reference kernel's argument names: cu_seqlens / fixed-length
+    batches, seqused_k, GQA, causal and local windows, paged K/V.  Pointer
+    arguments are device tensors (flattened to 1-D views); softcap, dropout,
+    alibi, return_softmax and seqlenq_ngroups_swapped must be off."""
+    unknown = set(args) - set(_VARLEN_VIEWS) - set(_VARLEN_SCALARS) - set(_VARLEN_TILE)
+    if unknown:
+        raise TypeError(f"flash_varlen_fwd_kernel: unexpected arguments {sorted(unknown)}")
+    missing = [n for n in _VARLEN_VIEWS + _VARLEN_SCALARS if n not in args]
+    if missing:
+        raise TypeError(f"flash_varlen_fwd_kernel: missing arguments {missing}")
+    views = {n: args[n].reshape(-1) for n in _VARLEN_VIEWS}
+    scalars = {n: args[n] for n in _VARLEN_SCALARS}
+    return _launch(rt.OP_FLASH_VARLEN, views, {"o_ptr", "softmax_lse_ptr"}, scalars, stream, sync, prepare)
+
+
 def rms_layernorm_forward_kernel(Y, Y_row_stride, X, X_row_stride, W, W_row_stride, r,
                                  r_row_stride, n_cols, eps, *, stream=None, sync=False, prepare=False):
     """RMSNorm forward (ops/suite/perf/fast_rms_layernorm.py:20-42)."""

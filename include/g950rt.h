@@ -125,6 +125,18 @@ typedef struct g950_scalar {
  *           share one dtype (f32 | bf16 | f16)
  *   scalars K, N, stride_bk, stride_bn, stride_fpbk, stride_fpbn (element
  *           strides; must agree with the views wherever the extent exceeds 1)
+ * G950_OP_FLASH_VARLEN flash_varlen_fwd_kernel (ops/suite/dev/flash_varlen_fwd_kernel.py:22-320):
+ *                      variable-length batches (cu_seqlens_q/k, seqused_k),
+ *                      GQA, causal and local windows (bottom-right aligned),
+ *                      paged K/V; O = 0 and LSE = +inf for a row without keys
+ *   views   alibi_slopes_ptr, cu_seqlens_k_ptr i32, cu_seqlens_q_ptr i32, k_ptr,
+ *           o_ptr, p_ptr, page_table_ptr i32, philox_args, q_ptr, seqused_k_ptr i32,
+ *           softmax_lse_ptr f32 (all 1-D flat buffers; q/k/v/o share one dtype)
+ *   scalars the kernel's 46 non-pointer arguments with semantics, sorted
+ *           (alibi_slopes_batch_stride, b, bk, block_size, d, h, h_hk_ratio, hk,
+ *           is_alibi, is_causal, ... window_size_left, window_size_right);
+ *           is_softcap, is_dropout, return_softmax, seqlenq_ngroups_swapped and
+ *           is_alibi must be 0 (refused otherwise)
  */
 enum g950_op {
   G950_OP_SOFTMAX = 1,
@@ -137,7 +149,8 @@ enum g950_op {
   G950_OP_ATTENTION_LSE = 8,
   G950_OP_COPY = 9,
   G950_OP_LOGSUMEXP = 10,
-  G950_OP_DEQUANTIZE = 11
+  G950_OP_DEQUANTIZE = 11,
+  G950_OP_FLASH_VARLEN = 12
 };
 
 typedef struct g950_module g950_module;

@@ -24,6 +24,11 @@ How each function is pinned (besides restating the formula):
   * ``attention``            -- reference-held attention fixtures (non-causal) in
                                 3 dtypes; causal row 0 == V[0]; uniform V -> V;
                                 LSE of equal scores == s + log(n).
+  * ``flash_varlen``         -- per-sequence equality with ``attention`` (dense
+                                and causal, GQA); local window 0 picks V[i];
+                                huge windows == dense; permuted pages ==
+                                contiguous; seqused_k == truncated keys;
+                                brute-force loop with bottom-right causal mask.
   * ``bf16_round``           -- known bit patterns (ties-to-even, NaN quieting,
                                 overflow to inf) and torch's RNE conversion.
 """
@@ -39,6 +44,7 @@ __all__ = [
     "TOLERANCES",
     "logsumexp",
     "dequantize",
+    "flash_varlen",
 ]
 
 # Shared value tolerances per dtype (ops/harness/opslib/case.py:153-157) and the
@@ -233,6 +239,87 @@ def attention(q, k, v, scale, causal=True, block_rows=512):
 
 
 # ------------------------------------------------------------- comparison
+def flash_varlen(q, k, v, *, b, h, hk, d, scale, q_row_stride, k_row_stride, v_row_stride,
+                 q_head_stride, k_head_stride, v_head_stride, o_row_stride, o_head_stride,
+                 q_batch_stride=0, k_batch_stride=0, v_batch_stride=0, o_batch_stride=0,
+                 seqlen_q=0, seqlen_k=0, total_q=0, cu_seqlens_q=None, cu_seqlens_k=None,
+                 seqused_k=None, causal=False, local=False, window_left=-1, window_right=-1,
+                 page_table=None, page_table_batch_stride=0, block_size=1, k_page_stride=0,
+                 o, lse):
+    """Variable-length attention forward in float64 over flat buffers:
+    returns (o, lse) copies with every written position set.
+
+    Follows ops/suite/dev/flash_varlen_fwd_kernel.py:22-320: per batch ``bid``
+    the query rows are ``cu_seqlens_q[bid] ..`` (row-stride addressed) or
+    ``bid * q_batch_stride`` with ``seqlen_q`` rows (:25-36), keys likewise
+    (:37-48) with ``seqused_k`` overriding the key count (:49-52); query head
+    ``hid`` reads key head ``hid // (h // hk)`` (:69-72).  Row ``i`` sees keys
+    ``j < k_len`` with ``j <= i + k_len - q_len + window_right`` when causal or
+    local and ``j >= i + k_len - q_len - window_left`` when local (:132-145).
+    Paged K/V (:99-117): key ``j`` lives at ``page_table[bid *
+    page_table_batch_stride + j // block_size] * k_page_stride + (j %
+    block_size) * k_row_stride`` past the head offset, for K and V alike.
+    LSE = log(sum(exp(scale * s))) in natural log, at ``h * total_q +
+    (cu_seqlens_q[bid] or bid * seqlen_q) + i``; a row without keys gets O = 0
+    and LSE = +inf (:309-312).  ``o`` and ``lse`` are the flat output
+    buffers' initial contents (positions no row writes keep them).
+    """
+    q = np.asarray(q, dtype=np.float64).reshape(-1)
+    k = np.asarray(k, dtype=np.float64).reshape(-1)
+    v = np.asarray(v, dtype=np.float64).reshape(-1)
+    ratio = h // hk
+    out = np.asarray(o, dtype=np.float64).reshape(-1).copy()
+    lse_out = np.asarray(lse, dtype=np.float64).reshape(-1).copy()
+    dim = np.arange(d)
+    for bid in range(b):
+        if cu_seqlens_q is not None:
+            q_bos, q_len = int(cu_seqlens_q[bid]), int(cu_seqlens_q[bid + 1]) - int(cu_seqlens_q[bid])
+            q_off, o_off, lse_off = q_bos * q_row_stride, q_bos * o_row_stride, q_bos
+        else:
+            q_len = seqlen_q
+            q_off, o_off, lse_off = bid * q_batch_stride, bid * o_batch_stride, bid * seqlen_q
+        if cu_seqlens_k is not None:
+            k_bos = int(cu_seqlens_k[bid])
+            k_len = int(cu_seqlens_k[bid + 1]) - k_bos
+            k_off, v_off = k_bos * k_row_stride, k_bos * v_row_stride
+        else:
+            k_len = seqlen_k
+            k_off, v_off = bid * k_batch_stride, bid * v_batch_stride
+        if seqused_k is not None:
+            k_len = int(seqused_k[bid])
+        keys = np.arange(k_len)
+        if page_table is not None:
+            phys = np.asarray(page_table).reshape(-1)[bid * page_table_batch_stride + keys // block_size]
+            k_rows = phys.astype(np.int64) * k_page_stride + (keys % block_size) * k_row_stride
+            v_rows = k_rows
+        else:
+            k_rows = k_off + keys * k_row_stride
+            v_rows = v_off + keys * v_row_stride
+        rows = np.arange(q_len)
+        allowed = np.ones((q_len, k_len), dtype=bool)
+        diag = rows[:, None] + (k_len - q_len)
+        if causal or local:
+            allowed &= keys[None, :] <= diag + window_right
+        if local:
+            allowed &= keys[None, :] >= diag - window_left
+        for hid in range(h):
+            kh = hid // ratio
+            qt = q[q_off + hid * q_head_stride + rows[:, None] * q_row_stride + dim[None, :]]
+            kt = k[k_rows[:, None] + kh * k_head_stride + dim[None, :]]
+            vt = v[v_rows[:, None] + kh * v_head_stride + dim[None, :]]
+            s = np.where(allowed, (qt @ kt.T) * float(scale), -np.inf)
+            m = s.max(axis=1, keepdims=True) if k_len else np.full((q_len, 1), -np.inf)
+            m_safe = np.where(np.isfinite(m), m, 0.0)
+            p = np.exp(s - m_safe)
+            l = p.sum(axis=1, keepdims=True)
+            empty = l == 0
+            out[o_off + hid * o_head_stride + rows[:, None] * o_row_stride + dim[None, :]] = (
+                np.where(empty, 0.0, p / np.where(empty, 1.0, l)) @ vt if k_len else 0.0)
+            with np.errstate(divide="ignore"):
+                lse_out[hid * total_q + lse_off + rows] = np.where(empty[:, 0], np.inf, (m_safe + np.log(l))[:, 0])
+    return out, lse_out
+
+
 def isclose_verdict(actual, expected, rtol, atol, equal_nan=True):
     """(ok, max_abs_error) with the corpus comparator rule.
 

@@ -48,7 +48,7 @@ def test_strerror_codes():
 class Args:
     """Builds fake views (host shape/stride arrays, fake device addresses)."""
 
-    ITEM = {rt.DT_F32: 4, rt.DT_BF16: 2, rt.DT_F16: 2, rt.DT_INT8: 1, rt.DT_UINT8: 1, rt.DT_INT32: 4}
+    ITEM = {rt.DT_F32: 4, rt.DT_BF16: 2, rt.DT_F16: 2, rt.DT_INT8: 1, rt.DT_UINT8: 1, rt.DT_INT32: 4, rt.DT_INT64: 8}
 
     def __init__(self):
         self.specs = []
@@ -187,6 +187,68 @@ def test_dequantize_refusals():
     rc, name, err = validate(rt.OP_DEQUANTIZE, dq_args(32, 32, rt.DT_F32, b_strides=[1, 32]),
                              [np.int32(32), np.int32(32), np.int32(1), np.int32(32), np.int32(32), np.int32(1)])
     assert rc == 0 and name == "g950_dequant_i8_general", err
+
+
+NP_DT = {"float32": rt.DT_F32, "float16": rt.DT_F16, "bfloat16": rt.DT_BF16, "int32": rt.DT_INT32,
+         "uint64": rt.DT_UINT64}
+
+
+def varlen_validate(a, meta, dt="bfloat16", **override):
+    """g950_validate for a flash_varlen case: 12 flat views + 46 scalars, sorted."""
+    from compiler_amd.operators import _VARLEN_SCALARS, _VARLEN_VIEWS
+    merged = {**a, **meta, **override}
+    args = Args()
+    for name in sorted(_VARLEN_VIEWS):
+        arr = np.asarray(merged[name])
+        code = dt if name in ("q_ptr", "k_ptr", "v_ptr", "o_ptr") else arr.dtype.name
+        args.view([arr.size], NP_DT.get(code, rt.DT_F32) if code != "uint64" else rt.DT_INT64,
+                  output=name in ("o_ptr", "softmax_lse_ptr"))
+    scal = []
+    for name in sorted(_VARLEN_SCALARS):
+        val = merged[name]
+        scal.append(np.float32(val) if isinstance(val, float) else (np.int32(1 if val else 0)
+                    if isinstance(val, bool) else np.int32(val)))
+    return validate(rt.OP_FLASH_VARLEN, args, scal)
+
+
+def test_flash_varlen_contract():
+    from oracle import inputs
+    a, meta = inputs.varlen_case()                       # the reference case: d=16 -> general kernel
+    rc, name, err = varlen_validate(a, meta)
+    assert rc == 0 and name == "g950_attn_varlen_general", err
+    a, meta = inputs.varlen_case(batches=3, max_q=300, max_k=400, h=8, hk=2, d=128)
+    rc, name, err = varlen_validate(a, meta)
+    assert rc == 0 and name == "g950_attn_fwd_bf16_d128_varlen", err
+    rc, name, err = varlen_validate(a, meta, dt="float16")
+    assert rc == 0 and name == "g950_attn_fwd_f16_d128_varlen", err
+    a, meta = inputs.varlen_case(batches=3, max_q=64, max_k=200, h=4, hk=4, d=64, paged=True, block_size=16,
+                                 causal=True, window_right=0)
+    rc, name, err = varlen_validate(a, meta)
+    assert rc == 0 and name == "g950_attn_fwd_bf16_d64_varlen", err
+    a, meta = inputs.varlen_case(strided=True, d=64)      # padded strides: not 16-byte multiples
+    rc, name, err = varlen_validate(a, meta)
+    assert rc == 0 and name == "g950_attn_varlen_general", err
+
+
+def test_flash_varlen_refusals():
+    from oracle import inputs
+    a, meta = inputs.varlen_case()
+    for flag in ("is_softcap", "is_dropout", "return_softmax", "is_alibi", "seqlenq_ngroups_swapped"):
+        rc, _, err = varlen_validate(a, meta, **{flag: True})
+        assert rc == rt.USAGE and flag in err
+    rc, _, err = varlen_validate(a, meta, scale_softmax_log2=0.5)
+    assert rc == rt.USAGE and "scale_softmax_log2" in err
+    rc, _, err = varlen_validate(a, meta, h_hk_ratio=3)
+    assert rc == rt.USAGE
+    rc, _, err = varlen_validate(a, meta, total_q=a["total_q"] + 1)   # lse too small for h x total_q
+    assert rc == rt.USAGE and "softmax_lse_ptr" in err
+    rc, _, err = varlen_validate(a, meta, cu_seqlens_q_ptr=a["cu_seqlens_q_ptr"].astype(np.float32))
+    assert rc == rt.USAGE and "int32" in err
+    a2, meta2 = inputs.varlen_case(var_q=False, var_k=False)
+    rc, _, err = varlen_validate(a2, meta2, seqlen_q=a2["seqlen_q"] + 1)
+    assert rc == rt.USAGE and "seqlen_q" in err
+    rc, _, err = varlen_validate(a2, meta2, seqlen_k=a2["seqlen_k"] + 5)
+    assert rc == rt.USAGE and "seqlen_k" in err
 
 
 def test_view_reach_outside_storage_is_rejected():

@@ -1,0 +1,133 @@
+"""GPU parity of flash_varlen_fwd_kernel (variable-length attention with
+cu_seqlens / fixed-length batches, seqused_k, GQA, causal and local windows,
+paged K/V) through the C ABI against the CPU oracle on the same inputs.
+
+Cases: the reference's own case shapes (ops/suite/dev/flash_varlen_fwd_kernel.py
+:320-330, d = 16/32/64) and MFMA-path cases at d = 64/128 with the features
+the reference case layer leaves at their defaults.  Bars are the reference
+case's own (:348-354 with :412): fp32 1e-4, bf16 1e-2, fp16 3e-2 (rtol = atol,
+np.isclose form) on O -- including the positions no row writes, which must
+keep their initial value -- and on LSE (+inf for rows without keys).
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from compiler_amd import operators as ops  # noqa: E402
+from compiler_amd import runtime as rt  # noqa: E402
+from compiler_amd.operators import _VARLEN_SCALARS, _VARLEN_VIEWS  # noqa: E402
+from oracle import inputs  # noqa: E402
+from oracle import reference as ref  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TD = {"float32": torch.float32, "bfloat16": torch.bfloat16, "float16": torch.float16}
+BAR = {"float32": 1e-4, "bfloat16": 1e-2, "float16": 3e-2}
+
+
+def run(a, meta, dt):
+    t = {}
+    for n in _VARLEN_VIEWS:
+        arr = np.ascontiguousarray(a[n])
+        if arr.dtype == np.uint64:
+            arr = arr.view(np.int64)
+        t[n] = torch.from_numpy(arr).to(DEV)
+        if n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr"):
+            t[n] = t[n].to(TD[dt])
+    rounded = {n: t[n].float().cpu().numpy() for n in ("q_ptr", "k_ptr", "v_ptr", "o_ptr")}
+    merged = {**a, **meta}
+    ops.flash_varlen_fwd_kernel(**t, **{n: merged[n] for n in _VARLEN_SCALARS}, sync=True)
+    expect_o, expect_lse = inputs.varlen_oracle({**a, **rounded}, meta)
+    return t["o_ptr"].float().cpu().numpy(), t["softmax_lse_ptr"].cpu().numpy(), expect_o, expect_lse
+
+
+def check(a, meta, dt, kernel_prefix):
+    o, lse, eo, el = run(a, meta, dt)
+    assert rt.module().last_kernel.startswith(kernel_prefix), rt.module().last_kernel
+    bar = BAR[dt]
+    ok, err = ref.isclose_verdict(o, eo, bar, bar)
+    assert ok, f"O max err {err}"
+    ok, err = ref.isclose_verdict(lse, el, bar, bar)
+    assert ok, f"LSE max err {err}"
+    assert np.array_equal(np.isinf(lse), np.isinf(el))
+
+
+REF_SHAPES = [(2, 17, 19, 4, 2, 16), (3, 17, 19, 6, 2, 32), (3, 33, 35, 6, 2, 32), (4, 65, 67, 8, 4, 64),
+              (2, 17, 35, 4, 2, 16, 0, 0, 1), (2, 17, 35, 4, 2, 16, 1, 1, 1), (2, 17, 35, 4, 2, 16, 1, 0, 1),
+              (2, 17, 35, 4, 2, 16, 0, 1, 1), (3, 17, 19, 4, 2, 16)]
+
+
+@pytest.mark.parametrize("dt", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("shape", REF_SHAPES)
+def test_reference_case_shapes(shape, dt):
+    b, mq, mk, h, hk, d = shape[:6]
+    var_q, var_k, strided = (True, True, False) if len(shape) == 6 else map(bool, shape[6:])
+    a, meta = inputs.varlen_case(b, mq, mk, h, hk, d, var_q=var_q, var_k=var_k, strided=strided)
+    mfma = dt != "float32" and d in (64, 128) and not strided
+    check(a, meta, dt, "g950_attn_fwd_" if mfma else "g950_attn_varlen_general")
+
+
+MFMA_CASES = {
+    "dense": dict(batches=3, max_q=700, max_k=900, h=8, hk=2, d=128),
+    "causal": dict(batches=3, max_q=700, max_k=900, h=8, hk=2, d=128, causal=True, window_right=0),
+    "causal_square": dict(batches=2, max_q=600, max_k=600, h=4, hk=4, d=64, var_q=False, var_k=False,
+                          causal=True, window_right=0),
+    "local": dict(batches=3, max_q=700, max_k=900, h=8, hk=2, d=128, local=True, window_left=100,
+                  window_right=50),
+    "local_empty_rows": dict(batches=2, max_q=300, max_k=300, h=4, hk=2, d=64, local=True, window_left=-40,
+                             window_right=80),
+    "paged16": dict(batches=3, max_q=500, max_k=777, h=8, hk=2, d=128, paged=True, block_size=16),
+    "paged64_causal": dict(batches=3, max_q=500, max_k=777, h=8, hk=2, d=64, paged=True, block_size=64,
+                           causal=True, window_right=0),
+    "seqused": dict(batches=3, max_q=400, max_k=520, h=8, hk=8, d=128, seqused_trim=37),
+    "fixed_len": dict(batches=2, max_q=513, max_k=700, h=4, hk=2, d=128, var_q=False, var_k=False),
+}
+
+
+@pytest.mark.parametrize("dt", ["bfloat16", "float16"])
+@pytest.mark.parametrize("case", sorted(MFMA_CASES))
+def test_mfma_varlen_features(case, dt):
+    a, meta = inputs.varlen_case(**MFMA_CASES[case])
+    check(a, meta, dt, "g950_attn_fwd_")
+
+
+def test_general_kernel_features_fp32():
+    """The same features through the fp32 one-thread-per-row kernel."""
+    for kw in (dict(causal=True, window_right=0), dict(local=True, window_left=3, window_right=2),
+               dict(paged=True, block_size=4), dict(seqused_trim=2), dict(strided=True, causal=True,
+                                                                          window_right=1)):
+        a, meta = inputs.varlen_case(batches=3, max_q=17, max_k=24, h=4, hk=2, d=16, **kw)
+        check(a, meta, "float32", "g950_attn_varlen_general")
+
+
+def test_invalid_device_lengths_leave_memory_alone():
+    """cu_seqlens that would address past q/o make that sequence empty: no
+    write outside the views (guard bytes behind o stay), the valid sequence
+    is still right."""
+    a, meta = inputs.varlen_case(batches=2, max_q=17, max_k=19, h=4, hk=2, d=64)
+    a = dict(a)
+    cu = a["cu_seqlens_q_ptr"].copy()
+    cu[2] = cu[1] + 10_000          # second sequence claims rows far past the buffers
+    a["cu_seqlens_q_ptr"] = cu
+    t = {n: torch.from_numpy(np.ascontiguousarray(a[n]).view(np.int64) if a[n].dtype == np.uint64
+                             else np.ascontiguousarray(a[n])).to(DEV) for n in _VARLEN_VIEWS}
+    for n in ("q_ptr", "k_ptr", "v_ptr"):
+        t[n] = t[n].to(torch.bfloat16)
+    guard = torch.full((t["o_ptr"].numel() + 64,), 5.0, dtype=torch.bfloat16, device=DEV)
+    guard[: t["o_ptr"].numel()] = -0.875
+    t["o_ptr"] = guard[: t["o_ptr"].numel()]
+    merged = {**a, **meta}
+    ops.flash_varlen_fwd_kernel(**t, **{n: merged[n] for n in _VARLEN_SCALARS}, sync=True)
+    assert torch.all(guard[t["o_ptr"].numel():] == 5.0)
+    first = int(a["cu_seqlens_q_ptr"][1]) * meta["h"] * meta["d"]
+    rounded = {n: t[n].float().cpu().numpy() for n in ("q_ptr", "k_ptr", "v_ptr")}
+    ok_case = dict(a, **rounded)
+    ok_case["cu_seqlens_q_ptr"] = inputs.varlen_case(batches=2, max_q=17, max_k=19, h=4, hk=2,
+                                                     d=64)[0]["cu_seqlens_q_ptr"]
+    eo, _ = inputs.varlen_oracle(dict(ok_case, o_ptr=np.full(t["o_ptr"].numel(), -0.875, np.float32)), meta)
+    got = t["o_ptr"].float().cpu().numpy()
+    ok, err = ref.isclose_verdict(got[:first], eo[:first], 1e-2, 1e-2)
+    assert ok, err
+    assert np.all(got[first:] == -0.875)
