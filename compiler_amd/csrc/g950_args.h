@@ -38,6 +38,8 @@ struct GemmArgs {
   int M, N, K;
   int tiles_m, tiles_n;
   int a_dtype, b_dtype, c_dtype;
+  const void* bscale; // fused weight dequantisation: per-column scale of an int8 B
+  int bscale_dtype;   //   (float dtype code), applied to the fp32 accumulator
 };
 
 struct AttnArgs {

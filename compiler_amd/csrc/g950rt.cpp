@@ -602,6 +602,54 @@ int op_dequantize(g950_module* m, const g950_view* views, uint32_t nviews, const
   return launch(m, "g950_dequant_i8_general", (unsigned)(blocks < cap ? blocks : cap), 256u, a, stream);
 }
 
+// Fused weight dequantisation + GEMM (W8A16): y = a . (b * b_scale[n]).
+int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+                      uint32_t nsc, void* stream) {
+  if (nviews != 4 || nsc != 3)
+    return fail(G950_USAGE, "dequant_matmul: needs views (a_ptr, b_ptr, b_scale_ptr, y_ptr), scalars (K, M, N)");
+  View a, b, s, y;
+  if (int rc = check_view(views, 0, "a_ptr", 2, a, false)) return rc;
+  if (int rc = check_view(views, 1, "b_ptr", 2, b, false)) return rc;
+  if (int rc = check_view(views, 2, "b_scale_ptr", 1, s, false)) return rc;
+  if (int rc = check_view(views, 3, "y_ptr", 2, y, true)) return rc;
+  long long M, N, K;
+  if (int rc = gemm_views(a, b, y, sc, M, N, K)) return rc;
+  if (b.v->dtype != G950_DTYPE_INT8) return fail(G950_USAGE, "dequant_matmul: b_ptr must be int8");
+  if (!is_float(a.v->dtype) || !is_float(y.v->dtype) || s.v->dtype != a.v->dtype)
+    return fail(G950_USAGE, "dequant_matmul: a_ptr, b_scale_ptr (same dtype) and y_ptr must be float");
+  if (s.shape[0] != N) return fail(G950_USAGE, "dequant_matmul: b_scale_ptr needs one entry per column");
+  GemmArgs g{};
+  g.a = a.v->data; g.b = b.v->data; g.c = y.v->data;
+  g.M = (int)M; g.N = (int)N; g.K = (int)K;
+  g.a_dtype = (int)a.v->dtype; g.b_dtype = G950_DTYPE_INT8; g.c_dtype = (int)y.v->dtype;
+  g.c_s0 = y.stride[0]; g.c_s1 = y.stride[1];
+  g.bscale = s.v->data; g.bscale_dtype = (int)s.v->dtype;
+  if (M == 0 || N == 0) return launch(m, "g950_gemm_general", 0, 256, g, stream);
+  if (N > 1 && s.stride[0] != 1) {
+    // the kernels index the scale densely: only a contiguous scale row is taken
+    return fail(G950_USAGE, "dequant_matmul: b_scale_ptr must be contiguous");
+  }
+  const bool fast = is_float16ish(a.v->dtype) && K % 16 == 0 && (K < 2 || (a.stride[1] == 1 && b.stride[0] == 1)) &&
+                    a.stride[0] % 8 == 0 && b.stride[1] % 16 == 0 && aligned16(a.addr()) && aligned16(b.addr()) &&
+                    y.stride[1] == 1 && aligned16(y.addr());
+  if (fast) {
+    g.a_s0 = a.stride[0];
+    g.b_s0 = b.stride[1];  // Bt row (n) stride
+    g.tiles_m = (int)((M + 127) / 128);
+    g.tiles_n = (int)((N + 127) / 128);
+    const long long tiles = (long long)g.tiles_m * g.tiles_n;
+    if (tiles > 0x7FFFFFFF) return fail(G950_USAGE, "dequant_matmul: too many tiles");
+    return launch(m, a.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_gemm_w8a16_bf16_128x128" : "g950_gemm_w8a16_f16_128x128",
+                  (unsigned)tiles, 256u, g, stream);
+  }
+  g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
+  g.b_s0 = b.stride[0]; g.b_s1 = b.stride[1];
+  g.tiles_n = (int)((N + 63) / 64);
+  const long long blocks = ((M + 63) / 64) * g.tiles_n;
+  if (blocks > 0x7FFFFFFF) return fail(G950_USAGE, "dequant_matmul: too many tiles");
+  return launch(m, "g950_gemm_general", (unsigned)blocks, 256u, g, stream);
+}
+
 // ---------------------------------------------------------------- attention
 int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
                  uint32_t nsc, bool with_lse, void* stream) {
@@ -931,6 +979,7 @@ int dispatch(g950_module* m, uint32_t op, const g950_view* views, uint32_t nview
       case G950_OP_COPY: return op_copy(m, views, nviews, nscalars, stream);
       case G950_OP_DEQUANTIZE: return op_dequantize(m, views, nviews, scalars, nscalars, stream);
       case G950_OP_FLASH_VARLEN: return op_flash_varlen(m, views, nviews, scalars, nscalars, stream);
+      case G950_OP_DEQUANT_MATMUL: return op_dequant_matmul(m, views, nviews, scalars, nscalars, stream);
       default: return fail(G950_USAGE, "g950_launch: unknown operator contract %u", op);
     }
   } catch (...) {

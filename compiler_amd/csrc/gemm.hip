@@ -293,6 +293,144 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   gemm_epilogue<MODE, FM, FN>(p, accf, acci, m0 + wm * (BM / WM), n0 + wn * (BN / WN), r, g);
 }
 
+// --------------------------------------------- fused weight dequantisation
+// W8A16 (dequantize_matmul fused into the GEMM): Y = A . (B * scale[n]) for A
+// bf16/fp16 [M,K] (K-contiguous) and B int8 stored as Bt[N,K] (K-contiguous),
+// scale per column (ops/suite/perf/dequantize_matmul.py:28-43 followed by
+// matmul.py:21-37).  int8 values are exact in bf16/fp16, so A.B accumulates
+// exactly as the unfused pair would from exact weights; the scale multiplies
+// the fp32 accumulator and the result rounds once at the store.
+//   * workgroup tile 128 x 128, 4 waves (2 x 2), wave tile 64 x 64 = 2 x 2
+//     fragments of v_mfma_f32_32x32x16; K in tiles of 64
+//   * register-staged: each thread loads its 4 A and 2 B 16-byte vectors of
+//     the next K tile while the current one is multiplied, widens the 32 int8
+//     weights to 16-bit once (per workgroup, not per wave), and writes both
+//     to the other LDS stage (128-byte rows, the main kernel's XOR swizzle, so
+//     fragment reads are the main kernel's); one barrier per K tile
+//   * B moves as int8: half the weight bytes of the unfused path, which
+//     matters where the product is bandwidth-bound (few rows of A)
+//   * K must be a multiple of 16 (whole 16-byte B vectors); a K tile past K
+//     is zero-filled; M/N edges clamp loads and mask stores
+template <bool F16>
+__device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
+  constexpr int TM = 128, TN = 128, TK = 64;
+  constexpr int ROW = TK * 2;              // LDS row bytes (16-bit elements)
+  constexpr int STAGE = (TM + TN) * ROW;   // 32 KiB
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * TM, n0 = tn * TN;
+  const long long lda = p.a_s0 * 2, ldb = p.b_s0;  // bytes
+  const int nk = (p.K + TK - 1) / TK;
+
+  // register staging: A vector i (of 4): row (tid + 256 i) >> 3, chunk & 7;
+  // B vector i (of 2): row (tid + 256 i) >> 2, 16-int8 part & 3
+  u32x4 ra[4], rb[2];
+  auto load = [&](int kt) {
+    const int k0 = kt * TK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = tid + 256 * i, row = v >> 3, ch = v & 7;
+      const int k = k0 + ch * 8;
+      const char* src = (const char*)p.a + (long long)min(m0 + row, p.M - 1) * lda + (long long)k * 2;
+      ra[i] = k < p.K ? *(const u32x4*)src : (u32x4){0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int v = tid + 256 * i, row = v >> 2, part = v & 3;
+      const int k = k0 + part * 16;
+      const char* src = (const char*)p.b + (long long)min(n0 + row, p.N - 1) * ldb + k;
+      rb[i] = k < p.K ? *(const u32x4*)src : (u32x4){0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&](int stage) {
+    char* st = lds + stage * STAGE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = tid + 256 * i, row = v >> 3, ch = v & 7;
+      *(u32x4*)(st + row * ROW + ((ch ^ ((row >> 1) & 7)) << 4)) = ra[i];
+    }
+    char* sb = st + TM * ROW;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int v = tid + 256 * i, row = v >> 2, part = v & 3;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // 8 int8 -> 8 16-bit values = one 16-byte chunk
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t w = rb[i][2 * h + j / 2];
+          const int sh = (j & 1) * 16;
+          const float lo = (float)(int8_t)((w >> sh) & 0xFFu);
+          const float hi = (float)(int8_t)((w >> (sh + 8)) & 0xFFu);
+          o[j] = F16 ? (uint32_t)f32_to_f16(lo) | ((uint32_t)f32_to_f16(hi) << 16)
+                     : (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+        }
+        const int ch = part * 2 + h;
+        *(u32x4*)(sb + row * ROW + ((ch ^ ((row >> 1) & 7)) << 4)) = o;
+      }
+    }
+  };
+
+  const int g = lane >> 5, r = lane & 31;
+  f32x16 acc[2][2];
+  i32x16 unused[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x16){};
+  load(0);
+  store(0);
+  __syncthreads();
+  int cur = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) load(kt + 1);
+    const char* st = lds + cur * STAGE;
+    const char* sb = st + TM * ROW;
+#pragma unroll
+    for (int ks = 0; ks < TK / 16; ++ks) {
+      const int chunk = ks * 2 + g;
+      u32x4 af[2], bf[2];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) {
+        const int row = wm * 64 + mi * 32 + r;
+        af[mi] = *(const u32x4*)(st + row * ROW + ((chunk ^ ((row >> 1) & 7)) << 4));
+      }
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const int row = wn * 64 + ni * 32 + r;
+        bf[ni] = *(const u32x4*)(sb + row * ROW + ((chunk ^ ((row >> 1) & 7)) << 4));
+      }
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+          mfma_step<F16 ? GEMM_F16 : GEMM_BF16>(bf[ni], af[mi], acc[mi][ni], unused[mi][ni]);
+    }
+    if (kt + 1 < nk) store(cur ^ 1);
+    __syncthreads();
+    cur ^= 1;
+  }
+  // scale the accumulator by its column's scale (lane layout of gemm_epilogue)
+  const int wm0 = m0 + wm * 64, wn0 = n0 + wn * 64;
+#pragma unroll
+  for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int n = wn0 + ni * 32 + q * 8 + g * 4 + e;
+        const float sc = n < p.N ? load_as_f32(p.bscale, n, p.bscale_dtype) : 0.0f;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) acc[mi][ni][q * 4 + e] *= sc;
+      }
+  gemm_epilogue<F16 ? GEMM_F16 : GEMM_BF16, 2, 2>(p, acc, unused, wm0, wn0, r, g);
+}
+
 // ------------------------------------------------------------ general GEMM
 // 64x64 output tile, 256 threads, each 4x4 outputs; K in steps of 16 staged
 // through LDS with bounds-checked element loads (zero fill past the edges).
@@ -321,6 +459,7 @@ __device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
       const bool inbb = (n < p.N) && (k < p.K);
       const long long ib = (long long)k * p.b_s0 + (long long)n * p.b_s1;
       if (INT8) Bi[kk][mm] = inbb ? (int)((const int8_t*)p.b)[ib] : 0;
+      else if (p.b_dtype == DT_INT8) Bs[kk][mm] = inbb ? (float)((const int8_t*)p.b)[ib] : 0.0f;
       else Bs[kk][mm] = inbb ? load_as_f32(p.b, ib, p.b_dtype) : 0.0f;
     }
     __syncthreads();
@@ -351,6 +490,7 @@ __device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
         v = ((float)acci[i][j] * p.sa[m]) * p.sb[n];
       } else {
         v = accf[i][j];
+        if (p.bscale) v *= load_as_f32(p.bscale, n, p.bscale_dtype);
       }
       store_from_f32(p.c, (long long)m * p.c_s0 + (long long)n * p.c_s1, p.c_dtype, v);
     }
@@ -366,6 +506,12 @@ __device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
 G950_GEMM_MFMA(g950_gemm_bf16_256x256, g950::GEMM_BF16, 4, 2)
 G950_GEMM_MFMA(g950_gemm_f16_256x256, g950::GEMM_F16, 4, 2)
 G950_GEMM_MFMA(g950_gemm_i8_256x256, g950::GEMM_I8, 4, 2)
+extern "C" __global__ __launch_bounds__(256) void g950_gemm_w8a16_bf16_128x128(const g950::GemmArgs p) {
+  g950::gemm_w8a16_body<false>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void g950_gemm_w8a16_f16_128x128(const g950::GemmArgs p) {
+  g950::gemm_w8a16_body<true>(p);
+}
 extern "C" __global__ __launch_bounds__(256) void g950_gemm_general(const g950::GemmArgs p) {
   g950::gemm_general_body<false>(p);
 }

@@ -91,6 +91,16 @@ def flash_varlen_fwd_kernel(*, stream=None, sync=False, prepare=False, **args):
     return _launch(rt.OP_FLASH_VARLEN, views, {"o_ptr", "softmax_lse_ptr"}, scalars, stream, sync, prepare)
 
 
+def dequant_matmul_kernel(a_ptr, b_ptr, b_scale_ptr, y_ptr, M, N, K, *, stream=None, sync=False, prepare=False):
+    """dequantize_matmul fused into one GEMM: y = a . (b * b_scale[None, :])
+    (ops/suite/perf/dequantize_matmul.py:28-43 then matmul.py:21-37).  a: [M, K]
+    float, b: int8 logical [K, N] (pass ``bt.t()`` of a row-major [N, K] for the
+    MFMA path), b_scale: [N] in a's dtype, y: [M, N]."""
+    return _launch(rt.OP_DEQUANT_MATMUL, {"a_ptr": a_ptr, "b_ptr": b_ptr, "b_scale_ptr": b_scale_ptr,
+                                          "y_ptr": y_ptr}, {"y_ptr"}, {"M": M, "N": N, "K": K},
+                   stream, sync, prepare)
+
+
 def rms_layernorm_forward_kernel(Y, Y_row_stride, X, X_row_stride, W, W_row_stride, r,
                                  r_row_stride, n_cols, eps, *, stream=None, sync=False, prepare=False):
     """RMSNorm forward (ops/suite/perf/fast_rms_layernorm.py:20-42)."""
@@ -187,6 +197,16 @@ def dequantize(b, scale, out=None, **kw):
     y = torch.empty(b.shape, dtype=scale.dtype, device=b.device) if out is None else out
     dequantize_kernel(b, scale, y, b.shape[0], b.shape[1], b.stride(0), b.stride(1), y.stride(0),
                       y.stride(1), **kw)
+    return y
+
+
+def dequant_matmul(a, b, scale, out=None, **kw):
+    """a [M,K] @ (b [K,N] int8 * scale[N]); pass ``bt.t()`` for a K-contiguous b."""
+    import torch
+    m, k = a.shape
+    n = b.shape[1]
+    y = torch.empty((m, n), dtype=a.dtype, device=a.device) if out is None else out
+    dequant_matmul_kernel(a, b, scale, y, m, n, k, **kw)
     return y
 
 

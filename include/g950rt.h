@@ -137,6 +137,15 @@ typedef struct g950_scalar {
  *           is_alibi, is_causal, ... window_size_left, window_size_right);
  *           is_softcap, is_dropout, return_softmax, seqlenq_ngroups_swapped and
  *           is_alibi must be 0 (refused otherwise)
+ * G950_OP_DEQUANT_MATMUL  dequantize_matmul fused into the GEMM: the
+ *                      reference's dequantize_kernel (ops/suite/perf/
+ *                      dequantize_matmul.py:28-43) feeding matmul_kernel
+ *                      (ops/suite/perf/matmul.py:21-37) as one kernel:
+ *                      y = a . (b * b_scale[n]), fp32 accumulation of a . b
+ *                      (int8 exact in 16-bit floats), scale on the accumulator
+ *   views   a_ptr[M,K] f32 | bf16 | f16, b_ptr i8[K,N] (K-contiguous for the MFMA
+ *           path), b_scale_ptr[N] (a's dtype), y_ptr[M,N] float
+ *   scalars K, M, N
  */
 enum g950_op {
   G950_OP_SOFTMAX = 1,
@@ -150,7 +159,8 @@ enum g950_op {
   G950_OP_COPY = 9,
   G950_OP_LOGSUMEXP = 10,
   G950_OP_DEQUANTIZE = 11,
-  G950_OP_FLASH_VARLEN = 12
+  G950_OP_FLASH_VARLEN = 12,
+  G950_OP_DEQUANT_MATMUL = 13
 };
 
 typedef struct g950_module g950_module;

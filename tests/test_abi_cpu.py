@@ -251,6 +251,25 @@ def test_flash_varlen_refusals():
     assert rc == rt.USAGE and "seqlen_k" in err
 
 
+def test_dequant_matmul_contract():
+    def args(m, n, k, adt=rt.DT_BF16, col_b=True, sdt=None):
+        return (Args().view([m, k], adt).view([k, n], rt.DT_INT8, strides=[1, k] if col_b else None)
+                .view([n], sdt or adt).view([m, n], adt, output=True))
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(256, 512, 1024), [1024, 256, 512])
+    assert rc == 0 and name == "g950_gemm_w8a16_bf16_128x128", err
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(16, 4096, 4096, rt.DT_F16), [4096, 16, 4096])
+    assert rc == 0 and name == "g950_gemm_w8a16_f16_128x128", err
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 64, col_b=False), [64, 64, 64])
+    assert rc == 0 and name == "g950_gemm_general", err
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 40), [40, 64, 64])
+    assert rc == 0 and name == "g950_gemm_general", err
+    assert validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 64, sdt=rt.DT_F32), [64, 64, 64])[0] == rt.USAGE
+    assert validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 64), [64, 64, 65])[0] == rt.USAGE
+    wrong_b = Args().view([64, 64], rt.DT_BF16).view([64, 64], rt.DT_BF16).view([64], rt.DT_BF16) \
+        .view([64, 64], rt.DT_BF16, output=True)
+    assert validate(rt.OP_DEQUANT_MATMUL, wrong_b, [64, 64, 64])[0] == rt.USAGE
+
+
 def test_view_reach_outside_storage_is_rejected():
     a = softmax_args(4, 97, rt.DT_F32)
     shape, strides, dtype, out, data, storage, size = a.specs[0]

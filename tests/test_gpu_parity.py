@@ -316,6 +316,43 @@ def test_gemm_bf16_config3_sampled(m, n, k):
     close(got, ref.matmul(c["a"][rows], c["bt"].T), 2e-2, 2e-2)
 
 
+@pytest.mark.parametrize("dt", ["bfloat16", "float16"])
+@pytest.mark.parametrize("m,n,k", [(32, 32, 32), (33, 33, 48), (256, 256, 128), (300, 260, 192), (16, 4096, 4096),
+                                   (1, 1000, 4096), (2048, 2048, 4096)])
+def test_dequant_matmul_fused(m, n, k, dt):
+    """dequantize_matmul fused into the GEMM: a [M,K] in dt, b int8 ~ U{-127..127}
+    (K-contiguous), scale ~ U[0,1) / 64 in dt.  Bar 2e-2 (the bf16 GEMM bar,
+    np.isclose form) against float64 a . (b * scale) on the rounded inputs; rows
+    sampled at the largest shape."""
+    rng = np.random.default_rng(m + 7 * n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32) * 0.5
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = (rng.random(n) / 64).astype(np.float32)
+    ad, sd = dev(a, dt), dev(s, dt)
+    bt = torch.from_numpy(np.ascontiguousarray(b.T)).to(DEV)
+    y = ops.dequant_matmul(ad, bt.t(), sd, sync=True)
+    assert rt.module().last_kernel == ("g950_gemm_w8a16_%s_128x128" % ("bf16" if dt == "bfloat16" else "f16")
+                                       if k % 16 == 0 else "g950_gemm_general")
+    rows = np.arange(m) if m <= 512 else np.unique(np.r_[0, 127, 128, m - 1,
+                                                        np.random.default_rng(5).integers(0, m, 24)])
+    expect = ref.matmul(host(ad)[rows], ref.dequantize(b, host(sd)))
+    close(host(y)[rows], expect, 2e-2, 2e-2)
+
+
+def test_dequant_matmul_general_layouts():
+    """Row-major int8 b, fp32 a and a ragged K take the general kernel, same bar
+    (fp32: 1e-4)."""
+    rng = np.random.default_rng(12)
+    a = rng.standard_normal((70, 40)).astype(np.float32)
+    b = rng.integers(-128, 128, (40, 90)).astype(np.int8)
+    s = rng.random(90).astype(np.float32)
+    for dt, bar in (("float32", 1e-4), ("bfloat16", 2e-2)):
+        ad, sd = dev(a, dt), dev(s, dt)
+        y = ops.dequant_matmul(ad, torch.from_numpy(b).to(DEV), sd, sync=True)
+        assert rt.module().last_kernel == "g950_gemm_general"
+        close(host(y), ref.matmul(host(ad), ref.dequantize(b, host(sd))), bar, bar)
+
+
 def test_gemm_f16_and_general_paths():
     rng = np.random.default_rng(3)
     a = rng.standard_normal((130, 192)).astype(np.float16).astype(np.float32)
