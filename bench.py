@@ -274,6 +274,39 @@ def suite(torch, ops):
     del q, k, v, o, lse
     torch.cuda.empty_cache()
 
+    # few long rows (split-row two-phase path): softmax bf16 [4, 2^22]
+    xs = [torch.randn((4, 1 << 22), device=dev, generator=g).to(torch.bfloat16) for _ in range(ROTATE)]
+    ys = [torch.empty_like(x) for x in xs]
+    sp_calls = [ops.softmax_kernel(x, y, 1 << 22, prepare=True) for x, y in zip(xs, ys)]
+    ms = event_time(torch, lambda i: sp_calls[i % ROTATE](), 100, 10, warm_s=0.3)
+    gbs = 2 * 4 * (1 << 22) * 2 / (ms * 1e-3) / 1e9
+    out.append({"config": "F split-row softmax bf16 [4,4194304]", "kernel": sp_calls[0].kernel,
+                "us": round(ms * 1e3, 2), "value": round(gbs, 1), "unit": "GB/s", "bound": "hbm",
+                "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    del xs, ys, sp_calls
+
+    # dequantize_matmul fused into the GEMM (W8A16): 8192^3 and a decode shape
+    # (16 rows; split-K), bf16 activations, int8 K-contiguous weights
+    for m_, n_, k_ in ((8192, 8192, 8192), (16, 8192, 8192)):
+        a_ = torch.randn((m_, k_), device=dev, generator=g).to(torch.bfloat16)
+        bt_ = torch.randint(-127, 127, (n_, k_), device=dev, generator=g, dtype=torch.int8)
+        s_ = torch.rand(n_, device=dev, generator=g).to(torch.bfloat16)
+        y_ = torch.empty((m_, n_), device=dev, dtype=torch.bfloat16)
+        call = ops.dequant_matmul_kernel(a_, bt_.t(), s_, y_, m_, n_, k_, prepare=True)
+        ms = event_time(torch, lambda i: call(), 10 if m_ > 1000 else 50, 3, warm_s=0.3)
+        if m_ > 1000:
+            tf = 2.0 * m_ * n_ * k_ / (ms * 1e-3) / 1e12
+            out.append({"config": f"F dequant_matmul W8A16 bf16 {m_}x{n_}x{k_}", "kernel": call.kernel,
+                        "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
+                        "frac": round(tf / BF16_PEAK_TFS, 4)})
+        else:
+            gbs = (n_ * k_ + m_ * k_ * 2 + m_ * n_ * 2) / (ms * 1e-3) / 1e9
+            out.append({"config": f"F dequant_matmul W8A16 bf16 {m_}x{n_}x{k_} (decode)", "kernel": call.kernel,
+                        "us": round(ms * 1e3, 1), "value": round(gbs, 1), "unit": "GB/s", "bound": "hbm",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del a_, bt_, s_, y_
+    torch.cuda.empty_cache()
+
     # varlen attention (flash_varlen_fwd_kernel): 8 sequences of 4096 - 256 i
     # tokens (q = k lengths, causal), 32 query / 8 KV heads, d 128, bf16;
     # contiguous and paged (64-token pages, shuffled) K/V

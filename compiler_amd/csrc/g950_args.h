@@ -40,6 +40,10 @@ struct GemmArgs {
   int a_dtype, b_dtype, c_dtype;
   const void* bscale; // fused weight dequantisation: per-column scale of an int8 B
   int bscale_dtype;   //   (float dtype code), applied to the fp32 accumulator
+  int splits;         // split-K: K ranges per output tile (1: none)
+  int kchunk;         // split-K: K elements per range (multiple of the K tile)
+  float* part;        // split-K: [splits, M, N] fp32 partial products
+  int* tile_count;    // split-K: per-tile arrival counters, zero between calls
 };
 
 struct AttnArgs {

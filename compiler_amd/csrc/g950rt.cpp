@@ -37,10 +37,13 @@ struct g950_module {
   int cus = 256;  // compute units of the device (persistent grid sizing)
   std::mutex mu;
   std::unordered_map<std::string, hipFunction_t> fns;
-  // per-stream device workspace (split-row partials); launches on one stream
-  // are ordered, so each stream owns one buffer, grown on demand
+  // per-stream device workspace (split-row and split-K partials); launches on
+  // one stream are ordered, so each stream owns one buffer, grown on demand
   std::mutex ws_mu;
   std::unordered_map<void*, std::pair<void*, size_t>> ws;
+  // per-stream arrival counters (split-K), zeroed at allocation; every kernel
+  // that uses them leaves them zero
+  std::unordered_map<void*, std::pair<void*, size_t>> counters;
 };
 
 namespace {
@@ -241,6 +244,34 @@ int workspace(g950_module* m, void* stream, size_t bytes, void** out) {
     w.second = n;
   }
   *out = w.first;
+  return G950_OK;
+}
+
+// Zeroed per-stream counters of at least `n` ints for launches on `stream`.
+int tile_counters(g950_module* m, void* stream, size_t n, int** out) {
+  std::lock_guard<std::mutex> lock(m->ws_mu);
+  auto& w = m->counters[stream];
+  const size_t bytes = n * sizeof(int);
+  if (w.second < bytes) {
+    if (w.first) {
+      if (hipError_t e = hipStreamSynchronize((hipStream_t)stream))
+        return fail(G950_SYNC, "counters: %s", hipGetErrorString(e));
+      (void)hipFree(w.first);
+      w = {nullptr, 0};
+    }
+    const size_t nb = ((bytes < (size_t)4096 ? (size_t)4096 : bytes * 2) + 255) & ~(size_t)255;
+    if (hipError_t e = hipMalloc(&w.first, nb)) {
+      w = {nullptr, 0};
+      return fail(G950_RESOURCE, "counters: hipMalloc(%zu): %s", nb, hipGetErrorString(e));
+    }
+    if (hipError_t e = hipMemsetAsync(w.first, 0, nb, (hipStream_t)stream)) {
+      (void)hipFree(w.first);
+      w = {nullptr, 0};
+      return fail(G950_RESOURCE, "counters: hipMemsetAsync: %s", hipGetErrorString(e));
+    }
+    w.second = nb;
+  }
+  *out = (int*)w.first;
   return G950_OK;
 }
 
@@ -639,8 +670,30 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
     g.tiles_n = (int)((N + 127) / 128);
     const long long tiles = (long long)g.tiles_m * g.tiles_n;
     if (tiles > 0x7FFFFFFF) return fail(G950_USAGE, "dequant_matmul: too many tiles");
+    // split-K when the output tiles cannot fill the chip and A has few rows
+    // (the partial tiles are then small next to B): about two workgroups per
+    // CU, K ranges of whole 64-element tiles, at least 512 long.  Measured on
+    // MI355X at N = K = 8192: M = 16 163 -> 59 us, M = 1 162 -> 42 us; at
+    // M = 128 the partial traffic made it slower (165 -> 212 us).
+    const long long cus = m ? m->cus : 256;
+    long long splits = 1;
+    if (tiles * 2 < cus && K >= 1024 && M <= 64) {
+      splits = std::min((2 * cus + tiles - 1) / tiles, K / 512);
+      const long long kchunk = ((K + splits - 1) / splits + 63) / 64 * 64;
+      splits = (K + kchunk - 1) / kchunk;
+      g.kchunk = (int)kchunk;
+    }
+    g.splits = (int)splits;
+    if (splits == 1) g.kchunk = (int)K;
+    if (splits > 1 && m) {
+      void* ws = nullptr;
+      // + one tile row of padding: the merge reads whole 128-column tile rows
+      if (int rc = workspace(m, stream, (size_t)((splits * M * N + 128) * 4), &ws)) return rc;
+      g.part = (float*)ws;
+      if (int rc = tile_counters(m, stream, (size_t)tiles, &g.tile_count)) return rc;
+    }
     return launch(m, a.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_gemm_w8a16_bf16_128x128" : "g950_gemm_w8a16_f16_128x128",
-                  (unsigned)tiles, 256u, g, stream);
+                  (unsigned)(tiles * splits), 256u, g, stream);
   }
   g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
   g.b_s0 = b.stride[0]; g.b_s1 = b.stride[1];
@@ -1022,11 +1075,12 @@ const char* g950_last_error(void) { return t_error.c_str(); }
 
 void g950_close(g950_module* m) {
   if (!m) return;
-  for (auto& kv : m->ws)
-    if (kv.second.first) {
-      (void)hipStreamSynchronize((hipStream_t)kv.first);
-      (void)hipFree(kv.second.first);
-    }
+  for (auto* pool : {&m->ws, &m->counters})
+    for (auto& kv : *pool)
+      if (kv.second.first) {
+        (void)hipStreamSynchronize((hipStream_t)kv.first);
+        (void)hipFree(kv.second.first);
+      }
   if (m->mod) hipModuleUnload(m->mod);
   delete m;
 }

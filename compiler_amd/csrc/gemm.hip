@@ -311,6 +311,12 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
 //     matters where the product is bandwidth-bound (few rows of A)
 //   * K must be a multiple of 16 (whole 16-byte B vectors); a K tile past K
 //     is zero-filled; M/N edges clamp loads and mask stores
+//   * split-K for few output tiles (few rows of A, the decode shape): each
+//     workgroup multiplies one K range and stores its fp32 partial tile with
+//     device-coherent stores; the workgroup that arrives last at its tile's
+//     counter (one atomic increment after the stores completed; nobody waits)
+//     sums all partials in range order, scales, stores and resets the counter
+//     to zero for the next call
 template <bool F16>
 __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
   constexpr int TM = 128, TN = 128, TK = 64;
@@ -321,30 +327,34 @@ __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
+  const int split = blockIdx.x % p.splits;
+  const int tile = blockIdx.x / p.splits;
   int tm, tn;
-  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  tile_of(tile, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * TM, n0 = tn * TN;
   const long long lda = p.a_s0 * 2, ldb = p.b_s0;  // bytes
-  const int nk = (p.K + TK - 1) / TK;
+  const int kbeg = split * p.kchunk;
+  const int kend = min(p.K, kbeg + p.kchunk);
+  const int nk = kend > kbeg ? (kend - kbeg + TK - 1) / TK : 0;
 
   // register staging: A vector i (of 4): row (tid + 256 i) >> 3, chunk & 7;
   // B vector i (of 2): row (tid + 256 i) >> 2, 16-int8 part & 3
   u32x4 ra[4], rb[2];
   auto load = [&](int kt) {
-    const int k0 = kt * TK;
+    const int k0 = kbeg + kt * TK;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int v = tid + 256 * i, row = v >> 3, ch = v & 7;
       const int k = k0 + ch * 8;
       const char* src = (const char*)p.a + (long long)min(m0 + row, p.M - 1) * lda + (long long)k * 2;
-      ra[i] = k < p.K ? *(const u32x4*)src : (u32x4){0u, 0u, 0u, 0u};
+      ra[i] = k < kend ? *(const u32x4*)src : (u32x4){0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int v = tid + 256 * i, row = v >> 2, part = v & 3;
       const int k = k0 + part * 16;
       const char* src = (const char*)p.b + (long long)min(n0 + row, p.N - 1) * ldb + k;
-      rb[i] = k < p.K ? *(const u32x4*)src : (u32x4){0u, 0u, 0u, 0u};
+      rb[i] = k < kend ? *(const u32x4*)src : (u32x4){0u, 0u, 0u, 0u};
     }
   };
   auto store = [&](int stage) {
@@ -383,8 +393,10 @@ __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = (f32x16){};
-  load(0);
-  store(0);
+  if (nk > 0) {
+    load(0);
+    store(0);
+  }
   __syncthreads();
   int cur = 0;
   for (int kt = 0; kt < nk; ++kt) {
@@ -415,8 +427,69 @@ __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
     __syncthreads();
     cur ^= 1;
   }
-  // scale the accumulator by its column's scale (lane layout of gemm_epilogue)
   const int wm0 = m0 + wm * 64, wn0 = n0 + wn * 64;
+  if (p.splits > 1) {
+    // This range's partial tile goes out with device-coherent stores (agent
+    // scope: written through to the point where every XCD reads, no L2
+    // write-back needed); once they have completed, one atomic counts the
+    // arrival.  The last range to arrive reads the others' partials with
+    // device-coherent loads.
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+      const int m = wm0 + mi * 32 + r;
+      if (m >= p.M) continue;
+      float* row = p.part + ((long long)split * p.M + m) * p.N;
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int n = wn0 + ni * 32 + q * 8 + g * 4 + e;
+            if (n < p.N)
+              __hip_atomic_store(row + n, acc[mi][ni][q * 4 + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores complete
+    __syncthreads();
+    __shared__ int arrival;
+    if (tid == 0)
+      arrival = __hip_atomic_fetch_add(p.tile_count + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrival != p.splits - 1) return;  // another range's workgroup finishes the tile
+    // sum every range's partial in range order (the result does not depend
+    // on which workgroup arrived last); each range's loads issued together,
+    // at constant offsets from one row pointer per fragment row; columns past
+    // N read the workspace's padding and feed only outputs never stored
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = (f32x16){};
+    for (int sp = 0; sp < p.splits; ++sp) {
+      float v[2][2][16];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) {
+        const int m = min(wm0 + mi * 32 + r, p.M - 1);
+        const float* row = p.part + ((long long)sp * p.M + m) * p.N + wn0 + g * 4;
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              v[mi][ni][q * 4 + e] =
+                  __hip_atomic_load(row + ni * 32 + q * 8 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[mi][ni][e] += v[mi][ni][e];
+    }
+    if (tid == 0) __hip_atomic_store(p.tile_count + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // scale the accumulator by its column's scale (lane layout of gemm_epilogue)
 #pragma unroll
   for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
