@@ -27,7 +27,9 @@
 //     it by more than 8 (p <= 2^8, exact because l and O share the reference);
 //     the O rescale is skipped when no row of the wave moved.
 //   * K and V tiles (64 keys) are filled by direct global->LDS DMA
-//     (global_load_lds_dwordx4) into a 3-stage ring, two tiles ahead.  Tile
+//     (global_load_lds_dwordx4) into two-slot K and V rings (64 KiB at
+//     d = 128): K two tiles ahead (K of tile t is dead once S^T of tile t is
+//     formed, an iteration before P.V of tile t), V one tile ahead.  Tile
 //     layouts make every MFMA operand read a per-lane base plus a compile-time
 //     offset, bank-conflict free:  K as [16-d slab][key][32 B] with the two
 //     16-byte halves swapped on odd (key>>3); V as [32-d block][key][64 B], so
@@ -45,8 +47,9 @@ namespace g950 {
 
 
 
-constexpr int ATT_BK = 64;    // keys per tile
-constexpr int ATT_STAGES = 3; // LDS ring depth (one barrier per key tile)
+constexpr int ATT_BK = 64;     // keys per tile
+constexpr int ATT_KSLOTS = 2;  // K tiles in LDS: the one in use and the one in flight
+constexpr int ATT_VSLOTS = 2;  // V tiles in LDS: the one in use, the one in flight
 
 template <int D, int NW>
 struct AttnCfg {
@@ -55,7 +58,7 @@ struct AttnCfg {
   static constexpr int ROW = D * 2;               // tile row bytes (K and V)
   static constexpr int CHUNKS = D / 8;            // 16-byte chunks per row
   static constexpr int TILE = ATT_BK * ROW;       // one K or V tile
-  static constexpr int STAGE = 2 * TILE;          // K then V
+  static constexpr int LDS = (ATT_KSLOTS + ATT_VSLOTS) * TILE;  // K ring, then V ring
   static constexpr int DMAS = TILE / 1024;        // wave-instructions per tile
   static constexpr int DMA_PER_WAVE = (2 * DMAS + NW - 1) / NW;
   static constexpr int DBLK = D / 32;
@@ -189,7 +192,7 @@ __device__ __forceinline__ long long paged_row(const VarlenArgs& vl, int z, int 
 template <int D, bool F16, int NW, bool VL>
 __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* vl) {
   using C = AttnCfg<D, NW>;
-  __shared__ __attribute__((aligned(1024))) char lds[ATT_STAGES * C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds[C::LDS];
   if (blockDim.x != C::NT) return;  // launch shape must match the instantiation
 
   const int tid = threadIdx.x;
@@ -301,21 +304,27 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
     return (long long)ph * vl->page_stride * 2 - (long long)((kbeg + t * ATT_BK) / vl->block_size) *
                                                      vl->block_size * kstride;
   };
-  long long page_next = tile_page(0);  // byte shift of tile 0's page
-  auto dma_tile = [&](int t) {
-    char* stage = lds + (t % ATT_STAGES) * C::STAGE;
+  // K tiles and V tiles are each issued in increasing order, so each keeps
+  // its next page shift prefetched
+  long long kpage_next = tile_page(0), vpage_next = kpage_next;
+  // DMA of the K half (instructions u < DMA_PER_WAVE / 2) or the V half of
+  // tile t into its ring slot
+  auto dma_part = [&](bool kpart, int t) {
+    char* slot = kpart ? lds + (t % ATT_KSLOTS) * C::TILE : lds + (ATT_KSLOTS - 1 + t % ATT_VSLOTS) * C::TILE;
     const int kv0 = kbeg + t * ATT_BK;
     const bool tail = kv0 + ATT_BK > Sk;
     long long page_shift = 0;
     if constexpr (VL) {
       if (tile_pages) {
-        page_shift = page_next;
-        page_next = tile_page(t + 1);
+        long long& next = kpart ? kpage_next : vpage_next;
+        page_shift = next;
+        next = tile_page(t + 1);
       }
     }
 #pragma unroll
     for (int u = 0; u < C::DMA_PER_WAVE; ++u) {
       const bool is_k = u < C::DMA_PER_WAVE / 2;
+      if (is_k != kpart) continue;
       const char* base = is_k ? kbase : vbase;
       const long long stride = is_k ? kstride : vstride;
       const int key = tail ? min(kv0 + dkey[u], Sk - 1) : kv0 + dkey[u];
@@ -325,8 +334,10 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
         if (tile_pages) src = base + page_shift + key * kstride + dcol[u];
         else if (vl->page_table) src = base + 2 * paged_row(*vl, z, key, p.k_ss) + dcol[u];
       }
+      // instruction d = wave + u * NW fills 1 KiB at d * 1024 of the K tile,
+      // or (d - DMAS) * 1024 of the V tile (the V slot pointer is pre-shifted)
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(stage + (wave + u * NW) * 1024),
+                                       (__attribute__((address_space(3))) void*)(slot + (wave + u * NW) * 1024),
                                        16, 0, 0);
     }
   };
@@ -340,7 +351,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   // reads 16 B of key kb*32 + r in slab ks at ks*2048 + kb*1024 + k_lane
   const int k_lane = r * 32 + ((g ^ ((r >> 3) & 1)) << 4);
   auto qk = [&](int t, f32x16* s) {
-    const char* k_lds = lds + (t % ATT_STAGES) * C::STAGE + k_lane;
+    const char* k_lds = lds + (t % ATT_KSLOTS) * C::TILE + k_lane;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       s[kb] = (f32x16){};
@@ -366,7 +377,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   // softmax of one S^T tile + O^T += V^T P^T
   // O^T += V^T . P^T for tile t (P packed in registers)
   auto pv = [&](int t, const u32x4 (&pf)[2][2]) {
-    const char* v_lds = lds + (t % ATT_STAGES) * C::STAGE + C::TILE;
+    const char* v_lds = lds + (ATT_KSLOTS + t % ATT_VSLOTS) * C::TILE;
     const uint32_t vb = lds_addr(v_lds) + v_lane;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -448,10 +459,14 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   };
   // ---- prologue: DMA of tiles 0 and 1, S of tile 0
   f32x16 sa[2], sb[2];
-  if (ntiles > 0) dma_tile(0);
-  if (ntiles > 1) dma_tile(1);
+  if (ntiles > 0) {
+    dma_part(true, 0);
+    dma_part(false, 0);
+  }
+  if (ntiles > 1) dma_part(true, 1);
+  // K of tile 0 has landed (V of tile 0 and K of tile 1 may be in flight)
   if (ntiles > 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::DMA_PER_WAVE) : "memory");
-  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::DMA_PER_WAVE / 2) : "memory");
   __syncthreads();
   if (ntiles > 0 && active(0)) qk(0, sa);
 
@@ -501,16 +516,24 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
     }
     pv(t, pf);
   };
+  // Iteration t: K of tile t+1 and V of tile t have landed (this wave's
+  // DMAs: vmcnt(0); everyone's: the barrier), and every wave is done with
+  // K of tile t (its S^T was formed in iteration t-1) and V of tile t-1,
+  // whose slots now take K of tile t+2 and V of tile t+1.
+  auto issue_ahead = [&](int t) {
+    if (t + 2 < ntiles) dma_part(true, t + 2);
+    if (t + 1 < ntiles) dma_part(false, t + 1);
+  };
   auto fast_iteration = [&](int t, f32x16* s_cur, f32x16* s_next) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA of tile t+1
-    __syncthreads();  // tile t+1 visible; every wave is done with tile t-1
-    if (t + 2 < ntiles) dma_tile(t + 2);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    issue_ahead(t);
     fast(t, s_cur, s_next);
   };
   auto iteration = [&](int t, f32x16* s_cur, f32x16* s_next) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA of tile t+1
-    __syncthreads();  // tile t+1 visible; every wave is done with tile t-1
-    if (t + 2 < ntiles) dma_tile(t + 2);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    issue_ahead(t);
     if (t + 1 < ntiles && active(t + 1)) qk(t + 1, s_next);
     if (active(t)) consume(t, s_cur);
   };
@@ -669,11 +692,15 @@ __device__ __forceinline__ void attn_varlen_general_body(const AttnVarArgs& g) {
   extern "C" __global__ __launch_bounds__(NW * 64) void NAME##_varlen(const g950::AttnVarArgs p) { \
     g950::attn_body<D, F16, NW, true>(p.a, &p.v);                                      \
   }
-// 8 waves = 256 queries per workgroup (the launcher's grid assumes this)
-G950_ATTN(g950_attn_fwd_bf16_d128, 128, false, 8)
-G950_ATTN(g950_attn_fwd_bf16_d64, 64, false, 8)
-G950_ATTN(g950_attn_fwd_f16_d128, 128, true, 8)
-G950_ATTN(g950_attn_fwd_f16_d64, 64, true, 8)
+// waves per workgroup (32 queries each); the launcher reads the workgroup
+// size back from the kernel's launch bounds
+#ifndef G950_ATT_WAVES
+#define G950_ATT_WAVES 8
+#endif
+G950_ATTN(g950_attn_fwd_bf16_d128, 128, false, G950_ATT_WAVES)
+G950_ATTN(g950_attn_fwd_bf16_d64, 64, false, G950_ATT_WAVES)
+G950_ATTN(g950_attn_fwd_f16_d128, 128, true, G950_ATT_WAVES)
+G950_ATTN(g950_attn_fwd_f16_d64, 64, true, G950_ATT_WAVES)
 extern "C" __global__ __launch_bounds__(64) void g950_attn_fwd_general(const g950::AttnGenArgs p) {
   g950::attn_general_body(p);
 }

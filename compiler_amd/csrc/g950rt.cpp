@@ -197,6 +197,17 @@ int launch(g950_module* m, const std::string& name, unsigned grid, unsigned bloc
 
 bool aligned16(uintptr_t p) { return (p & 15) == 0; }
 
+// Workgroup size a kernel was built for (its launch bounds); `dflt` when
+// validating without a module.
+int kernel_threads(g950_module* m, const char* name, int dflt) {
+  if (!m) return dflt;
+  hipFunction_t f = function(m, name);
+  int v = 0;
+  if (!f || hipFuncGetAttribute(&v, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, f) != hipSuccess || v <= 0)
+    return dflt;
+  return v;
+}
+
 // ------------------------------------------------------------ row reductions
 // Register configurations in order of preference: the first whose
 // items*block vectors cover the row is used.  One wavefront per row while the
@@ -777,13 +788,15 @@ int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const 
                     v.stride[2] % 8 == 0 && o.stride[0] % 4 == 0 && o.stride[1] % 4 == 0 &&
                     o.stride[2] % 4 == 0;
   if (mfma) {
-    // 8 waves x 32 queries per workgroup (attention.hip instantiations)
-    a.nqb = (int)((S + 255) / 256);
-    const long long grid = (long long)a.nqb * Z * H;
-    if (grid > 0x7FFFFFFF) return fail(G950_USAGE, "attention: grid too large");
+    // waves x 32 queries per workgroup (attention.hip instantiations)
     char name[64];
     snprintf(name, sizeof name, "g950_attn_fwd_%s_d%lld", dt == G950_DTYPE_BFLOAT16 ? "bf16" : "f16", D);
-    return launch(m, name, (unsigned)grid, 512u, a, stream);
+    const int threads = kernel_threads(m, name, 512);
+    const int bq = threads / 2;
+    a.nqb = (int)((S + bq - 1) / bq);
+    const long long grid = (long long)a.nqb * Z * H;
+    if (grid > 0x7FFFFFFF) return fail(G950_USAGE, "attention: grid too large");
+    return launch(m, name, (unsigned)grid, (unsigned)threads, a, stream);
   }
   AttnGenArgs ga{};
   ga.a = a;
@@ -948,12 +961,14 @@ int op_flash_varlen(g950_module* m, const g950_view* views, uint32_t nviews, con
                     m8(a.k_sh) && m8(a.v_ss) && m8(a.v_sh) && a.o_ss % 4 == 0 && a.o_sh % 4 == 0 &&
                     m8(vl.q_bs) && m8(vl.k_bs) && m8(vl.v_bs) && vl.o_bs % 4 == 0 && (!paged || m8(vl.page_stride));
   if (mfma) {
-    va.a.nqb = (int)((SQ + 255) / 256);
-    const long long grid = (long long)va.a.nqb * B * H;
-    if (grid > 0x7FFFFFFF) return fail(G950_USAGE, "flash_varlen: grid too large");
     char name[64];
     snprintf(name, sizeof name, "g950_attn_fwd_%s_d%lld_varlen", dt == G950_DTYPE_BFLOAT16 ? "bf16" : "f16", D);
-    return launch(m, name, (unsigned)grid, 512u, va, stream);
+    const int threads = kernel_threads(m, name, 512);
+    const int bq = threads / 2;
+    va.a.nqb = (int)((SQ + bq - 1) / bq);
+    const long long grid = (long long)va.a.nqb * B * H;
+    if (grid > 0x7FFFFFFF) return fail(G950_USAGE, "flash_varlen: grid too large");
+    return launch(m, name, (unsigned)grid, (unsigned)threads, va, stream);
   }
   const long long rows = B * H * SQ;
   if ((rows + 63) / 64 > 0x7FFFFFFF) return fail(G950_USAGE, "flash_varlen: grid too large");
