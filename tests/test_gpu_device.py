@@ -94,6 +94,88 @@ def test_device_dequantize_autotuned_kernel():
     assert np.array_equal(d.download(yb), expect)
 
 
+def matmul_kernel(a_ptr, b_ptr, y_ptr, M, N, K):  # noqa: N803 - ops/suite/perf/matmul.py:21
+    raise AssertionError("dispatched by name, never called")
+
+
+def rms_layernorm_forward_kernel(Y, Y_row_stride, X, X_row_stride, W, W_row_stride, r, r_row_stride,  # noqa
+                                 n_cols, eps, BLOCK_SIZE):
+    raise AssertionError("dispatched by name, never called")
+
+
+def attention_forward_kernel(q_ptr, k_ptr, v_ptr, out_ptr, Z, H, N_CTX, scale,  # noqa: N803
+                             stride_qz, stride_qh, stride_qm, stride_qk, stride_kz, stride_kh, stride_kn,
+                             stride_kk, stride_vz, stride_vh, stride_vk, stride_vn, stride_oz, stride_oh,
+                             stride_om, stride_on, HEAD_DIM, BLOCK_N, CAUSAL):
+    raise AssertionError("dispatched by name, never called")
+
+
+def _upload_case(d, b, names, dt):
+    """Upload a held bundle's views the way stage_case does: bf16 cases as the
+    float32 values (rounded on upload), others in their own dtype."""
+    from tests._fixtures import values
+    out = {}
+    for n in names:
+        out[n] = d.upload(values(b, n), dt)
+    return out
+
+
+@pytest.mark.parametrize("case", ["matmul16-bfloat16-t1", "matmul128-float16-t1", "matmul-tail-float32-t1"])
+def test_device_matmul_on_held_bundles(case):
+    """The held post-run matmul bundles driven through the Device protocol:
+    outputs match the reference path's own outputs to the dtype's bar."""
+    from tests._fixtures import dtype_of, load, values
+    d = G950Device()
+    b, dt = load(case), dtype_of(case)
+    buf = _upload_case(d, b, ("a_ptr", "b_ptr"), dt)
+    y = d.alloc(values(b, "y_ptr").shape, dt)
+    M, N, K = (int(b.scalar(n)) for n in ("M", "N", "K"))
+    d.launch(matmul_kernel, None, (buf["a_ptr"], buf["b_ptr"], y, M, N, K), {})
+    rtol, atol = ref.TOLERANCES[dt]
+    ok, err = ref.isclose_verdict(d.download(y), values(b, "y_ptr"), rtol, atol)
+    assert ok, err
+
+
+@pytest.mark.parametrize("case", ["attention-bfloat16-t1", "attention-float32-t1"])
+def test_device_attention_on_held_bundles(case):
+    from tests._fixtures import dtype_of, load, values
+    d = G950Device()
+    b, dt = load(case), dtype_of(case)
+    buf = _upload_case(d, b, ("q_ptr", "k_ptr", "v_ptr"), dt)
+    out = d.alloc(values(b, "out_ptr").shape, dt)
+    strides = []
+    for t in (buf["q_ptr"], buf["k_ptr"], buf["v_ptr"], out):
+        strides += list(t.tensor.stride())
+    z, h, s, dd = values(b, "q_ptr").shape
+    d.launch(attention_forward_kernel, None,
+             (buf["q_ptr"], buf["k_ptr"], buf["v_ptr"], out, z, h, s, np.float32(b.scalar("scale")), *strides,
+              dd, 16, False), {})
+    rtol, atol = ref.TOLERANCES[dt]
+    ok, err = ref.isclose_verdict(d.download(out), values(b, "out_ptr"), rtol, atol)
+    assert ok, err
+
+
+def test_device_rms_layernorm_case_shapes():
+    """fast_rms_layernorm.py case shapes (4, 64) and (7, 67) in fp32 and bf16."""
+    d = G950Device()
+    rng = np.random.default_rng(21)
+    for dt in ("float32", "bfloat16"):
+        for rows, cols in ((4, 64), (7, 67)):
+            x = (rng.standard_normal((rows, cols)) * 0.5).astype(np.float32)
+            w = (rng.standard_normal(cols) * 0.5 + 1.0).astype(np.float32)
+            xb, wb = d.upload(x, dt), d.upload(w, dt)
+            yb, rb = d.alloc((rows, cols), dt), d.alloc((rows,), np.float32)
+            d.launch(rms_layernorm_forward_kernel, None, (yb, cols, xb, cols, wb, 1, rb, 1, cols, 1e-5, 128), {})
+            xin = ref.bf16_round(x) if dt == "bfloat16" else x
+            win = ref.bf16_round(w) if dt == "bfloat16" else w
+            ey, er = ref.rms_layernorm(xin, win, 1e-5)
+            rtol, atol = ref.TOLERANCES[dt]
+            ok, err = ref.isclose_verdict(d.download(yb), ey, rtol, atol)
+            assert ok, err
+            ok, err = ref.isclose_verdict(d.download(rb), er, 1e-5, 1e-6)
+            assert ok, err
+
+
 def test_device_refuses_other_kernels():
     d = G950Device()
     xb, yb = d.upload(np.zeros(8, np.float32)), d.alloc((8,), np.float32)
