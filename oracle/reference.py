@@ -105,7 +105,8 @@ def logsumexp(x) -> np.ndarray:
     x64 = np.asarray(x, dtype=np.float64)
     nan = np.isnan(x64).any(axis=-1)
     finite_or_inf = np.where(np.isnan(x64), -np.inf, x64)
-    mx = finite_or_inf.max(axis=-1)
+    # the kernel's running max starts at -inf (:23), so an empty row gives -inf
+    mx = finite_or_inf.max(axis=-1, initial=-np.inf)
     with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
         safe = np.where(np.isfinite(mx), mx, 0.0)
         s = np.exp(finite_or_inf - safe[..., None]).sum(axis=-1)

@@ -270,6 +270,19 @@ def test_dequant_matmul_contract():
     assert validate(rt.OP_DEQUANT_MATMUL, wrong_b, [64, 64, 64])[0] == rt.USAGE
 
 
+def test_empty_views_may_be_null_nonempty_may_not():
+    a = Args().view([3, 0], rt.DT_F32).view([3], rt.DT_F32, output=True)
+    shape, strides, dtype, out, data, storage, size = a.specs[0]
+    a.specs[0] = (shape, strides, dtype, out, 0, 0, 0)          # empty x with null pointers
+    rc, name, err = validate(rt.OP_LOGSUMEXP, a, [0])
+    assert rc == 0, err
+    b = Args().view([3, 4], rt.DT_F32).view([3], rt.DT_F32, output=True)
+    shape, strides, dtype, out, data, storage, size = b.specs[0]
+    b.specs[0] = (shape, strides, dtype, out, 0, 0, size)
+    rc, _, err = validate(rt.OP_LOGSUMEXP, b, [4])
+    assert rc == rt.REJECTED and "null" in err
+
+
 def test_view_reach_outside_storage_is_rejected():
     a = softmax_args(4, 97, rt.DT_F32)
     shape, strides, dtype, out, data, storage, size = a.specs[0]

@@ -98,6 +98,14 @@ def test_logsumexp(rows, cols, dt):
     close(host(yd), expect, rtol, atol)
 
 
+def test_logsumexp_empty_rows():
+    """n_cols = 0: the kernel's max stays -inf, which is the result
+    (logsumexp.py:23-38: maximum = -inf, an infinite maximum is returned)."""
+    x = torch.empty((3, 0), dtype=torch.float32, device=DEV)
+    y = host(ops.logsumexp(x, sync=True))
+    assert np.all(y == -np.inf)
+
+
 @pytest.mark.parametrize("cols", [97, 3000, 100000])
 def test_logsumexp_special_rows(cols):
     """NaN anywhere -> NaN (also beside +inf), +inf -> +inf, all -inf -> -inf,

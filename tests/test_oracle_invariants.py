@@ -64,6 +64,10 @@ def test_logsumexp_closed_forms_and_library():
     assert np.all(ref.logsumexp(x) <= x.max(axis=1) + math.log(97) + 1e-12)
 
 
+def test_logsumexp_empty_row_is_minus_inf():
+    assert np.all(ref.logsumexp(np.zeros((2, 0))) == -np.inf)
+
+
 def test_logsumexp_special_values():
     x = np.zeros((5, 8))
     x[0, 3] = np.nan                       # NaN anywhere -> NaN
