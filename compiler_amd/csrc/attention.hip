@@ -127,6 +127,31 @@ __device__ __forceinline__ void read_tr8(uint32_t base, u32x2 (&v)[8]) {
       : "memory");
 }
 
+// Maximum of one tile's 32 scores (per lane) with v_max3_f32: four
+// independent chains of eight, then their maximum.  fmaxf would first
+// canonicalise every MFMA result (one v_max_f32 x, x each, as its NaN rule
+// requires for inputs that may be signalling); the scores here are MFMA
+// results of finite inputs or the -inf of a mask, so plain v_max3 gives the
+// same maximum in 18 instructions instead of ~55.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+__device__ __forceinline__ float tile_max(const f32x16* s) {
+  float c[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const f32x16& t = s[h >> 1];
+    const int o = (h & 1) * 8;
+    float m = max3f(t[o], t[o + 1], t[o + 2]);
+    m = max3f(m, t[o + 3], t[o + 4]);
+    m = max3f(m, t[o + 5], t[o + 6]);
+    c[h] = max3f(m, t[o + 7], t[o + 7]);
+  }
+  return max3f(max3f(c[0], c[1], c[2]), c[3], c[3]);
+}
+
 // Rows of sequence z of a variable-length batch (flash_varlen_fwd_kernel.py:
 // 24-52): cu_seqlens row starts or fixed lengths with batch strides, and
 // seqused_k overriding the key count; paged K/V carries no key offset (the
@@ -420,11 +445,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
             s[kb][vv] = -__builtin_huge_valf();
         }
     }
-    float mt = fmaxf(s[0][0], s[0][1]);
-#pragma unroll
-    for (int vv = 2; vv < 16; vv += 2) mt = fmaxf(mt, fmaxf(s[0][vv], s[0][vv + 1]));
-#pragma unroll
-    for (int vv = 0; vv < 16; vv += 2) mt = fmaxf(mt, fmaxf(s[1][vv], s[1][vv + 1]));
+    float mt = tile_max(s);
     mt = fmaxf(mt, __shfl_xor(mt, 32)) * c2;
     // move the reference only when the tile max exceeds it by more than 8
     const bool move = mt > ms + 8.0f;
@@ -478,11 +499,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   // work while its MFMAs execute.  The rare O rescale and the P.V MFMAs follow.
   auto fast = [&](int t, f32x16* s, f32x16* s_next) {
     qk(t + 1, s_next);
-    float mt = fmaxf(s[0][0], s[0][1]);
-#pragma unroll
-    for (int vv = 2; vv < 16; vv += 2) mt = fmaxf(mt, fmaxf(s[0][vv], s[0][vv + 1]));
-#pragma unroll
-    for (int vv = 0; vv < 16; vv += 2) mt = fmaxf(mt, fmaxf(s[1][vv], s[1][vv + 1]));
+    float mt = tile_max(s);
     mt = fmaxf(mt, __shfl_xor(mt, 32)) * c2;
     const bool move = mt > ms + 8.0f;
     const float ms_new = move ? mt : ms;
