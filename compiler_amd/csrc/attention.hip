@@ -127,29 +127,22 @@ __device__ __forceinline__ void read_tr8(uint32_t base, u32x2 (&v)[8]) {
       : "memory");
 }
 
-// Maximum of one tile's 32 scores (per lane) with v_max3_f32: four
-// independent chains of eight, then their maximum.  fmaxf would first
-// canonicalise every MFMA result (one v_max_f32 x, x each, as its NaN rule
-// requires for inputs that may be signalling); the scores here are MFMA
-// results of finite inputs or the -inf of a mask, so plain v_max3 gives the
-// same maximum in 18 instructions instead of ~55.
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-  float d;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-  return d;
-}
+// Maximum of one tile's 32 scores (per lane) with v_max3_f32 (vmax3): four
+// independent chains of eight, then their maximum -- 18 instructions where
+// fmaxf's per-operand canonicalisation of the MFMA results made ~55.  The
+// scores are MFMA results of finite inputs or the -inf of a mask.
 __device__ __forceinline__ float tile_max(const f32x16* s) {
   float c[4];
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
     const f32x16& t = s[h >> 1];
     const int o = (h & 1) * 8;
-    float m = max3f(t[o], t[o + 1], t[o + 2]);
-    m = max3f(m, t[o + 3], t[o + 4]);
-    m = max3f(m, t[o + 5], t[o + 6]);
-    c[h] = max3f(m, t[o + 7], t[o + 7]);
+    float m = vmax3(t[o], t[o + 1], t[o + 2]);
+    m = vmax3(m, t[o + 3], t[o + 4]);
+    m = vmax3(m, t[o + 5], t[o + 6]);
+    c[h] = vmax3(m, t[o + 7], t[o + 7]);
   }
-  return max3f(max3f(c[0], c[1], c[2]), c[3], c[3]);
+  return vmax3(vmax3(c[0], c[1], c[2]), c[3], c[3]);
 }
 
 // Rows of sequence z of a variable-length batch (flash_varlen_fwd_kernel.py:

@@ -60,6 +60,17 @@ __device__ __forceinline__ void store_from_f32(void* p, long long i, int dt, flo
   else ((uint16_t*)p)[i] = f32_to_f16(v);
 }
 
+// max(a, b, c) in one v_max3_f32.  For values that may not be canonical
+// (loaded bits, MFMA results) fmaxf first canonicalises each operand (one
+// v_max_f32 x, x per value, its rule for possibly signalling NaNs); v_max3
+// directly treats a quiet NaN as missing, as fmaxf does.  Used where NaN
+// handling beyond that is not needed (attention's score maxima).
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
 // ---------------------------------------------------------------- DPP
 // Wavefront (64-lane) reductions with DPP row operations: quad swaps, half-row
 // and row mirrors, then row_bcast15 / row_bcast31 to fold the four 16-lane
