@@ -12,7 +12,8 @@
 //     port, the wave's Q fragment (registers, loaded once) the B port.  Each
 //     lane then holds 16 scores of ONE query (lane%32) per 32-key block, so
 //     the running max / sum of the online softmax are per-lane scalars; the
-//     two half-waves holding the same query combine with one cross-lane swap.
+//     two half-waves holding the same query exchange their maxima only on a
+//     tile where some lane's exceeds the running reference.
 //   * O^T = V^T . P^T: the A port takes V^T straight from the row-major V
 //     tile through ds_read_b64_tr_b16 (gfx950's transposing LDS read: in each
 //     16-lane group, output lane i, slot k = element i%4 of the 8 bytes read
@@ -34,14 +35,20 @@
 //     offset, bank-conflict free:  K as [16-d slab][key][32 B] with the two
 //     16-byte halves swapped on odd (key>>3); V as [32-d block][key][64 B], so
 //     the four rows a transposing read touches form one contiguous 256 B run.
-//     The S^T MFMAs of tile j+1 are issued before the softmax of tile j, so
-//     VALU and MFMA work overlap.
+//   * ping-pong: waves w and w+4 share a SIMD.  Per key tile, the MFMA phase
+//     (P.V of tile t and S^T of tile t+1, 32 MFMAs at d = 128, operand reads
+//     software-pipelined two V groups / eight K fragments ahead) of one wave
+//     runs while the other wave of the pair runs its softmax; waves 0-3 take
+//     the MFMA phase first, waves 4-7 the softmax, then the roles swap.  The
+//     MFMA phase runs at raised wave priority so its issue slots come first.
 //   * causal: a q-block stops at its diagonal tile, waves skip key tiles that
 //     lie wholly above their queries, and the mask is applied only on tiles
 //     crossing the diagonal.  Q-blocks are issued longest-first, and the Hq/Hkv
 //     query heads sharing a KV head are placed on the same XCD so the shared
 //     K/V tiles hit in that XCD's L2.
 #include "g950_common.h"
+
+#include <utility>
 
 namespace g950 {
 
@@ -127,6 +134,46 @@ __device__ __forceinline__ void read_tr8(uint32_t base, u32x2 (&v)[8]) {
       : "memory");
 }
 
+// compile-time loop: f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>)
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// LDS reads issued without a completion wait, for software pipelining.
+// lds_wait<N> completes every LDS read of the wave but the newest N (LDS
+// reads return in order; any other outstanding LDS or scalar operation only
+// makes the wait longer) and names the destination registers as in/out
+// operands, so no use of them can be scheduled before the wait and the
+// registers stay reserved while their data is in flight.
+template <int OFF>
+__device__ __forceinline__ void lds_rd128(u32x4& d, uint32_t a) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(a), "n"(OFF) : "memory");
+}
+template <int OFF>
+__device__ __forceinline__ void lds_rdtr(u32x2& d, uint32_t a) {
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(d) : "v"(a), "n"(OFF) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4& d) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(d) : "n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x2 (&v)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+               : "n"(N)
+               : "memory");
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x2 (&v)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "n"(N) : "memory");
+}
+
 // Maximum of one tile's 32 scores (per lane) with v_max3_f32 (vmax3): four
 // independent chains of eight, then their maximum -- 18 instructions where
 // fmaxf's per-operand canonicalisation of the MFMA results made ~55.  The
@@ -203,10 +250,11 @@ __device__ __forceinline__ long long paged_row(const VarlenArgs& vl, int z, int 
   return (long long)ph * vl.page_stride + (long long)(j % vl.block_size) * row_stride;
 }
 
-// NW waves x 32 queries of one (z, q-head); key tiles of 64 in a 3-stage LDS
-// ring.  Iteration j: wait for this wave's DMA of tile j+1; barrier; issue
-// the DMA of tile j+2; issue the S^T MFMAs of tile j+1; online softmax of
-// tile j on the VALU while those MFMAs execute; O^T += V^T.P^T for tile j.
+// NW waves x 32 queries of one (z, q-head); key tiles of 64 in two-slot K and
+// V rings.  Iteration t: wait for this wave's DMA of K(t+1) and V(t);
+// barrier; DMA of K(t+2) and V(t+1); then, in the order of the wave's half
+// of the ping-pong, the softmax of tile t and the MFMA phase (O^T += V^T.P^T
+// of tile t, S^T of tile t+1), or the MFMA phase and the softmax of tile t+1.
 template <int D, bool F16, int NW, bool VL>
 __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* vl) {
   using C = AttnCfg<D, NW>;
@@ -386,14 +434,14 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   for (int b = 0; b < C::DBLK; ++b) oacc[b] = (f32x16){};
   const float c2 = p.scale_log2;
   float ms = -__builtin_huge_valf();  // reference max of the row, scaled (log2 units)
-  float l_run = 0.0f;                 // this lane's partial row sum
+  float l_run[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // this lane's partial row sums (four chains)
   // transposing-read geometry: lane j of 16-lane group (g, half) reads key
   // 4g + j/4 (+ kb*32 + 16tt (+8)), d = 32b + 16*half + 4*(j%4) .. +3
   const int trj = lane & 15;
   const int v_lane = ((lane >> 5) * 4 + (trj >> 2)) * 64 + ((lane >> 4) & 1) * 32 + (trj & 3) * 8;
 
-  // softmax of one S^T tile + O^T += V^T P^T
-  // O^T += V^T . P^T for tile t (P packed in registers)
+  // O^T += V^T . P^T for tile t (P packed in registers), reads completed per
+  // group; the edge tiles' counterpart of mma_phase
   auto pv = [&](int t, const u32x4 (&pf)[2][2]) {
     const char* v_lds = lds + (ATT_KSLOTS + t % ATT_VSLOTS) * C::TILE;
     const uint32_t vb = lds_addr(v_lds) + v_lane;
@@ -422,13 +470,81 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
       }
   };
 
-  auto consume = [&](int t, f32x16* s) {
+  // MFMA phase of iteration t with its operand reads software-pipelined: P.V
+  // of tile t (four groups of transposing V reads, DBLK MFMAs each) and S^T
+  // of tile t+1 (NK K fragments, one MFMA each).  Two V groups and up to
+  // eight K fragments are in flight ahead of the MFMAs that consume them.
+  auto mma_phase = [&](int t, f32x16* s, const u32x4 (&pf)[2][2]) {
+    constexpr int R = 2 * C::DBLK;     // transposing reads per V group
+    constexpr int NK = 2 * C::DSTEPS;  // K fragments of one S^T tile
+    const uint32_t vaddr = lds_addr(lds + (ATT_KSLOTS + t % ATT_VSLOTS) * C::TILE) + v_lane;
+    const uint32_t kaddr = lds_addr(lds + ((t + 1) % ATT_KSLOTS) * C::TILE + k_lane);
+    u32x2 vt[2][R];
+    u32x4 kf[8];
+    // V group I = (kb, tt) = (I >> 1, I & 1): read Q of group I at 32-d block
+    // Q >> 1 (4096 B apart), key rows kb*32 + 16tt + 8(Q & 1) (64 B each)
+    auto vread = [&](auto ic) {
+      constexpr int I = decltype(ic)::value;
+      static_for<R>([&](auto qc) {
+        constexpr int Q = decltype(qc)::value;
+        lds_rdtr<(Q >> 1) * 4096 + (Q & 1) * 512 + (I >> 1) * 2048 + (I & 1) * 1024>(vt[I & 1][Q], vaddr);
+      });
+    };
+    auto vmma = [&](auto ic) {
+      constexpr int I = decltype(ic)::value;
+      static_for<C::DBLK>([&](auto bc) {
+        constexpr int B = decltype(bc)::value;
+        const u32x4 vf = {vt[I & 1][2 * B][0], vt[I & 1][2 * B][1], vt[I & 1][2 * B + 1][0],
+                          vt[I & 1][2 * B + 1][1]};
+        oacc[B] = mfma16<F16>(vf, pf[I >> 1][I & 1], oacc[B]);
+      });
+    };
+    // K fragment J = (kb, ks) = (J / DSTEPS, J % DSTEPS), as in qk()
+    auto kread = [&](auto jc) {
+      constexpr int J = decltype(jc)::value;
+      if constexpr (J < NK) lds_rd128<(J % C::DSTEPS) * 2048 + (J / C::DSTEPS) * 1024>(kf[J & 7], kaddr);
+    };
+    auto kmma = [&](auto jc) {
+      constexpr int J = decltype(jc)::value;
+      constexpr int KB = J / C::DSTEPS, KS = J % C::DSTEPS;
+      s[KB] = mfma16<F16>(kf[J & 7], qf[KS], KS == 0 ? (f32x16){} : s[KB]);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    // each wait names how many reads were issued after the group it completes
+    vread(I0{});
+    vread(I1{});
+    lds_wait<R>(vt[0]);
+    vmma(I0{});
+    vread(I2{});
+    lds_wait<R>(vt[1]);
+    vmma(I1{});
+    vread(I3{});
+    lds_wait<R>(vt[0]);
+    vmma(I2{});
+    static_for<4>([&](auto jc) { kread(jc); });
+    lds_wait<4>(vt[1]);
+    vmma(I3{});
+    static_for<4>([&](auto jc) { kread(std::integral_constant<int, decltype(jc)::value + 4>{}); });
+    static_for<NK>([&](auto jc) {
+      constexpr int J = decltype(jc)::value;
+      constexpr int after = (NK - J - 1) < 7 ? (NK - J - 1) : 7;  // K reads issued after fragment J
+      lds_wait<after>(kf[J & 7]);
+      kmma(jc);
+      kread(std::integral_constant<int, J + 8>{});
+    });
+  };
+
+  // online softmax of the S^T tile t held in s: mask, running max, O and l
+  // rescale, P packed to 16 bits for the B port of P.V
+  auto softmax = [&](int t, f32x16* s, u32x4 (&pf)[2][2]) {
     const int kv0 = kbeg + t * ATT_BK;
     const bool need_mask = (has_hi && kv0 + ATT_BK - 1 > qw + hi_off) || (has_lo && kv0 < qw + 31 + lo_off) ||
                            (kv0 + ATT_BK > Sk);
     if (need_mask) {
-      // key kv0 + 32kb + 8(vv>>2) + 4g + (vv&3) is kept iff its in-tile
-      // offset 32kb + 8(vv>>2) + (vv&3) <= thr (one compare per score)
+      // key kv0 + 32kb + 8(vv>>2) + 4g + (vv&3) of this lane's query my_q
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -438,16 +554,19 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
             s[kb][vv] = -__builtin_huge_valf();
         }
     }
-    float mt = tile_max(s);
-    mt = fmaxf(mt, __shfl_xor(mt, 32)) * c2;
-    // move the reference only when the tile max exceeds it by more than 8
-    const bool move = mt > ms + 8.0f;
-    if (__any(move)) {
+    // this half-wave's tile maximum (scale > 0, so scaling commutes with the
+    // maximum); the two halves holding a query combine theirs only when some
+    // lane's exceeds the reference by more than 8 -- otherwise no row moves
+    const float mh = tile_max(s) * c2;
+    if (__any(mh > ms + 8.0f)) {
+      const float mt = fmaxf(mh, __shfl_xor(mh, 32));
+      const bool move = mt > ms + 8.0f;
       const float ms_new = move ? mt : ms;
       // 0 on a row's first keys; 1 on rows that keep their reference (also a
       // row with no visible key yet, ms = -inf, beside rows that moved)
       const float alpha = move ? __builtin_amdgcn_exp2f(ms - ms_new) : 1.0f;
-      l_run *= alpha;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) l_run[j] *= alpha;
 #pragma unroll
       for (int b = 0; b < C::DBLK; ++b) oacc[b] *= alpha;
       ms = ms_new;
@@ -455,13 +574,12 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
     // a row whose keys so far are all masked keeps ms = -inf: exponent base 0
     // gives exp2(-inf) = 0 instead of NaN
     const float mb = (ms == -__builtin_huge_valf()) ? 0.0f : ms;
-    u32x4 pf[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int vv = 0; vv < 16; ++vv) {
         s[kb][vv] = __builtin_amdgcn_exp2f(fmaf(s[kb][vv], c2, -mb));
-        l_run += s[kb][vv];
+        l_run[vv & 3] += s[kb][vv];
       }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
@@ -469,10 +587,11 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
         for (int e = 0; e < 4; ++e)
           pf[kb][tt][e] = pack2(s[kb][8 * tt + 2 * e], s[kb][8 * tt + 2 * e + 1], F16);
     }
-    pv(t, pf);
   };
-  // ---- prologue: DMA of tiles 0 and 1, S of tile 0
-  f32x16 sa[2], sb[2];
+
+  // ---- prologue: DMA of K(0), V(0), K(1); S^T of tile 0
+  f32x16 s[2];
+  u32x4 pf[2][2];
   if (ntiles > 0) {
     dma_part(true, 0);
     dma_part(false, 0);
@@ -482,90 +601,39 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   if (ntiles > 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::DMA_PER_WAVE) : "memory");
   else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::DMA_PER_WAVE / 2) : "memory");
   __syncthreads();
-  if (ntiles > 0 && active(0)) qk(0, sa);
+  if (ntiles > 0 && active(0)) qk(0, s);
+  // waves w and w + NW/2 share a SIMD (waves are dealt round-robin over the
+  // four SIMDs) and run opposite halves of the ping-pong
+  const bool lead = wave < NW / 2;
+  if (lead && ntiles > 0 && active(0)) softmax(0, s, pf);
 
-  // ---- main loop, unrolled by two so the S buffers alternate without copies
-  // Interior tiles (this and the next tile active, no mask) take a branch-free
-  // path: the S^T MFMAs of tile t+1 and the softmax VALU/exp work of tile t
-  // form one basic block, interleaved one MFMA at a time with the operand
-  // read and ~10 VALU/transcendental instructions, so the wave issues VALU
-  // work while its MFMAs execute.  The rare O rescale and the P.V MFMAs follow.
-  auto fast = [&](int t, f32x16* s, f32x16* s_next) {
-    qk(t + 1, s_next);
-    float mt = tile_max(s);
-    mt = fmaxf(mt, __shfl_xor(mt, 32)) * c2;
-    const bool move = mt > ms + 8.0f;
-    const float ms_new = move ? mt : ms;
-    const float alpha = __builtin_amdgcn_exp2f(ms - ms_new);  // 1 unless moved
-    l_run *= alpha;
-    ms = ms_new;
-    u32x4 pf[2][2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int vv = 0; vv < 16; ++vv) {
-        s[kb][vv] = __builtin_amdgcn_exp2f(fmaf(s[kb][vv], c2, -ms));
-        l_run += s[kb][vv];
-      }
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          pf[kb][tt][e] = pack2(s[kb][8 * tt + 2 * e], s[kb][8 * tt + 2 * e + 1], F16);
-    }
-#pragma unroll
-    for (int i = 0; i < 2 * C::DSTEPS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // operand read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
-      __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
-    }
-    if (__any(move)) {
-#pragma unroll
-      for (int b = 0; b < C::DBLK; ++b) oacc[b] *= alpha;
-    }
-    pv(t, pf);
-  };
-  // Iteration t: K of tile t+1 and V of tile t have landed (this wave's
-  // DMAs: vmcnt(0); everyone's: the barrier), and every wave is done with
-  // K of tile t (its S^T was formed in iteration t-1) and V of tile t-1,
-  // whose slots now take K of tile t+2 and V of tile t+1.
-  auto issue_ahead = [&](int t) {
+  // ---- main loop.  Iteration t: K of tile t+1 and V of tile t have landed
+  // (this wave's DMAs: vmcnt(0); everyone's: the barrier), and every wave is
+  // done with K of tile t (its S^T was formed in iteration t-1) and V of
+  // tile t-1, whose slots now take K of tile t+2 and V of tile t+1.
+  for (int t = 0; t < ntiles; ++t) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
     if (t + 2 < ntiles) dma_part(true, t + 2);
     if (t + 1 < ntiles) dma_part(false, t + 1);
-  };
-  auto fast_iteration = [&](int t, f32x16* s_cur, f32x16* s_next) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    issue_ahead(t);
-    fast(t, s_cur, s_next);
-  };
-  auto iteration = [&](int t, f32x16* s_cur, f32x16* s_next) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    issue_ahead(t);
-    if (t + 1 < ntiles && active(t + 1)) qk(t + 1, s_next);
-    if (active(t)) consume(t, s_cur);
-  };
-  // interior tiles: below every wave's diagonal (causal) and inside Sk, with
-  // a successor tile; rounded down to even so both loops start on sa
-  int full = has_lo ? 0 : has_hi ? max(0, q0 + hi_off + 1) / ATT_BK : Sk / ATT_BK;
-  full = min(min(full, Sk / ATT_BK), ntiles - 1);
-  const int nfast = full > 0 ? (full & ~1) : 0;
-  int t = 0;
-  for (; t < nfast; t += 2) {
-    fast_iteration(t, sa, sb);
-    fast_iteration(t + 1, sb, sa);
+    const bool cur = active(t);
+    const bool nxt = t + 1 < ntiles && active(t + 1);
+    if (!lead && cur) softmax(t, s, pf);
+    if (cur && nxt) {
+      __builtin_amdgcn_s_setprio(2);
+      mma_phase(t, s, pf);
+      __builtin_amdgcn_s_setprio(0);
+    } else {
+      if (cur) pv(t, pf);
+      if (nxt) qk(t + 1, s);
+    }
+    if (lead && nxt) softmax(t + 1, s, pf);
   }
-  for (; t + 1 < ntiles; t += 2) {
-    iteration(t, sa, sb);
-    iteration(t + 1, sb, sa);
-  }
-  if (t < ntiles) iteration(t, sa, sb);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue: O = O / l ; lse = (ms + log2 l) * ln2
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_sum = (l_run[0] + l_run[1]) + (l_run[2] + l_run[3]);
+  const float l_tot = l_sum + __shfl_xor(l_sum, 32);
   if (my_q < Sq) {
     const bool empty = !(l_tot > 0.0f);  // zero or NaN
     const float inv = empty ? 1.0f : 1.0f / l_tot;

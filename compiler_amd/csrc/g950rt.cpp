@@ -781,7 +781,10 @@ int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const 
   a.causal = causal ? 1 : 0;
   if (Z == 0 || H == 0 || S == 0) return launch(m, "g950_attn_fwd_general", 0, 64, a, stream);
   if (Sk == 0) return fail(G950_USAGE, "attention: no keys");
-  const bool mfma = is_float16ish(dt) && (D == 64 || D == 128) &&
+  // the MFMA kernel's running maximum assumes scale > 0 (scaling then commutes
+  // with the maximum); other scales take the general kernel
+  const bool mfma = is_float16ish(dt) && (D == 64 || D == 128) && a.scale_log2 > 0.0f &&
+                    std::isfinite(a.scale_log2) &&
                     aligned16(q.addr()) && aligned16(k.addr()) && aligned16(v.addr()) &&
                     (o.addr() & 7) == 0 && q.stride[0] % 8 == 0 && q.stride[1] % 8 == 0 &&
                     q.stride[2] % 8 == 0 && k.stride[0] % 8 == 0 && k.stride[1] % 8 == 0 &&
@@ -957,7 +960,8 @@ int op_flash_varlen(g950_module* m, const g950_view* views, uint32_t nviews, con
   va.a = a; va.v = vl; va.D = (int)D; va.dtype = (int)dt;
   if (B == 0 || SQ == 0) return launch(m, "g950_attn_varlen_general", 0, 64u, va, stream);
   auto m8 = [](long long x) { return x % 8 == 0; };
-  const bool mfma = is_float16ish(dt) && (D == 64 || D == 128) && aligned16(q.addr()) && aligned16(k.addr()) &&
+  const bool mfma = is_float16ish(dt) && (D == 64 || D == 128) && a.scale_log2 > 0.0f &&
+                    std::isfinite(a.scale_log2) && aligned16(q.addr()) && aligned16(k.addr()) &&
                     aligned16(v.addr()) && (o.addr() & 7) == 0 && m8(a.q_ss) && m8(a.q_sh) && m8(a.k_ss) &&
                     m8(a.k_sh) && m8(a.v_ss) && m8(a.v_sh) && a.o_ss % 4 == 0 && a.o_sh % 4 == 0 &&
                     m8(vl.q_bs) && m8(vl.k_bs) && m8(vl.v_bs) && vl.o_bs % 4 == 0 && (!paged || m8(vl.page_stride));

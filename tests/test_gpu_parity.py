@@ -448,6 +448,19 @@ def test_attention_small(z, h, hkv, s, d, causal):
     close(lse.cpu().numpy(), el, 1e-4, 1e-4)
 
 
+@pytest.mark.parametrize("scale", [-0.125, 0.0])
+def test_attention_non_positive_scale_takes_general_kernel(scale):
+    """The MFMA kernel's running maximum needs scale > 0; other scales run the
+    general kernel and still match the oracle's softmax of the scaled scores."""
+    c = inputs.config4(1, 2, 1, 70, 64)
+    o, lse = ops.attention(dev(c["q"], "bfloat16"), dev(c["k"], "bfloat16"), dev(c["v"], "bfloat16"),
+                           scale=scale, causal=True, sync=True)
+    assert rt.module().last_kernel == "g950_attn_fwd_general"
+    eo, el = ref.attention(c["q"], c["k"], c["v"], scale, causal=True)
+    close(host(o), eo, 2e-2, 2e-2)
+    close(lse.cpu().numpy(), el, 1e-4, 1e-4)
+
+
 def test_attention_config4_sampled_heads():
     """Config 4 at full size; three (batch, head) pairs checked in full."""
     c = inputs.config4()
