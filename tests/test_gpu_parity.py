@@ -448,6 +448,21 @@ def test_attention_small(z, h, hkv, s, d, causal):
     close(lse.cpu().numpy(), el, 1e-4, 1e-4)
 
 
+@pytest.mark.parametrize("dt", ["bfloat16", "float16"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_every_mfma_instantiation(dt, d, causal):
+    """Every fixed-length MFMA kernel over many key tiles (the interior tiles
+    run the pipelined MFMA phase, the edges the plain one)."""
+    c = inputs.config4(1, 4, 2, 520, d)
+    o, lse = ops.attention(dev(c["q"], dt), dev(c["k"], dt), dev(c["v"], dt), causal=causal, sync=True)
+    assert rt.module().last_kernel == f"g950_attn_fwd_{'bf16' if dt == 'bfloat16' else 'f16'}_d{d}"
+    q, k, v = (host(dev(c[n], dt)) for n in ("q", "k", "v"))
+    eo, el = ref.attention(q, k, v, c["scale"], causal=causal)
+    close(host(o), eo, 2e-2, 2e-2)
+    close(lse.cpu().numpy(), el, 1e-4, 1e-4)
+
+
 @pytest.mark.parametrize("scale", [-0.125, 0.0])
 def test_attention_non_positive_scale_takes_general_kernel(scale):
     """The MFMA kernel's running maximum needs scale > 0; other scales run the
