@@ -414,6 +414,37 @@ def pmc_probe(torch, ops):
     log(f"pmc probe: copy {src.numel() * 2} B read + write; layernorm/softmax x8 each")
 
 
+def mfma_probe(torch, ops):
+    """Counter-collection workload for the MFMA-bound kernels (run under
+    rocprofv3 --pmc): C3 bf16 GEMM 8192^3 and C4 causal GQA attention, three
+    launches each after one warm-up launch."""
+    import math
+    from oracle import inputs
+    dev = "cuda:0"
+    m = n = k = 8192
+    c = inputs.config3(m, n, k)
+    a = torch.from_numpy(c["a"]).to(dev).to(torch.bfloat16)
+    bt = torch.from_numpy(c["bt"]).to(dev).to(torch.bfloat16)
+    del c
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    gemm = ops.matmul_kernel(a, bt.t(), y, m, n, k, prepare=True)
+    for _ in range(4):
+        gemm()
+    torch.cuda.synchronize()
+    del a, bt, y
+    c = inputs.config4()
+    bf = lambda x: torch.from_numpy(x).to(dev).to(torch.bfloat16)  # noqa: E731
+    q, kk, v = bf(c["q"]), bf(c["k"]), bf(c["v"])
+    o = torch.empty_like(q)
+    lse = torch.empty((4, 32, 4096), dtype=torch.float32, device=dev)
+    attn = ops.attn_fwd_causal_kernel(q, kk, v, o, 4, 32, 4096, 1 / math.sqrt(128), *q.stride(), *kk.stride(),
+                                      *v.stride(), *o.stride(), CAUSAL=True, lse_ptr=lse, prepare=True)
+    for _ in range(4):
+        attn()
+    torch.cuda.synchronize()
+    log(f"mfma probe: {gemm.kernel} x4, {attn.kernel} x4")
+
+
 def traffic_for(kernel):
     """HBM bytes per launch measured for `kernel` (profiles/hbm_traffic.json,
     from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes, copy-calibrated)."""
@@ -437,6 +468,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run only the counter-collection workload (for rocprofv3 --pmc)")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="run only the GEMM + attention counter workload (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the multi-GPU "
@@ -449,6 +482,9 @@ def main():
         sys.exit("bench.py needs the MI355X")
     if args.pmc_probe:
         pmc_probe(torch, ops)
+        return
+    if args.mfma_probe:
+        mfma_probe(torch, ops)
         return
     log("bench: headline (config 2) ...")
     value, ms_step, wall, roof, per_kernel, step_bytes = headline(torch, ops, args)
