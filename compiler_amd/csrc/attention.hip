@@ -72,9 +72,6 @@ struct AttnCfg {
   static constexpr int DSTEPS = D / 16;
 };
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // two fp32 -> one packed 16-bit pair (a in the low half): one
 // v_cvt_pk_bf16_f32 / v_cvt_pkrtz-free f16 conversion

@@ -20,6 +20,9 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // dtype codes of the a100-native-io/v1 format (a100c/runtime/a100rt.h:58-72)
 enum : int { DT_INT8 = 2, DT_INT32 = 6, DT_F16 = 10, DT_BF16 = 11, DT_F32 = 12 };

@@ -675,6 +675,16 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
   const bool fast = is_float16ish(a.v->dtype) && K % 16 == 0 && (K < 2 || (a.stride[1] == 1 && b.stride[0] == 1)) &&
                     a.stride[0] % 8 == 0 && b.stride[1] % 16 == 0 && aligned16(a.addr()) && aligned16(b.addr()) &&
                     y.stride[1] == 1 && aligned16(y.addr());
+  if (fast && M <= 16) {
+    // decode shapes: the 16-row kernel streams B, 32 columns and all of K per
+    // workgroup (8 waves, one K range each, summed in LDS)
+    g.a_s0 = a.stride[0];
+    g.b_s0 = b.stride[1];
+    const long long blocks = (N + 31) / 32;
+    if (blocks > 0x7FFFFFFF) return fail(G950_USAGE, "dequant_matmul: too many tiles");
+    return launch(m, a.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_gemm_w8a16_skinny_bf16" : "g950_gemm_w8a16_skinny_f16",
+                  (unsigned)blocks, 512u, g, stream);
+  }
   if (fast) {
     g.a_s0 = a.stride[0];
     g.b_s0 = b.stride[1];  // Bt row (n) stride

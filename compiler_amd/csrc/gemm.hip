@@ -504,6 +504,125 @@ __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
   gemm_epilogue<F16 ? GEMM_F16 : GEMM_BF16, 2, 2>(p, acc, unused, wm0, wn0, r, g);
 }
 
+// -------------------------------------- W8A16 for few rows of A (decode)
+// M <= 16: the 128-row tile would multiply mostly padding and stage 128 A
+// rows per K tile, so a decode-shaped product streams B instead.  A
+// workgroup of 8 waves owns 32 columns (two 16-column tiles) and the whole
+// K: wave w sums K range w of 8, and the waves' partial tiles are added in
+// wave order through LDS (no workspace, no second launch, the same result
+// every run).  Each wave multiplies with v_mfma_f32_16x16x32 (the A rows on
+// the A port, B columns widened from int8 on the B port).  Per 64-element
+// K step, lane (g = lane/16, i = lane%16) loads 16 contiguous int8 of column
+// n0 + 16t + i at k + 16g (64-byte runs per column) and the 32 bytes of A
+// row i at the same k: its first 8 k feed one MFMA, the next 8 a second one
+// (the two MFMAs' k sets interleave, which leaves each dot product
+// unchanged).  Steps are loaded SKINNY_STEPS at a time, before their MFMAs.
+constexpr int SKINNY_STEPS = 8;   // 64-element K steps loaded together
+constexpr int SKINNY_WAVES = 8;   // K ranges (waves) per workgroup
+constexpr int SKINNY_TILES = 2;   // 16-column tiles per workgroup
+
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   c, 0, 0, 0);
+}
+
+// 16 int8 -> 16 exact 16-bit floats, as two 8-element operands (k 0..7, 8..15)
+template <bool F16>
+__device__ __forceinline__ void widen_i8x16(const u32x4& w, u32x4& lo, u32x4& hi) {
+  uint32_t o[8];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int x = (int)w[d];
+    const float f0 = (float)((x << 24) >> 24), f1 = (float)((x << 16) >> 24);
+    const float f2 = (float)((x << 8) >> 24), f3 = (float)(x >> 24);
+    if constexpr (F16) {
+      o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f0, f1}, f16x2));
+      o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f2, f3}, f16x2));
+    } else {
+      o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f0, f1}, bf16x2));
+      o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){f2, f3}, bf16x2));
+    }
+  }
+  lo = (u32x4){o[0], o[1], o[2], o[3]};
+  hi = (u32x4){o[4], o[5], o[6], o[7]};
+}
+
+template <bool F16>
+__device__ __forceinline__ void gemm_w8a16_skinny_body(const GemmArgs& p) {
+  constexpr int T = SKINNY_TILES;
+  __shared__ f32x4 part[SKINNY_WAVES][T][64];
+  if (blockDim.x != SKINNY_WAVES * 64) return;  // launch shape must match the kernel
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int i = lane & 15;
+  const int n0 = blockIdx.x * 16 * T;
+  const int kw = (p.K + SKINNY_WAVES * 64 - 1) / (SKINNY_WAVES * 64) * 64;  // K range of one wave
+  const int kb = wave * kw;
+  const int ke = min(p.K, kb + kw);
+  // rows past M repeat row M-1 and columns past N repeat column N-1: their
+  // outputs are never stored
+  const char* arow = (const char*)p.a + (long long)min(i, p.M - 1) * p.a_s0 * 2;
+  const char* bcol[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) bcol[t] = (const char*)p.b + (long long)min(n0 + 16 * t + i, p.N - 1) * p.b_s0;
+  f32x4 acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = (f32x4){};
+  for (int k0 = kb; k0 < ke; k0 += SKINNY_STEPS * 64) {
+    // a lane whose 16 k lie past the range contributes zeros (K % 16 == 0)
+    u32x4 a0[SKINNY_STEPS], a1[SKINNY_STEPS], bw[SKINNY_STEPS][T];
+#pragma unroll
+    for (int st = 0; st < SKINNY_STEPS; ++st) {
+      const int kk = k0 + st * 64 + 16 * g;
+      if (kk < ke) {
+        a0[st] = *(const u32x4*)(arow + 2 * (long long)kk);
+        a1[st] = *(const u32x4*)(arow + 2 * (long long)kk + 16);
+#pragma unroll
+        for (int t = 0; t < T; ++t) bw[st][t] = __builtin_nontemporal_load((const u32x4*)(bcol[t] + kk));
+      } else {
+        a0[st] = a1[st] = (u32x4){};
+#pragma unroll
+        for (int t = 0; t < T; ++t) bw[st][t] = (u32x4){};
+      }
+    }
+#pragma unroll
+    for (int st = 0; st < SKINNY_STEPS; ++st)
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        u32x4 lo, hi;
+        widen_i8x16<F16>(bw[st][t], lo, hi);
+        acc[t] = mfma16x16x32<F16>(a0[st], lo, acc[t]);
+        acc[t] = mfma16x16x32<F16>(a1[st], hi, acc[t]);
+      }
+  }
+  // lane (g, i) holds rows 4g .. 4g+3 of column n0 + 16t + i; wave 0 adds
+  // the waves' tiles in wave order, scales and stores
+#pragma unroll
+  for (int t = 0; t < T; ++t) part[wave][t][lane] = acc[t];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    f32x4 sum = part[0][t][lane];
+#pragma unroll
+    for (int w = 1; w < SKINNY_WAVES; ++w) sum += part[w][t][lane];
+    const int n = n0 + 16 * t + i;
+    if (n >= p.N) continue;
+    const float sc = load_as_f32(p.bscale, n, p.bscale_dtype);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = 4 * g + j;
+      if (m < p.M) store_from_f32(p.c, (long long)m * p.c_s0 + n, p.c_dtype, sum[j] * sc);
+    }
+  }
+}
+
 // ------------------------------------------------------------ general GEMM
 // 64x64 output tile, 256 threads, each 4x4 outputs; K in steps of 16 staged
 // through LDS with bounds-checked element loads (zero fill past the edges).
@@ -581,6 +700,12 @@ G950_GEMM_MFMA(g950_gemm_f16_256x256, g950::GEMM_F16, 4, 2)
 G950_GEMM_MFMA(g950_gemm_i8_256x256, g950::GEMM_I8, 4, 2)
 extern "C" __global__ __launch_bounds__(256) void g950_gemm_w8a16_bf16_128x128(const g950::GemmArgs p) {
   g950::gemm_w8a16_body<false>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void g950_gemm_w8a16_skinny_bf16(const g950::GemmArgs p) {
+  g950::gemm_w8a16_skinny_body<false>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void g950_gemm_w8a16_skinny_f16(const g950::GemmArgs p) {
+  g950::gemm_w8a16_skinny_body<true>(p);
 }
 extern "C" __global__ __launch_bounds__(256) void g950_gemm_w8a16_f16_128x128(const g950::GemmArgs p) {
   g950::gemm_w8a16_body<true>(p);

@@ -258,6 +258,8 @@ def test_dequant_matmul_contract():
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(256, 512, 1024), [1024, 256, 512])
     assert rc == 0 and name == "g950_gemm_w8a16_bf16_128x128", err
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(16, 4096, 4096, rt.DT_F16), [4096, 16, 4096])
+    assert rc == 0 and name == "g950_gemm_w8a16_skinny_f16", err   # decode shape (M <= 16)
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 4096, 4096, rt.DT_F16), [4096, 64, 4096])
     assert rc == 0 and name == "g950_gemm_w8a16_f16_128x128", err   # split-K shape
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 64, col_b=False), [64, 64, 64])
     assert rc == 0 and name == "g950_gemm_general", err

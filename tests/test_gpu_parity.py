@@ -326,7 +326,8 @@ def test_gemm_bf16_config3_sampled(m, n, k):
 
 @pytest.mark.parametrize("dt", ["bfloat16", "float16"])
 @pytest.mark.parametrize("m,n,k", [(32, 32, 32), (33, 33, 48), (256, 256, 128), (300, 260, 192), (16, 4096, 4096),
-                                   (1, 1000, 4096), (2048, 2048, 4096)])
+                                   (1, 1000, 4096), (2048, 2048, 4096), (7, 70, 208), (16, 8192, 8192),
+                                   (5, 130, 1040), (64, 4096, 4096)])
 def test_dequant_matmul_fused(m, n, k, dt):
     """dequantize_matmul fused into the GEMM: a [M,K] in dt, b int8 ~ U{-127..127}
     (K-contiguous), scale ~ U[0,1) / 64 in dt.  Bar 2e-2 (the bf16 GEMM bar,
@@ -339,8 +340,10 @@ def test_dequant_matmul_fused(m, n, k, dt):
     ad, sd = dev(a, dt), dev(s, dt)
     bt = torch.from_numpy(np.ascontiguousarray(b.T)).to(DEV)
     y = ops.dequant_matmul(ad, bt.t(), sd, sync=True)
-    assert rt.module().last_kernel == ("g950_gemm_w8a16_%s_128x128" % ("bf16" if dt == "bfloat16" else "f16")
-                                       if k % 16 == 0 else "g950_gemm_general")
+    short = "bf16" if dt == "bfloat16" else "f16"
+    want = ("g950_gemm_general" if k % 16 else
+            f"g950_gemm_w8a16_skinny_{short}" if m <= 16 else f"g950_gemm_w8a16_{short}_128x128")
+    assert rt.module().last_kernel == want
     rows = np.arange(m) if m <= 512 else np.unique(np.r_[0, 127, 128, m - 1,
                                                         np.random.default_rng(5).integers(0, m, 24)])
     expect = ref.matmul(host(ad)[rows], ref.dequantize(b, host(sd)))
