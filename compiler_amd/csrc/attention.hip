@@ -67,7 +67,6 @@ struct AttnCfg {
   static constexpr int TILE = ATT_BK * ROW;       // one K or V tile
   static constexpr int LDS = (ATT_KSLOTS + ATT_VSLOTS) * TILE;  // K ring, then V ring
   static constexpr int DMAS = TILE / 1024;        // wave-instructions per tile
-  static constexpr int DMA_PER_WAVE = (2 * DMAS + NW - 1) / NW;
   static constexpr int DBLK = D / 32;
   static constexpr int DSTEPS = D / 16;
 };
@@ -334,19 +333,26 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   const int ntiles = kend > kbeg ? (kend - kbeg + ATT_BK - 1) / ATT_BK : 0;
 
   // ---- DMA of one K+V tile: wave-instruction d (0..2*DMAS-1) fills 1 KiB,
-  // dealt round-robin over the waves.  K instruction d = (slab ks, key half
-  // kh): 32 keys x 32 B; V instruction (block b, key quarter kq): 16 keys x 64 B.
-  // Per-lane tile-relative source offsets are computed once: instruction u
-  // of a wave is a K instruction for u < DMA_PER_WAVE / 2, a V one after.
-  // Interior tiles then cost one 64-bit add per instruction; only a tile that
-  // runs past Sk clamps key indices.
-  static_assert(C::DMAS % NW == 0 && C::DMA_PER_WAVE * NW == 2 * C::DMAS, "DMA deal");
+  // dealt round-robin over the first NL = NW/2 waves only: those are the
+  // waves that start an iteration in the MFMA phase, so the DMA issue stalls
+  // land in front of MFMA work while the other half of each SIMD pair starts
+  // its softmax straight after the barrier (1.2% over dealing the DMA to all
+  // NW waves; dealing it to the softmax half instead loses 7%).  K
+  // instruction d = (slab ks, key half kh): 32 keys x 32 B; V instruction
+  // (block b, key quarter kq): 16 keys x 64 B.  Per-lane tile-relative source
+  // offsets are computed once: instruction u of a DMA wave is a K instruction
+  // for u < DPW / 2, a V one after.  Interior tiles then cost one 64-bit add
+  // per instruction; only a tile that runs past Sk clamps key indices.
+  constexpr int NL = NW / 2;
+  constexpr int DPW = 2 * C::DMAS / NL;
+  static_assert(C::DMAS % NL == 0, "DMA deal");
+  const int dwave = wave % NL;
   const long long kstride = 2 * (long long)p.k_ss, vstride = 2 * (long long)p.v_ss;
-  int dkey[C::DMA_PER_WAVE], dcol[C::DMA_PER_WAVE];
+  int dkey[DPW], dcol[DPW];
 #pragma unroll
-  for (int u = 0; u < C::DMA_PER_WAVE; ++u) {
-    const int d = wave + u * NW;
-    if (u < C::DMA_PER_WAVE / 2) {
+  for (int u = 0; u < DPW; ++u) {
+    const int d = dwave + u * NL;
+    if (u < DPW / 2) {
       const int ks = d >> 1, key = (d & 1) * 32 + (lane >> 1);
       dkey[u] = key;
       dcol[u] = ks * 32 + (((lane & 1) ^ ((key >> 3) & 1)) * 16);
@@ -370,9 +376,10 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   // K tiles and V tiles are each issued in increasing order, so each keeps
   // its next page shift prefetched
   long long kpage_next = tile_page(0), vpage_next = kpage_next;
-  // DMA of the K half (instructions u < DMA_PER_WAVE / 2) or the V half of
-  // tile t into its ring slot
+  // DMA of the K half (instructions u < DPW / 2) or the V half of tile t into
+  // its ring slot; waves NL.. issue none
   auto dma_part = [&](bool kpart, int t) {
+    if (wave >= NL) return;
     char* slot = kpart ? lds + (t % ATT_KSLOTS) * C::TILE : lds + (ATT_KSLOTS - 1 + t % ATT_VSLOTS) * C::TILE;
     const int kv0 = kbeg + t * ATT_BK;
     const bool tail = kv0 + ATT_BK > Sk;
@@ -385,8 +392,8 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
       }
     }
 #pragma unroll
-    for (int u = 0; u < C::DMA_PER_WAVE; ++u) {
-      const bool is_k = u < C::DMA_PER_WAVE / 2;
+    for (int u = 0; u < DPW; ++u) {
+      const bool is_k = u < DPW / 2;
       if (is_k != kpart) continue;
       const char* base = is_k ? kbase : vbase;
       const long long stride = is_k ? kstride : vstride;
@@ -400,7 +407,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
       // instruction d = wave + u * NW fills 1 KiB at d * 1024 of the K tile,
       // or (d - DMAS) * 1024 of the V tile (the V slot pointer is pre-shifted)
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(slot + (wave + u * NW) * 1024),
+                                       (__attribute__((address_space(3))) void*)(slot + (dwave + u * NL) * 1024),
                                        16, 0, 0);
     }
   };
@@ -595,8 +602,8 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   }
   if (ntiles > 1) dma_part(true, 1);
   // K of tile 0 has landed (V of tile 0 and K of tile 1 may be in flight)
-  if (ntiles > 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::DMA_PER_WAVE) : "memory");
-  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::DMA_PER_WAVE / 2) : "memory");
+  if (ntiles > 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DPW) : "memory");
+  else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DPW / 2) : "memory");
   __syncthreads();
   if (ntiles > 0 && active(0)) qk(0, s);
   // waves w and w + NW/2 share a SIMD (waves are dealt round-robin over the
