@@ -44,6 +44,8 @@ struct GemmArgs {
   int kchunk;         // split-K: K elements per range (multiple of the K tile)
   float* part;        // split-K: [splits, M, N] fp32 partial products
   int* tile_count;    // split-K: per-tile arrival counters, zero between calls
+  const void* cscale; // bf16/f16 MFMA GEMM: optional per-column output scale
+  int cscale_dtype;   //   (float dtype code), applied in the epilogue
 };
 
 struct AttnArgs {

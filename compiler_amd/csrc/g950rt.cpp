@@ -685,6 +685,34 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
     return launch(m, a.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_gemm_w8a16_skinny_bf16" : "g950_gemm_w8a16_skinny_f16",
                   (unsigned)blocks, 512u, g, stream);
   }
+  // Many output tiles: widen B once into an exact bf16 / f16 copy in the
+  // workspace and run the 256x256 GEMM with the column scale in its epilogue.
+  // The fused kernel converts every B element once per 128-row output tile,
+  // which costs more than one copy (3 bytes per weight through HBM) as soon as
+  // the 256x256 tiles fill the chip.
+  const long long cus = m ? m->cus : 256;
+  const bool bf16 = a.v->dtype == G950_DTYPE_BFLOAT16;
+  if (fast && K % 64 == 0 && ((M + 255) / 256) * ((N + 255) / 256) >= cus &&
+      (unsigned long long)N * K * 2 <= (1ull << 31)) {
+    GemmArgs w{};
+    w.b = g.b; w.b_s0 = b.stride[1]; w.N = (int)N; w.K = (int)K;
+    void* ws = nullptr;
+    if (m)
+      if (int rc = workspace(m, stream, (size_t)(N * K * 2), &ws)) return rc;
+    w.c = ws;
+    const long long chunks = N * (K / 16);
+    if (int rc = launch(m, bf16 ? "g950_widen_i8_bf16" : "g950_widen_i8_f16", (unsigned)((chunks + 255) / 256), 256u,
+                        w, stream))
+      return rc;
+    g.b = ws; g.b_dtype = (int)a.v->dtype;
+    g.a_s0 = a.stride[0];
+    g.b_s0 = K;
+    g.bscale = nullptr;
+    g.cscale = s.v->data; g.cscale_dtype = (int)s.v->dtype;
+    const int tiles = gemm_tiles(g);
+    if (tiles < 0) return fail(G950_USAGE, "dequant_matmul: too many tiles");
+    return launch(m, bf16 ? "g950_gemm_bf16_256x256" : "g950_gemm_f16_256x256", (unsigned)tiles, 512u, g, stream);
+  }
   if (fast) {
     g.a_s0 = a.stride[0];
     g.b_s0 = b.stride[1];  // Bt row (n) stride
@@ -697,7 +725,6 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
     // CU, K ranges of whole 64-element tiles, at least 512 long.  Measured on
     // MI355X at N = K = 8192: M = 16 163 -> 59 us, M = 1 162 -> 42 us; at
     // M = 128 the partial traffic made it slower (165 -> 212 us).
-    const long long cus = m ? m->cus : 256;
     long long splits = 1;
     if (tiles * 2 < cus && K >= 1024 && M <= 64) {
       splits = std::min((2 * cus + tiles - 1) / tiles, K / 512);

@@ -104,6 +104,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = accf[mi][ni][q * 4 + e];
+          if (p.cscale) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              v[e] *= (n + e < p.N) ? load_as_f32(p.cscale, n + e, p.cscale_dtype) : 0.0f;
+          }
         }
         char* crow = (char*)p.c + (long long)m * p.c_s0 * (p.c_dtype == DT_F32 ? 4 : 2);
         if (p.c_dtype == DT_F32) {
@@ -552,6 +557,24 @@ __device__ __forceinline__ void widen_i8x16(const u32x4& w, u32x4& lo, u32x4& hi
   hi = (u32x4){o[4], o[5], o[6], o[7]};
 }
 
+// Exact copy of an int8 weight matrix Bt[N, K] (row stride b_s0 bytes, K a
+// multiple of 16) into a contiguous bf16 / f16 Bt[N, K] at p.c: one thread per
+// 16 int8 values, one 16-byte load and two 16-byte stores.  Every int8 value
+// is representable in both formats, so the copy loses nothing.
+template <bool F16>
+__device__ __forceinline__ void widen_i8_body(const GemmArgs& p) {
+  const long long chunks = p.K / 16;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)p.N * chunks) return;
+  const long long n = i / chunks, c = i - n * chunks;
+  const u32x4 w = *(const u32x4*)((const char*)p.b + n * p.b_s0 + c * 16);
+  u32x4 lo, hi;
+  widen_i8x16<F16>(w, lo, hi);
+  u32x4* dst = (u32x4*)((char*)p.c + (n * p.K + c * 16) * 2);
+  dst[0] = lo;
+  dst[1] = hi;
+}
+
 template <bool F16>
 __device__ __forceinline__ void gemm_w8a16_skinny_body(const GemmArgs& p) {
   constexpr int T = SKINNY_TILES;
@@ -715,4 +738,10 @@ extern "C" __global__ __launch_bounds__(256) void g950_gemm_general(const g950::
 }
 extern "C" __global__ __launch_bounds__(256) void g950_gemm_general_i8(const g950::GemmArgs p) {
   g950::gemm_general_body<true>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void g950_widen_i8_bf16(const g950::GemmArgs p) {
+  g950::widen_i8_body<false>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void g950_widen_i8_f16(const g950::GemmArgs p) {
+  g950::widen_i8_body<true>(p);
 }

@@ -261,6 +261,10 @@ def test_dequant_matmul_contract():
     assert rc == 0 and name == "g950_gemm_w8a16_skinny_f16", err   # decode shape (M <= 16)
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 4096, 4096, rt.DT_F16), [4096, 64, 4096])
     assert rc == 0 and name == "g950_gemm_w8a16_f16_128x128", err   # split-K shape
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(4096, 4096, 256), [256, 4096, 4096])
+    assert rc == 0 and name == "g950_gemm_bf16_256x256", err   # B widened once, 256 tiles
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(4096, 4096, 208), [208, 4096, 4096])
+    assert rc == 0 and name == "g950_gemm_w8a16_bf16_128x128", err   # K not a multiple of 64
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 64, col_b=False), [64, 64, 64])
     assert rc == 0 and name == "g950_gemm_general", err
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 40), [40, 64, 64])
