@@ -263,6 +263,10 @@ def test_dequant_matmul_contract():
     assert rc == 0 and name == "g950_gemm_w8a16_f16_128x128", err   # split-K shape
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(4096, 4096, 256), [256, 4096, 4096])
     assert rc == 0 and name == "g950_gemm_bf16_256x256", err   # B widened once, 256 tiles
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(1024, 8192, 128), [128, 1024, 8192])
+    assert rc == 0 and name == "g950_gemm_w8a16_bf16_128x128", err   # 128 tiles: half the CUs
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(1025, 8192, 128), [128, 1025, 8192])
+    assert rc == 0 and name == "g950_gemm_bf16_256x256", err   # 160 tiles
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(4096, 4096, 208), [208, 4096, 4096])
     assert rc == 0 and name == "g950_gemm_w8a16_bf16_128x128", err   # K not a multiple of 64
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 64, col_b=False), [64, 64, 64])

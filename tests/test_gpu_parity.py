@@ -327,7 +327,8 @@ def test_gemm_bf16_config3_sampled(m, n, k):
 @pytest.mark.parametrize("dt", ["bfloat16", "float16"])
 @pytest.mark.parametrize("m,n,k", [(32, 32, 32), (33, 33, 48), (256, 256, 128), (300, 260, 192), (16, 4096, 4096),
                                    (1, 1000, 4096), (2048, 2048, 4096), (7, 70, 208), (16, 8192, 8192),
-                                   (5, 130, 1040), (64, 4096, 4096), (4096, 4096, 256), (4100, 4096, 320)])
+                                   (5, 130, 1040), (64, 4096, 4096), (4096, 4096, 256), (4100, 4096, 320),
+                                   (1100, 8192, 128), (1024, 8192, 128)])
 def test_dequant_matmul_fused(m, n, k, dt):
     """dequantize_matmul fused into the GEMM: a [M,K] in dt, b int8 ~ U{-127..127}
     (K-contiguous), scale ~ U[0,1) / 64 in dt.  Bar 2e-2 (the bf16 GEMM bar,
@@ -341,8 +342,8 @@ def test_dequant_matmul_fused(m, n, k, dt):
     bt = torch.from_numpy(np.ascontiguousarray(b.T)).to(DEV)
     y = ops.dequant_matmul(ad, bt.t(), sd, sync=True)
     short = "bf16" if dt == "bfloat16" else "f16"
-    # at least one 256x256 tile per CU: B is widened once and the bf16/f16 GEMM runs
-    widened = k % 64 == 0 and -(-m // 256) * -(-n // 256) >= 256
+    # more 256x256 tiles than half the CUs: B is widened once and the bf16/f16 GEMM runs
+    widened = k % 64 == 0 and 2 * -(-m // 256) * -(-n // 256) > 256
     want = ("g950_gemm_general" if k % 16 else
             f"g950_gemm_w8a16_skinny_{short}" if m <= 16 else
             f"g950_gemm_{short}_256x256" if widened else f"g950_gemm_w8a16_{short}_128x128")
