@@ -2,7 +2,8 @@
 //
 // Operator semantics: ops/suite/perf/attn_fwd_causal.py:20-55 (scores
 // q.k*scale, causal mask key <= query, softmax, P.V); GQA head map
-// h_kv = h // (Hq/Hkv) (ops/suite/dev/gqa.py:29); online softmax over key
+// h_kv = h // GROUP (ops/suite/dev/gqa.py:29; GROUP = Hq/Hkv for the
+// attention contracts, the kernel's own constexpr for gqa_kernel); online softmax over key
 // tiles (gqa.py:43-58); per-row logsumexp of the scaled scores,
 // lse = rowmax + log(rowsum), +inf for an empty row
 // (ops/suite/dev/flash_varlen_fwd_kernel.py:309, :318-320).
@@ -270,8 +271,8 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   const int qb = p.nqb - 1 - pid / per_qb;
   const int i = pid % per_qb;
   int z, h;
-  const int G = p.Hq / p.Hkv;
-  if ((per_qb % (8 * G)) == 0) {
+  const int G = p.group;
+  if (p.Hq == p.Hkv * G && (per_qb % (8 * G)) == 0) {
     const int xcd = i & 7;
     const int j = i >> 3;
     const int zk = xcd + 8 * (j / G);  // (z, kv-head) pair index
@@ -676,7 +677,7 @@ __device__ __forceinline__ void attn_general_body(const AttnGenArgs& g) {
   const int qi = row % p.Sq;
   const int h = (row / p.Sq) % p.Hq;
   const int z = row / ((long long)p.Sq * p.Hq);
-  const int hk = h / (p.Hq / p.Hkv);
+  const int hk = h / p.group;
   const long long qo = (long long)z * p.q_sz + (long long)h * p.q_sh + (long long)qi * p.q_ss;
   const long long kb = (long long)z * p.k_sz + (long long)hk * p.k_sh;
   const long long vb = (long long)z * p.v_sz + (long long)hk * p.v_sh;
@@ -724,7 +725,7 @@ __device__ __forceinline__ void attn_varlen_general_body(const AttnVarArgs& g) {
   const int z = row / ((long long)p.Sq * p.Hq);
   const SeqGeom sg = varlen_geom(p, vl, z);
   if (qi >= sg.q_len) return;
-  const int hk = h / (p.Hq / p.Hkv);
+  const int hk = h / p.group;
   const int dg = sg.k_len - sg.q_len;
   const int jlo = vl.local ? max(0, qi + dg - vl.wl) : 0;
   const int jhi = (p.causal || vl.local) ? min(sg.k_len - 1, qi + dg + vl.wr) : sg.k_len - 1;

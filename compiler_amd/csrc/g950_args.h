@@ -46,6 +46,24 @@ struct GemmArgs {
   int* tile_count;    // split-K: per-tile arrival counters, zero between calls
   const void* cscale; // bf16/f16 MFMA GEMM: optional per-column output scale
   int cscale_dtype;   //   (float dtype code), applied in the epilogue
+  // int8 MFMA GEMM with an unsigned operand: the kernel multiplies u - 128
+  // (the byte XOR 0x80, a signed int8) and adds back, modulo 2^32,
+  //   128 * rsum[m] (B unsigned) + 128 * csum[n] (A unsigned) - 16384 * K (both)
+  // where rsum / csum are the int32 sums over k of A's rows / B's columns
+  const int* rsum;
+  const int* csum;
+};
+
+// Sums over k of int8 / uint8 rows (A[m, :] and Bt[n, :], K-contiguous):
+// out[0 .. a_rows) for A, out[a_rows .. a_rows + b_rows) for B, modulo 2^32.
+struct I8SumArgs {
+  const void* a;
+  const void* b;
+  int* out;
+  long long a_s0, b_s0;  // row strides in bytes
+  int a_rows, b_rows;    // 0: that operand's sums are not needed
+  int a_signed, b_signed;
+  int K;
 };
 
 struct AttnArgs {
@@ -62,7 +80,8 @@ struct AttnArgs {
   int Z, Hq, Hkv, Sq, Sk;
   float scale_log2;  // scale * log2(e)
   int causal;
-  int nqb;           // query blocks of 128
+  int nqb;           // query blocks
+  int group;         // query heads per KV head: KV head of query head h is h / group
 };
 
 struct CopyArgs {

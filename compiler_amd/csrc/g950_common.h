@@ -25,7 +25,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // dtype codes of the a100-native-io/v1 format (a100c/runtime/a100rt.h:58-72)
-enum : int { DT_INT8 = 2, DT_INT32 = 6, DT_F16 = 10, DT_BF16 = 11, DT_F32 = 12 };
+enum : int { DT_INT8 = 2, DT_UINT8 = 3, DT_INT32 = 6, DT_F16 = 10, DT_BF16 = 11, DT_F32 = 12 };
 
 struct bf16_t { uint16_t bits; };
 struct f16_t { uint16_t bits; };
@@ -91,6 +91,14 @@ struct OpSum {
 struct OpMax {
   static __device__ __forceinline__ float apply(float a, float b) { return fmaxf(a, b); }
   static constexpr float identity = -__builtin_huge_valf();
+};
+
+// 32-bit modular integer sum (carried through the float-typed DPP helper as bits)
+struct OpSumU32 {
+  static __device__ __forceinline__ float apply(float a, float b) {
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, a) + __builtin_bit_cast(uint32_t, b));
+  }
+  static constexpr float identity = 0.0f;
 };
 
 template <class Op>

@@ -87,11 +87,16 @@ struct View {
   uintptr_t addr() const { return (uintptr_t)v->data; }
 };
 
+// ndim < 0: any rank from 1 to 8 (views the kernel addresses as flat arrays)
 int check_view(const g950_view* views, uint32_t idx, const char* name, int ndim, View& out,
                bool output) {
   const g950_view& v = views[idx];
   out.name = name;
   out.v = &v;
+  if (ndim < 0) {
+    if (v.ndim < 1 || v.ndim > 8) return fail(G950_REJECTED, "view %s: rank %u (1..8 accepted)", name, v.ndim);
+    ndim = (int)v.ndim;
+  }
   if ((int)v.ndim != ndim)
     return fail(G950_REJECTED, "view %s: rank %u, contract needs %d", name, v.ndim, ndim);
   if (!v.shape || !v.strides) return fail(G950_REJECTED, "view %s: null shape/strides", name);
@@ -122,6 +127,22 @@ int check_view(const g950_view* views, uint32_t idx, const char* name, int ndim,
       return fail(G950_REJECTED, "view %s: reach [%lld, %lld) outside its %llu-byte storage", name,
                   (long long)(base + lo), (long long)(base + hi + out.isz),
                   (unsigned long long)v.storage_size);
+  }
+  return G950_OK;
+}
+
+// A view the reference kernel addresses as one flat element array (base
+// pointer plus scalar offsets): any rank, C-contiguous; `elems` = its length.
+int flat_view(const g950_view* views, uint32_t idx, const char* name, View& out, bool output,
+              long long& elems) {
+  if (int rc = check_view(views, idx, name, -1, out, output)) return rc;
+  elems = 1;
+  long long expect = 1;
+  for (int i = out.nd - 1; i >= 0; --i) {
+    if (out.shape[i] > 1 && out.stride[i] != expect)
+      return fail(G950_USAGE, "view %s: must be contiguous (the kernel indexes it as a flat array)", name);
+    expect *= out.shape[i];
+    elems *= out.shape[i];
   }
   return G950_OK;
 }
@@ -248,7 +269,9 @@ int workspace(g950_module* m, void* stream, size_t bytes, void** out) {
       (void)hipFree(w.first);
       w = {nullptr, 0};
     }
-    const size_t n = (bytes < (size_t)65536 ? (size_t)65536 : bytes * 2 + 255) & ~(size_t)255;
+    // headroom for a larger next call, at most 64 MiB beyond the request
+    const size_t grow = std::min(bytes, (size_t)64 << 20);
+    const size_t n = (bytes < (size_t)65536 ? (size_t)65536 : bytes + grow + 255) & ~(size_t)255;
     if (hipError_t e = hipMalloc(&w.first, n)) {
       w = {nullptr, 0};
       return fail(G950_RESOURCE, "workspace: hipMalloc(%zu): %s", n, hipGetErrorString(e));
@@ -463,6 +486,83 @@ int op_layernorm(g950_module* m, const g950_view* views, uint32_t nviews, const 
   return launch_rows(m, "layernorm", a, x.v->dtype, x, y, &w, &b, stream);
 }
 
+// softmax_kernel_inner (ops/suite/dev/softmax_kernel_inner.py:12-72): row
+// softmax of M rows of N contiguous elements at input_ptr + m * N, written to
+// output_ptr + m * N (flat buffers; the masked tail reads -inf).
+int op_softmax_inner(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+                     uint32_t nsc, void* stream) {
+  if (nviews != 2 || nsc != 2)
+    return fail(G950_USAGE, "softmax_inner: needs views (input_ptr, output_ptr), scalars (M, N)");
+  View x, y;
+  long long nx, ny, M, N;
+  if (int rc = flat_view(views, 0, "input_ptr", x, false, nx)) return rc;
+  if (int rc = flat_view(views, 1, "output_ptr", y, true, ny)) return rc;
+  if (!is_float(x.v->dtype) || x.v->dtype != y.v->dtype)
+    return fail(G950_USAGE, "softmax_inner: input/output dtypes %s/%s unsupported (float32, bfloat16, float16, same)",
+                dtname(x.v->dtype), dtname(y.v->dtype));
+  if (int rc = scalar_int(&sc[0], "M", M)) return rc;
+  if (int rc = scalar_int(&sc[1], "N", N)) return rc;
+  if (M < 0 || N < 0 || M > 0x7FFFFFFF || N > 0x7FFFFFFF) return fail(G950_USAGE, "softmax_inner: M, N out of range");
+  if (M * N > nx || M * N > ny)
+    return fail(G950_USAGE, "softmax_inner: M x N = %lld elements exceed input_ptr (%lld) or output_ptr (%lld)",
+                M * N, nx, ny);
+  RowArgs a{};
+  a.x = x.v->data; a.y = y.v->data;
+  a.x_row = N; a.y_row = N;
+  a.rows = (int)M; a.cols = (int)N;
+  if (M == 0 || N == 0) return launch(m, "g950_rr_softmax_f32_v1_i1_b64", 0, 64u, a, stream);  // nothing stored
+  return launch_rows(m, "softmax", a, x.v->dtype, x, y, nullptr, nullptr, stream);
+}
+
+// _layer_norm_forward_row (ops/suite/dev/layer_norm_forward_row.py:11-36):
+// flat buffers addressed by the row-stride scalars; n_rows, n_cols and eps
+// are the kernel's constexprs.
+int op_layernorm_row(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
+                     uint32_t nsc, void* stream) {
+  if (nviews != 6 || nsc != 7)
+    return fail(G950_USAGE, "layer_norm_forward_row: needs views (B_ptr, Mean_ptr, RSTD_ptr, W_ptr, X_ptr, Y_ptr), "
+                "scalars (Mean_row_stride, RSTD_row_stride, X_row_stride, Y_row_stride, eps, n_cols, n_rows)");
+  View b, mean, rstd, w, x, y;
+  long long nb, nm, nr, nw, nx, ny;
+  if (int rc = flat_view(views, 0, "B_ptr", b, false, nb)) return rc;
+  if (int rc = flat_view(views, 1, "Mean_ptr", mean, true, nm)) return rc;
+  if (int rc = flat_view(views, 2, "RSTD_ptr", rstd, true, nr)) return rc;
+  if (int rc = flat_view(views, 3, "W_ptr", w, false, nw)) return rc;
+  if (int rc = flat_view(views, 4, "X_ptr", x, false, nx)) return rc;
+  if (int rc = flat_view(views, 5, "Y_ptr", y, true, ny)) return rc;
+  const uint32_t dt = x.v->dtype;
+  if (!is_float(dt) || y.v->dtype != dt || w.v->dtype != dt || b.v->dtype != dt)
+    return fail(G950_USAGE, "layer_norm_forward_row: X_ptr, Y_ptr, W_ptr, B_ptr must share one float dtype");
+  if (!is_float(mean.v->dtype) || mean.v->dtype != rstd.v->dtype)
+    return fail(G950_USAGE, "layer_norm_forward_row: Mean_ptr/RSTD_ptr must share one float dtype");
+  long long ms, rs, xs, ys, nc, nrow;
+  double eps;
+  if (int rc = scalar_int(&sc[0], "Mean_row_stride", ms)) return rc;
+  if (int rc = scalar_int(&sc[1], "RSTD_row_stride", rs)) return rc;
+  if (int rc = scalar_int(&sc[2], "X_row_stride", xs)) return rc;
+  if (int rc = scalar_int(&sc[3], "Y_row_stride", ys)) return rc;
+  if (int rc = scalar_float(&sc[4], "eps", eps)) return rc;
+  if (int rc = scalar_int(&sc[5], "n_cols", nc)) return rc;
+  if (int rc = scalar_int(&sc[6], "n_rows", nrow)) return rc;
+  if (nc <= 0 || nrow < 0 || nc > 0x7FFFFFFF || nrow > 0x7FFFFFFF)
+    return fail(G950_USAGE, "layer_norm_forward_row: n_cols must be positive, n_rows non-negative");
+  if (ms < 0 || rs < 0 || xs < 0 || ys < 0) return fail(G950_USAGE, "layer_norm_forward_row: negative row stride");
+  if (nrow > 1 && (ys < nc || ms < 1 || rs < 1))
+    return fail(G950_USAGE, "layer_norm_forward_row: output rows overlap (Y_row_stride < n_cols or a zero statistic stride)");
+  if (nw < nc || nb < nc) return fail(G950_USAGE, "layer_norm_forward_row: W_ptr/B_ptr need n_cols entries");
+  if (nrow > 0 && ((nrow - 1) * xs + nc > nx || (nrow - 1) * ys + nc > ny || (nrow - 1) * ms + 1 > nm ||
+                   (nrow - 1) * rs + 1 > nr))
+    return fail(G950_USAGE, "layer_norm_forward_row: n_rows rows exceed X_ptr, Y_ptr, Mean_ptr or RSTD_ptr");
+  RowArgs a{};
+  a.x = x.v->data; a.y = y.v->data; a.w = w.v->data; a.b = b.v->data;
+  a.stat0 = mean.v->data; a.stat1 = rstd.v->data;
+  a.x_row = xs; a.y_row = ys; a.stat0_stride = ms; a.stat1_stride = rs;
+  a.rows = (int)nrow; a.cols = (int)nc;
+  a.eps = (float)eps; a.stat_dtype = (int)mean.v->dtype;
+  if (nrow == 0) return launch(m, "g950_rr_lnrow_f32_v1_i1_b64", 0, 64u, a, stream);
+  return launch_rows(m, "lnrow", a, dt, x, y, &w, &b, stream);
+}
+
 // --------------------------------------------------------------------- GEMM
 int gemm_tiles(GemmArgs& g) {
   const long long tm = (g.M + 255) / 256, tn = (g.N + 255) / 256;
@@ -542,14 +642,18 @@ int op_matmul_i8(g950_module* m, const g950_view* views, uint32_t nviews, const 
   } else {
     if (int rc = check_view(views, 2, "c_ptr", 2, y, true)) return rc;
   }
-  if (a.v->dtype != G950_DTYPE_INT8 || b.v->dtype != G950_DTYPE_INT8)
-    return fail(G950_USAGE, "matmul_i8: operands must be int8");
+  auto byte_int = [](uint32_t dt) { return dt == G950_DTYPE_INT8 || dt == G950_DTYPE_UINT8; };
+  if (!byte_int(a.v->dtype) || !byte_int(b.v->dtype))
+    return fail(G950_USAGE, "matmul_i8: operands must be int8 or uint8");
   long long M, N, K;
   if (int rc = gemm_views(a, b, y, sc, M, N, K)) return rc;
   GemmArgs g{};
   g.a = a.v->data; g.b = b.v->data;
   g.M = (int)M; g.N = (int)N; g.K = (int)K;
-  g.a_dtype = g.b_dtype = G950_DTYPE_INT8;
+  g.a_dtype = (int)a.v->dtype;
+  g.b_dtype = (int)b.v->dtype;
+  // signedness pair (a100c/plan/tiles.py:121-126): bit 0 A unsigned, bit 1 B unsigned
+  const int umask = (a.v->dtype == G950_DTYPE_UINT8 ? 1 : 0) | (b.v->dtype == G950_DTYPE_UINT8 ? 2 : 0);
   if (dequant) {
     if (sa.v->dtype != G950_DTYPE_FLOAT32 || sb.v->dtype != G950_DTYPE_FLOAT32)
       return fail(G950_USAGE, "matmul_i8_dequant: scales must be float32");
@@ -572,7 +676,29 @@ int op_matmul_i8(g950_module* m, const g950_view* views, uint32_t nviews, const 
     g.b_s0 = b.stride[1];
     const int tiles = gemm_tiles(g);
     if (tiles < 0) return fail(G950_USAGE, "matmul_i8: too many tiles");
-    return launch(m, "g950_gemm_i8_256x256", (unsigned)tiles, 512u, g, stream);
+    static const char* const names[4] = {"g950_gemm_i8_256x256", "g950_gemm_u8s8_256x256",
+                                         "g950_gemm_s8u8_256x256", "g950_gemm_u8u8_256x256"};
+    if (umask) {
+      // the MFMA multiplies u - 128 for an unsigned operand: first the sums
+      // over k its correction needs (A's rows if B is unsigned, B's columns
+      // if A is), into the workspace
+      I8SumArgs sa{};
+      sa.a = g.a; sa.b = g.b; sa.a_s0 = g.a_s0; sa.b_s0 = g.b_s0;
+      sa.a_rows = (umask & 2) ? (int)M : 0;
+      sa.b_rows = (umask & 1) ? (int)N : 0;
+      sa.a_signed = a.v->dtype == G950_DTYPE_INT8;
+      sa.b_signed = b.v->dtype == G950_DTYPE_INT8;
+      sa.K = (int)K;
+      const long long rows = (long long)sa.a_rows + sa.b_rows;
+      void* ws = nullptr;
+      if (m)
+        if (int rc = workspace(m, stream, (size_t)rows * 4, &ws)) return rc;
+      sa.out = (int*)ws;
+      g.rsum = (umask & 2) ? sa.out : nullptr;
+      g.csum = (umask & 1) ? sa.out + sa.a_rows : nullptr;
+      if (int rc = launch(m, "g950_i8_sums", (unsigned)((rows + 3) / 4), 256u, sa, stream)) return rc;
+    }
+    return launch(m, names[umask], (unsigned)tiles, 512u, g, stream);
   }
   if (!dequant && N > 1 && y.stride[1] != 1) return fail(G950_USAGE, "matmul_i8: c_ptr layout");
   g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
@@ -693,13 +819,16 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
   // M = 1024 (128 tiles) 186 us fused vs 148 + 36 us; M = 1536 334 vs 172 + 36.
   const long long cus = m ? m->cus : 256;
   const bool bf16 = a.v->dtype == G950_DTYPE_BFLOAT16;
-  if (fast && K % 64 == 0 && 2 * ((M + 255) / 256) * ((N + 255) / 256) > cus &&
-      (unsigned long long)N * K * 2 <= (1ull << 31)) {
+  void* wide = nullptr;
+  bool widened = fast && K > 0 && K % 64 == 0 && 2 * ((M + 255) / 256) * ((N + 255) / 256) > cus &&
+                 (unsigned long long)N * K * 2 <= (1ull << 31);
+  // without the workspace for the copy, the fused kernel below (which needs
+  // none) serves the call
+  if (widened && m && workspace(m, stream, (size_t)(N * K * 2), &wide) != G950_OK) widened = false;
+  if (widened) {
     GemmArgs w{};
     w.b = g.b; w.b_s0 = b.stride[1]; w.N = (int)N; w.K = (int)K;
-    void* ws = nullptr;
-    if (m)
-      if (int rc = workspace(m, stream, (size_t)(N * K * 2), &ws)) return rc;
+    void* ws = wide;
     w.c = ws;
     const long long chunks = N * (K / 16);
     if (int rc = launch(m, bf16 ? "g950_widen_i8_bf16" : "g950_widen_i8_f16", (unsigned)((chunks + 255) / 256), 256u,
@@ -754,6 +883,9 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
 }
 
 // ---------------------------------------------------------------- attention
+int launch_attention(g950_module* m, AttnArgs& a, uint32_t dt, long long D, const View& q, const View& k,
+                     const View& v, const View& o, void* stream);
+
 int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
                  uint32_t nsc, bool with_lse, void* stream) {
   const uint32_t want = with_lse ? 5 : 4;
@@ -817,8 +949,17 @@ int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const 
   a.Z = (int)Z; a.Hq = (int)H; a.Hkv = (int)Hkv; a.Sq = (int)S; a.Sk = (int)Sk;
   a.scale_log2 = (float)(scale * 1.4426950408889634);
   a.causal = causal ? 1 : 0;
-  if (Z == 0 || H == 0 || S == 0) return launch(m, "g950_attn_fwd_general", 0, 64, a, stream);
-  if (Sk == 0) return fail(G950_USAGE, "attention: no keys");
+  a.group = (int)(H / Hkv);
+  return launch_attention(m, a, dt, D, q, k, v, o, stream);
+}
+
+// Pick and launch the attention kernel for checked views (q/k/v/o head_dim
+// contiguous) and a filled argument block.
+int launch_attention(g950_module* m, AttnArgs& a, uint32_t dt, long long D, const View& q, const View& k,
+                     const View& v, const View& o, void* stream) {
+  if (a.Z == 0 || a.Hq == 0 || a.Sq == 0) return launch(m, "g950_attn_fwd_general", 0, 64, a, stream);
+  if (a.Sk == 0) return fail(G950_USAGE, "attention: no keys");
+  const long long Z = a.Z, H = a.Hq, S = a.Sq;
   // the MFMA kernel's running maximum assumes scale > 0 (scaling then commutes
   // with the maximum); other scales take the general kernel
   const bool mfma = is_float16ish(dt) && (D == 64 || D == 128) && a.scale_log2 > 0.0f &&
@@ -846,6 +987,72 @@ int op_attention(g950_module* m, const g950_view* views, uint32_t nviews, const 
   ga.dtype = (int)dt;
   const long long rows = Z * H * S;
   return launch(m, "g950_attn_fwd_general", (unsigned)((rows + 63) / 64), 64u, ga, stream);
+}
+
+// gqa_kernel (ops/suite/dev/gqa.py:20-59): non-causal GQA attention over
+// [Z, H_Q, N_CTX, HEAD_DIM] queries and [Z, H_KV, N_CTX, HEAD_DIM] keys and
+// values.  The kernel addresses batch z at z * H * stride_h (gqa.py:30-33),
+// so each view's batch stride must be its head count times its head stride;
+// query head h reads KV head h // GROUP.
+int op_gqa(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc, uint32_t nsc,
+           void* stream) {
+  if (nviews != 4 || nsc != 18)
+    return fail(G950_USAGE, "gqa: needs views (K, Out, Q, V) and 18 scalars (GROUP, HEAD_DIM, H_KV, H_Q, "
+                "N_CTX, scale, 12 strides)");
+  View k, o, q, v;
+  if (int rc = check_view(views, 0, "K", 4, k, false)) return rc;
+  if (int rc = check_view(views, 1, "Out", 4, o, true)) return rc;
+  if (int rc = check_view(views, 2, "Q", 4, q, false)) return rc;
+  if (int rc = check_view(views, 3, "V", 4, v, false)) return rc;
+  const uint32_t dt = q.v->dtype;
+  if (!is_float(dt) || k.v->dtype != dt || v.v->dtype != dt || o.v->dtype != dt)
+    return fail(G950_USAGE, "gqa: Q/K/V/Out must share one float dtype");
+  long long group, hd, hkv, hq, n;
+  double scale;
+  if (int rc = scalar_int(&sc[0], "GROUP", group)) return rc;
+  if (int rc = scalar_int(&sc[1], "HEAD_DIM", hd)) return rc;
+  if (int rc = scalar_int(&sc[2], "H_KV", hkv)) return rc;
+  if (int rc = scalar_int(&sc[3], "H_Q", hq)) return rc;
+  if (int rc = scalar_int(&sc[4], "N_CTX", n)) return rc;
+  if (int rc = scalar_float(&sc[5], "scale", scale)) return rc;
+  const long long Z = q.shape[0];
+  if (q.shape[1] != hq || o.shape[1] != hq || k.shape[1] != hkv || v.shape[1] != hkv)
+    return fail(G950_USAGE, "gqa: Q/Out need H_Q heads and K/V H_KV heads");
+  for (const View* w : {&k, &o, &q, &v})
+    if (w->shape[0] != Z || w->shape[2] != n || w->shape[3] != hd)
+      return fail(G950_USAGE, "gqa: view %s must be [Z, heads, N_CTX, HEAD_DIM]", w->name);
+  if (hq <= 0 || hkv <= 0 || group < 1 || (hq - 1) / group >= hkv)
+    return fail(G950_USAGE, "gqa: GROUP must map every query head to a KV head ((H_Q - 1) // GROUP < H_KV)");
+  if (hd > 1 && (q.stride[3] != 1 || k.stride[3] != 1 || v.stride[3] != 1 || o.stride[3] != 1))
+    return fail(G950_USAGE, "gqa: head_dim must be contiguous");
+  // stride scalars, sorted: k(h,k,n) o(h,m,n) q(h,k,m) v(h,k,n) -> view dims
+  const struct { const View* vw; const char* names[3]; int dims[3]; long long heads; } st[4] = {
+      {&k, {"stride_kh", "stride_kk", "stride_kn"}, {1, 3, 2}, hkv},
+      {&o, {"stride_oh", "stride_om", "stride_on"}, {1, 2, 3}, hq},
+      {&q, {"stride_qh", "stride_qk", "stride_qm"}, {1, 3, 2}, hq},
+      {&v, {"stride_vh", "stride_vk", "stride_vn"}, {1, 2, 3}, hkv},
+  };
+  uint32_t si = 6;
+  for (const auto& e : st) {
+    for (int j = 0; j < 3; ++j)
+      if (int rc = stride_agrees(sc, si++, e.names[j], *e.vw, e.dims[j])) return rc;
+    if (Z > 1 && e.vw->stride[0] != e.heads * e.vw->stride[1])
+      return fail(G950_USAGE, "gqa: view %s batch stride must be heads x head stride (the kernel's batch offset)",
+                  e.vw->name);
+  }
+  if (Z * hq > 0x7FFFFFF || n > 0x7FFFFFF) return fail(G950_USAGE, "gqa: extent too large");
+  AttnArgs a{};
+  a.q = q.v->data; a.k = k.v->data; a.v = v.v->data; a.o = o.v->data;
+  a.lse = nullptr;
+  a.q_sz = q.stride[0]; a.q_sh = q.stride[1]; a.q_ss = q.stride[2];
+  a.k_sz = k.stride[0]; a.k_sh = k.stride[1]; a.k_ss = k.stride[2];
+  a.v_sz = v.stride[0]; a.v_sh = v.stride[1]; a.v_ss = v.stride[2];
+  a.o_sz = o.stride[0]; a.o_sh = o.stride[1]; a.o_ss = o.stride[2];
+  a.Z = (int)Z; a.Hq = (int)hq; a.Hkv = (int)hkv; a.Sq = (int)n; a.Sk = (int)n;
+  a.scale_log2 = (float)(scale * 1.4426950408889634);
+  a.causal = 0;
+  a.group = (int)group;
+  return launch_attention(m, a, dt, hd, q, k, v, o, stream);
 }
 
 // ------------------------------------------------------ varlen attention
@@ -994,6 +1201,7 @@ int op_flash_varlen(g950_module* m, const g950_view* views, uint32_t nviews, con
   a.Z = (int)B; a.Hq = (int)H; a.Hkv = (int)HK; a.Sq = (int)SQ; a.Sk = (int)SK;
   a.scale_log2 = (float)scale_log2;
   a.causal = I("is_causal") ? 1 : 0;
+  a.group = (int)(H / HK);
   AttnVarArgs va{};
   va.a = a; va.v = vl; va.D = (int)D; va.dtype = (int)dt;
   if (B == 0 || SQ == 0) return launch(m, "g950_attn_varlen_general", 0, 64u, va, stream);
@@ -1091,6 +1299,9 @@ int dispatch(g950_module* m, uint32_t op, const g950_view* views, uint32_t nview
       case G950_OP_DEQUANTIZE: return op_dequantize(m, views, nviews, scalars, nscalars, stream);
       case G950_OP_FLASH_VARLEN: return op_flash_varlen(m, views, nviews, scalars, nscalars, stream);
       case G950_OP_DEQUANT_MATMUL: return op_dequant_matmul(m, views, nviews, scalars, nscalars, stream);
+      case G950_OP_SOFTMAX_INNER: return op_softmax_inner(m, views, nviews, scalars, nscalars, stream);
+      case G950_OP_LAYERNORM_ROW: return op_layernorm_row(m, views, nviews, scalars, nscalars, stream);
+      case G950_OP_GQA: return op_gqa(m, views, nviews, scalars, nscalars, stream);
       default: return fail(G950_USAGE, "g950_launch: unknown operator contract %u", op);
     }
   } catch (...) {

@@ -63,8 +63,10 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& 
 
 // Epilogue: lane holds C[m][n..n+3] for m = row r of each 32-row fragment,
 // n = 8q + 4g + {0..3} of each 32-column fragment; (wm0, wn0) is the first
-// output row / column of the wave's tile.
-template <int MODE, int FM, int FN>
+// output row / column of the wave's tile.  UMASK (int8 only): bit 0 A
+// unsigned, bit 1 B unsigned -- the accumulator of the offset operands gets
+// its exact correction (modulo 2^32, GemmArgs::rsum / csum).
+template <int MODE, int FM, int FN, int UMASK = 0>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&accf)[FM][FN],
                                               const i32x16 (&acci)[FM][FN], int wm0, int wn0,
                                               int r, int g) {
@@ -75,6 +77,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
     if (m >= p.M) continue;
     float rs = 1.0f;
     if constexpr (MODE == GEMM_I8) rs = p.sa ? p.sa[m] : 1.0f;
+    uint32_t rcorr = 0;
+    if constexpr (MODE == GEMM_I8 && (UMASK & 2)) rcorr = 128u * (uint32_t)p.rsum[m];
+    if constexpr (MODE == GEMM_I8 && UMASK == 3) rcorr -= 16384u * (uint32_t)p.K;
 #pragma unroll
     for (int ni = 0; ni < FN; ++ni) {
 #pragma unroll
@@ -84,7 +89,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
         if constexpr (MODE == GEMM_I8) {
           int iv[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) iv[e] = acci[mi][ni][q * 4 + e];
+          for (int e = 0; e < 4; ++e) {
+            uint32_t c = rcorr;
+            if constexpr (UMASK & 1) c += (n + e < p.N) ? 128u * (uint32_t)p.csum[n + e] : 0u;
+            iv[e] = (int)((uint32_t)acci[mi][ni][q * 4 + e] + c);
+          }
           if (p.acc_out) {
             int* dst = p.acc_out + (long long)m * p.acc_s0 + n;
             if (((p.acc_s0 & 3) == 0) && n + 3 < p.N) {
@@ -155,7 +164,10 @@ __device__ __forceinline__ void mfma_step(const u32x4& bfrag, const u32x4& afrag
 }
 
 // WM x WN waves; wave tile (BM/WM) x (BN/WN) = FM x FN fragments of 32x32.
-template <int MODE, int WM, int WN>
+// UMASK (int8): bit 0 A unsigned, bit 1 B unsigned.  An unsigned operand's
+// bytes are flipped (XOR 0x80: u - 128, a signed int8) as its fragments enter
+// the MFMA; the epilogue adds the exact correction.
+template <int MODE, int WM, int WN, int UMASK = 0>
 __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   constexpr int NW = WM * WN;
   constexpr int FM = BM / WM / 32;
@@ -238,6 +250,14 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
     }
   };
   auto mfmas = [&](int buf) {
+    if constexpr (UMASK & 1) {
+#pragma unroll
+      for (int mi = 0; mi < FM; ++mi) af[buf][mi] ^= 0x80808080u;
+    }
+    if constexpr (UMASK & 2) {
+#pragma unroll
+      for (int ni = 0; ni < FN; ++ni) bfr[buf][ni] ^= 0x80808080u;
+    }
 #pragma unroll
     for (int mi = 0; mi < FM; ++mi)
 #pragma unroll
@@ -295,7 +315,35 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  gemm_epilogue<MODE, FM, FN>(p, accf, acci, m0 + wm * (BM / WM), n0 + wn * (BN / WN), r, g);
+  gemm_epilogue<MODE, FM, FN, UMASK>(p, accf, acci, m0 + wm * (BM / WM), n0 + wn * (BN / WN), r, g);
+}
+
+// Row sums over k of int8 / uint8 operands (I8SumArgs), modulo 2^32: one wave
+// per row, 16-byte loads.  A byte's value is (byte ^ 0x80) - 128 when signed,
+// the byte itself when unsigned, so every row sums unsigned bytes of
+// byte ^ flip and subtracts 128 K for a signed row.
+__device__ __forceinline__ uint32_t byte_sum(uint32_t w) {
+  const uint32_t t = (w & 0x00FF00FFu) + ((w >> 8) & 0x00FF00FFu);
+  return (t & 0xFFFFu) + (t >> 16);
+}
+
+__device__ __forceinline__ void i8_sums_body(const I8SumArgs& p) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= (long long)p.a_rows + p.b_rows) return;
+  const bool is_a = row < p.a_rows;
+  const char* src = is_a ? (const char*)p.a + row * p.a_s0 : (const char*)p.b + (row - p.a_rows) * p.b_s0;
+  const bool sgn = is_a ? p.a_signed : p.b_signed;
+  const uint32_t flip = sgn ? 0x80808080u : 0u;
+  uint32_t s = 0;
+  const int full = p.K / 16;
+  for (int c = lane; c < full; c += 64) {
+    const u32x4 w = __builtin_nontemporal_load((const u32x4*)(src + (long long)c * 16));
+    s += byte_sum(w[0] ^ flip) + byte_sum(w[1] ^ flip) + byte_sum(w[2] ^ flip) + byte_sum(w[3] ^ flip);
+  }
+  for (int k = full * 16 + lane; k < p.K; k += 64) s += (uint32_t)(((const uint8_t*)src)[k] ^ (flip & 0xFFu));
+  s = __builtin_bit_cast(uint32_t, wave_reduce<OpSumU32>(__builtin_bit_cast(float, s)));
+  if (lane == 0) p.out[row] = (int)(s - (sgn ? 128u * (uint32_t)p.K : 0u));
 }
 
 // --------------------------------------------- fused weight dequantisation
@@ -668,12 +716,14 @@ __device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
       const int m = m0 + mm, k = k0 + kk;
       const bool inb = (m < p.M) && (k < p.K);
       const long long ia = (long long)m * p.a_s0 + (long long)k * p.a_s1;
-      if (INT8) Ai[kk][mm] = inb ? (int)((const int8_t*)p.a)[ia] : 0;
+      if (INT8) Ai[kk][mm] = !inb ? 0 : p.a_dtype == DT_UINT8 ? (int)((const uint8_t*)p.a)[ia]
+                                                             : (int)((const int8_t*)p.a)[ia];
       else As[kk][mm] = inb ? load_as_f32(p.a, ia, p.a_dtype) : 0.0f;
       const int n = n0 + mm;
       const bool inbb = (n < p.N) && (k < p.K);
       const long long ib = (long long)k * p.b_s0 + (long long)n * p.b_s1;
-      if (INT8) Bi[kk][mm] = inbb ? (int)((const int8_t*)p.b)[ib] : 0;
+      if (INT8) Bi[kk][mm] = !inbb ? 0 : p.b_dtype == DT_UINT8 ? (int)((const uint8_t*)p.b)[ib]
+                                                               : (int)((const int8_t*)p.b)[ib];
       else if (p.b_dtype == DT_INT8) Bs[kk][mm] = inbb ? (float)((const int8_t*)p.b)[ib] : 0.0f;
       else Bs[kk][mm] = inbb ? load_as_f32(p.b, ib, p.b_dtype) : 0.0f;
     }
@@ -684,7 +734,7 @@ __device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          if (INT8) acci[i][j] += Ai[kk][ty * 4 + i] * Bi[kk][tx * 4 + j];
+          if (INT8) acci[i][j] = (int)((uint32_t)acci[i][j] + (uint32_t)(Ai[kk][ty * 4 + i] * Bi[kk][tx * 4 + j]));
           else accf[i][j] = fmaf(As[kk][ty * 4 + i], Bs[kk][tx * 4 + j], accf[i][j]);
         }
     }
@@ -714,13 +764,21 @@ __device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
 
 }  // namespace g950
 
-#define G950_GEMM_MFMA(NAME, MODE, WM, WN)                                                   \
+#define G950_GEMM_MFMA(NAME, MODE, WM, WN, UMASK)                                            \
   extern "C" __global__ __launch_bounds__(WM * WN * 64) void NAME(const g950::GemmArgs p) {  \
-    g950::gemm_mfma_body<MODE, WM, WN>(p);                                                 \
+    g950::gemm_mfma_body<MODE, WM, WN, UMASK>(p);                                          \
   }
-G950_GEMM_MFMA(g950_gemm_bf16_256x256, g950::GEMM_BF16, 4, 2)
-G950_GEMM_MFMA(g950_gemm_f16_256x256, g950::GEMM_F16, 4, 2)
-G950_GEMM_MFMA(g950_gemm_i8_256x256, g950::GEMM_I8, 4, 2)
+G950_GEMM_MFMA(g950_gemm_bf16_256x256, g950::GEMM_BF16, 4, 2, 0)
+G950_GEMM_MFMA(g950_gemm_f16_256x256, g950::GEMM_F16, 4, 2, 0)
+G950_GEMM_MFMA(g950_gemm_i8_256x256, g950::GEMM_I8, 4, 2, 0)
+// int8 signedness variants of the reference family (a100c/plan/tiles.py:121-126):
+// uint8 A x int8 B, int8 A x uint8 B, uint8 x uint8
+G950_GEMM_MFMA(g950_gemm_u8s8_256x256, g950::GEMM_I8, 4, 2, 1)
+G950_GEMM_MFMA(g950_gemm_s8u8_256x256, g950::GEMM_I8, 4, 2, 2)
+G950_GEMM_MFMA(g950_gemm_u8u8_256x256, g950::GEMM_I8, 4, 2, 3)
+extern "C" __global__ __launch_bounds__(256) void g950_i8_sums(const g950::I8SumArgs p) {
+  g950::i8_sums_body(p);
+}
 extern "C" __global__ __launch_bounds__(256) void g950_gemm_w8a16_bf16_128x128(const g950::GemmArgs p) {
   g950::gemm_w8a16_body<false>(p);
 }

@@ -9,6 +9,11 @@
 //             inv = 1/sqrt(sum(x^2)/n + eps); r[row] = inv; Y = (x*inv)*w
 //   LayerNorm ops/suite/dev/fused_layernorm_triton.py:27-42: mean; centered
 //             variance; rstd = 1/sqrt(var+eps); Y = (x-mean)*rstd*w + b
+//   LayerNorm row form ops/suite/dev/layer_norm_forward_row.py:11-36:
+//             mean = sum(x)/n, rstd = 1/sqrt(sum(x^2)/n - mean^2 + eps)
+//             (one pass, both sums together); x_hat = (x-mean)*rstd rounded
+//             to X's dtype, then Y = x_hat*W + B in X's dtype (16-bit types
+//             round the product and the sum, as the reference's typed ops do)
 // All arithmetic is fp32; 16-bit inputs widen exactly and outputs round once.
 //
 // Two kernel shapes:
@@ -29,7 +34,11 @@
 
 namespace g950 {
 
-enum RowOp : int { ROW_SOFTMAX = 0, ROW_RMSNORM = 1, ROW_LAYERNORM = 2, ROW_LOGSUMEXP = 3 };
+enum RowOp : int { ROW_SOFTMAX = 0, ROW_RMSNORM = 1, ROW_LAYERNORM = 2, ROW_LOGSUMEXP = 3, ROW_LNROW = 4 };
+
+// ops with per-column weight (and bias) rows
+constexpr bool row_has_w(int op) { return op == ROW_RMSNORM || op == ROW_LAYERNORM || op == ROW_LNROW; }
+constexpr bool row_has_b(int op) { return op == ROW_LAYERNORM || op == ROW_LNROW; }
 
 
 
@@ -184,6 +193,22 @@ __device__ __forceinline__ float row_exp(float x) {
   else return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
+// v rounded to T's precision (the value a store of T would keep)
+template <typename T>
+__device__ __forceinline__ float round_to(float v) {
+  if constexpr (sizeof(T) == 4) return v;
+  else return Elem<T>::to_f32(Elem<T>::from_f32(v));
+}
+
+// layer_norm_forward_row's affine on one element: x_hat = (x - mean) * rstd
+// in X's dtype, then x_hat * w + b with the reference's typed rounding
+template <typename T>
+__device__ __forceinline__ float lnrow_affine(float x, float mean, float rstd, float w, float b) {
+  const float xh = round_to<T>((x - mean) * rstd);
+  if constexpr (sizeof(T) == 4) return fmaf(xh, w, b);
+  else return round_to<T>(xh * w) + b;
+}
+
 // logsumexp of one row from its NaN-ignoring max m, sum s = sum(exp(x - m))
 // and NaN flag (ops/suite/perf/logsumexp.py kernel: a row with any NaN gives
 // NaN; an infinite max is returned as is; else m + log(s)).
@@ -210,13 +235,13 @@ __device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
 
   // parameters stay packed in registers (16-bit types: half the VGPRs)
   R wr[ITEMS], br[ITEMS];
-  if constexpr (OP == ROW_RMSNORM || OP == ROW_LAYERNORM) {
+  if constexpr (row_has_w(OP)) {
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
       const int j = tid + i * BLOCK;
       if (j < nvec) {
         wr[i] = IO::load_cached(a.w, (long long)j * VEC);
-        if constexpr (OP == ROW_LAYERNORM) br[i] = IO::load_cached(a.b, (long long)j * VEC);
+        if constexpr (row_has_b(OP)) br[i] = IO::load_cached(a.b, (long long)j * VEC);
       }
     }
   }
@@ -241,13 +266,13 @@ __device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
         if (j < nvec) nxt[i] = IO::load(xrow, (long long)j * VEC);
       }
     }
-    if constexpr (OP == ROW_RMSNORM || OP == ROW_LAYERNORM) {
+    if constexpr (row_has_w(OP)) {
       // keep the decode of the packed parameters inside the loop: hoisting it
       // would hold them as fp32 for the whole kernel (twice the VGPRs)
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) {
         asm volatile("" : "+v"(wr[i]));
-        if constexpr (OP == ROW_LAYERNORM) asm volatile("" : "+v"(br[i]));
+        if constexpr (row_has_b(OP)) asm volatile("" : "+v"(br[i]));
       }
     }
     void* yrow = (char*)a.y + (long long)row * ystride;
@@ -330,6 +355,37 @@ __device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
           IO::unpack(wr[i], w);
 #pragma unroll
           for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] * inv) * w[e];
+          store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+        }
+      }
+    } else if constexpr (OP == ROW_LNROW) {
+      // both sums in one pass (the reference's E[x^2] - mean^2 form)
+      float s = 0.0f, q = 0.0f;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          s += v[i][e];
+          q = fmaf(v[i][e], v[i][e], q);
+        }
+      s = block_reduce<OpSum, BLOCK>(s, scratch);
+      q = block_reduce<OpSum, BLOCK>(q, scratch);
+      const float inv_n = 1.0f / (float)a.cols;
+      const float mean = s * inv_n;
+      const float rstd = 1.0f / sqrtf(q * inv_n - mean * mean + a.eps);
+      if (tid == 0) {
+        store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mean);
+        store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, rstd);
+      }
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        const int j = tid + i * BLOCK;
+        if (j < nvec) {
+          float o[VEC], w[VEC], bb[VEC];
+          IO::unpack(wr[i], w);
+          IO::unpack(br[i], bb);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[e] = lnrow_affine<T>(v[i][e], mean, rstd, w[e], bb[e]);
           store_vec<T, VEC>(yrow, (long long)j * VEC, o);
         }
       }
@@ -459,6 +515,17 @@ __device__ __forceinline__ void rs_part_body(const RowArgs& a) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) ss = fmaf(v[i][e], v[i][e], ss);
     p[0] = block_reduce<OpSum, RS_BLOCK>(ss, scratch);
+  } else if constexpr (OP == ROW_LNROW) {
+    float s = 0.0f, q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RS_ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        s += v[i][e];
+        q = fmaf(v[i][e], v[i][e], q);
+      }
+    p[0] = block_reduce<OpSum, RS_BLOCK>(s, scratch);
+    p[1] = block_reduce<OpSum, RS_BLOCK>(q, scratch);
   } else {
     const int first = split * (RS_BLOCK * RS_ITEMS * VEC);
     const float n = (float)min(RS_BLOCK * RS_ITEMS * VEC, a.cols - first);
@@ -514,6 +581,14 @@ __device__ __forceinline__ f32x4 rs_merge(const RowArgs& a, int row, float* scra
     float ss = 0.0f;
     for (int k = threadIdx.x; k < a.splits; k += RS_BLOCK) ss += part[k][0];
     r[0] = block_reduce<OpSum, RS_BLOCK>(ss, scratch);
+  } else if constexpr (OP == ROW_LNROW) {
+    float s = 0.0f, q = 0.0f;
+    for (int k = threadIdx.x; k < a.splits; k += RS_BLOCK) {
+      s += part[k][0];
+      q += part[k][1];
+    }
+    r[0] = block_reduce<OpSum, RS_BLOCK>(s, scratch);
+    r[1] = block_reduce<OpSum, RS_BLOCK>(q, scratch);
   } else {
     // Chan et al.: mean = sum(n_k mean_k) / n; M2 = sum(M2_k + n_k (mean_k - mean)^2)
     float s = 0.0f;
@@ -552,6 +627,14 @@ __device__ __forceinline__ void rs_final_body(const RowArgs& a) {
     } else if constexpr (OP == ROW_RMSNORM) {
       mul = 1.0f / sqrtf(r[0] / (float)a.cols + a.eps);
       if (split == 0 && threadIdx.x == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mul);
+    } else if constexpr (OP == ROW_LNROW) {
+      const float inv_n = 1.0f / (float)a.cols;
+      sub = r[0] * inv_n;
+      mul = 1.0f / sqrtf(r[1] * inv_n - sub * sub + a.eps);
+      if (split == 0 && threadIdx.x == 0) {
+        store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, sub);
+        store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, mul);
+      }
     } else {
       sub = r[0];
       mul = 1.0f / sqrtf(r[1] / (float)a.cols + a.eps);
@@ -573,6 +656,12 @@ __device__ __forceinline__ void rs_final_body(const RowArgs& a) {
         load_param<T, VEC>(a.w, (long long)j * VEC, w);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] * mul) * w[e];
+      } else if constexpr (OP == ROW_LNROW) {
+        float w[VEC], bb[VEC];
+        load_param<T, VEC>(a.w, (long long)j * VEC, w);
+        load_param<T, VEC>(a.b, (long long)j * VEC, bb);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = lnrow_affine<T>(v[i][e], sub, mul, w[e], bb[e]);
       } else {
         float w[VEC], bb[VEC];
         load_param<T, VEC>(a.w, (long long)j * VEC, w);
@@ -638,6 +727,7 @@ G950_RR_ALL(softmax, g950::ROW_SOFTMAX)
 G950_RR_ALL(rmsnorm, g950::ROW_RMSNORM)
 G950_RR_ALL(layernorm, g950::ROW_LAYERNORM)
 G950_RR_ALL(logsumexp, g950::ROW_LOGSUMEXP)
+G950_RR_ALL(lnrow, g950::ROW_LNROW)
 
 // ------------------------------------------------------------- stream copy
 // y = x for n 16-byte vectors, grid-stride, nontemporal loads and stores --

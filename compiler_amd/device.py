@@ -71,6 +71,25 @@ def _softmax(a):
     ops.softmax_kernel(a["x_ptr"], a["y_ptr"], a["n_cols"], sync=True)
 
 
+def _softmax_inner(a):
+    ops.softmax_kernel_inner(a["output_ptr"], a["input_ptr"], a["M"], a["N"], a.get("TILE_N"),
+                             a.get("ONE_TILE_PER_CTA"), sync=True)
+
+
+def _layer_norm_row(a):
+    ops.layer_norm_forward_row(a["Y_ptr"], a["Y_row_stride"], a["X_ptr"], a["X_row_stride"], a["W_ptr"],
+                               a["B_ptr"], a["Mean_ptr"], a["Mean_row_stride"], a["RSTD_ptr"],
+                               a["RSTD_row_stride"], a["n_rows"], a["n_cols"], a["eps"], a.get("BLOCK_SIZE"),
+                               sync=True)
+
+
+def _gqa(a):
+    names = ["stride_qh", "stride_qm", "stride_qk", "stride_kh", "stride_kn", "stride_kk", "stride_vh",
+             "stride_vk", "stride_vn", "stride_oh", "stride_om", "stride_on"]
+    ops.gqa_kernel(a["Q"], a["K"], a["V"], a["Out"], *[a[n] for n in names], a["H_Q"], a["H_KV"], a["N_CTX"],
+                   a["scale"], a["GROUP"], a.get("HEAD_DIM"), sync=True)
+
+
 def _logsumexp(a):
     ops.logsumexp_kernel(a["x_ptr"], a["y_ptr"], a["n_cols"], sync=True)
 
@@ -112,6 +131,9 @@ def _attention(a, causal_default):
 # reference kernel name -> operator (hot path only)
 KERNELS = {
     "softmax_kernel": _softmax,
+    "softmax_kernel_inner": _softmax_inner,
+    "_layer_norm_forward_row": _layer_norm_row,
+    "gqa_kernel": _gqa,
     "logsumexp_kernel": _logsumexp,
     "dequantize_kernel": _dequantize,
     "flash_varlen_fwd_kernel": _flash_varlen,

@@ -38,6 +38,60 @@ def softmax_kernel(x_ptr, y_ptr, n_cols, *, stream=None, sync=False, prepare=Fal
                    {"n_cols": n_cols}, stream, sync, prepare)
 
 
+def softmax_kernel_inner(output_ptr, input_ptr, M, N, TILE_N=None, ONE_TILE_PER_CTA=None, *, stream=None,
+                         sync=False, prepare=False):
+    """Row softmax over flat buffers (ops/suite/dev/softmax_kernel_inner.py:12-72):
+    row m is the N contiguous elements at input_ptr + m*N, written to
+    output_ptr + m*N.  TILE_N / ONE_TILE_PER_CTA only shaped the reference's
+    tiles; the one-tile form covers a whole row only when TILE_N >= N, so a
+    call that asks for one tile narrower than the row is refused."""
+    if ONE_TILE_PER_CTA and TILE_N is not None and int(TILE_N) < int(N):
+        raise rt.G950Error(rt.USAGE, "softmax_kernel_inner: ONE_TILE_PER_CTA with TILE_N < N normalises only "
+                                     "the first TILE_N columns; not supported")
+    return _launch(rt.OP_SOFTMAX_INNER, {"input_ptr": input_ptr, "output_ptr": output_ptr}, {"output_ptr"},
+                   {"M": M, "N": N}, stream, sync, prepare)
+
+
+def layer_norm_forward_row(Y_ptr, Y_row_stride, X_ptr, X_row_stride, W_ptr, B_ptr, Mean_ptr, Mean_row_stride,
+                           RSTD_ptr, RSTD_row_stride, n_rows, n_cols, eps, BLOCK_SIZE=None, *, stream=None,
+                           sync=False, prepare=False):
+    """Row LayerNorm forward (ops/suite/dev/layer_norm_forward_row.py:11-36):
+    mean and rstd from sum(x) and sum(x^2) (E[x^2] - mean^2), x_hat rounded to
+    X's dtype, Y = x_hat*W + B.  Buffers are flat, addressed by the row-stride
+    scalars.  The reference loads BLOCK_SIZE columns unmasked, so BLOCK_SIZE
+    must equal n_cols (a wider block would read the next row)."""
+    if BLOCK_SIZE is not None and int(BLOCK_SIZE) != int(n_cols):
+        raise rt.G950Error(rt.USAGE, "_layer_norm_forward_row: BLOCK_SIZE must equal n_cols (the reference "
+                                     "loads BLOCK_SIZE columns without a mask)")
+    return _launch(rt.OP_LAYERNORM_ROW, {"B_ptr": B_ptr, "Mean_ptr": Mean_ptr, "RSTD_ptr": RSTD_ptr, "W_ptr": W_ptr,
+                                         "X_ptr": X_ptr, "Y_ptr": Y_ptr}, {"Y_ptr", "Mean_ptr", "RSTD_ptr"},
+                   {"Mean_row_stride": Mean_row_stride, "RSTD_row_stride": RSTD_row_stride,
+                    "X_row_stride": X_row_stride, "Y_row_stride": Y_row_stride,
+                    "eps": np.float32(eps) if not isinstance(eps, np.generic) else eps,
+                    "n_cols": n_cols, "n_rows": n_rows}, stream, sync, prepare)
+
+
+# the reference's kernel name (a leading underscore in ops/suite/dev/layer_norm_forward_row.py:11)
+_layer_norm_forward_row = layer_norm_forward_row
+
+
+def gqa_kernel(Q, K, V, Out, stride_qh, stride_qm, stride_qk, stride_kh, stride_kn, stride_kk,
+               stride_vh, stride_vk, stride_vn, stride_oh, stride_om, stride_on, H_Q, H_KV, N_CTX, scale,
+               GROUP, HEAD_DIM=None, BLOCK_N=None, *, stream=None, sync=False, prepare=False):
+    """Non-causal GQA attention forward (ops/suite/dev/gqa.py:20-59): Q/Out
+    [Z, H_Q, N_CTX, HEAD_DIM], K/V [Z, H_KV, N_CTX, HEAD_DIM]; query head h
+    reads KV head h // GROUP.  BLOCK_N only shaped the reference's tile."""
+    head_dim = Q.shape[-1] if HEAD_DIM is None else HEAD_DIM
+    return _launch(rt.OP_GQA, {"K": K, "Out": Out, "Q": Q, "V": V}, {"Out"},
+                   {"GROUP": GROUP, "HEAD_DIM": head_dim, "H_KV": H_KV, "H_Q": H_Q, "N_CTX": N_CTX,
+                    "scale": np.float32(scale) if not isinstance(scale, np.generic) else scale,
+                    "stride_kh": stride_kh, "stride_kk": stride_kk, "stride_kn": stride_kn,
+                    "stride_oh": stride_oh, "stride_om": stride_om, "stride_on": stride_on,
+                    "stride_qh": stride_qh, "stride_qk": stride_qk, "stride_qm": stride_qm,
+                    "stride_vh": stride_vh, "stride_vk": stride_vk, "stride_vn": stride_vn},
+                   stream, sync, prepare)
+
+
 def logsumexp_kernel(x_ptr, y_ptr, n_cols, *, stream=None, sync=False, prepare=False):
     """Row logsumexp (ops/suite/perf/logsumexp.py:16-38).  x: [rows, n_cols],
     y: [rows] (float32 in the reference): max over non-NaN entries plus
@@ -127,8 +181,9 @@ def matmul_kernel(a_ptr, b_ptr, y_ptr, M, N, K, *, stream=None, sync=False, prep
 
 
 def matmul_i8_kernel(a_ptr, b_ptr, c_ptr, M, N, K, *, stream=None, sync=False, prepare=False):
-    """int8 x int8 -> int32, bit-exact modular accumulation
-    (i8 dot family, a100c/plan/tiles.py:118-131)."""
+    """8-bit integer dot -> int32, bit-exact modular accumulation, for the
+    four signedness pairs of the i8 family (a100c/plan/tiles.py:118-131:
+    int8/uint8 a_ptr and b_ptr in any combination)."""
     return _launch(rt.OP_MATMUL_I8, {"a_ptr": a_ptr, "b_ptr": b_ptr, "c_ptr": c_ptr}, {"c_ptr"},
                    {"M": M, "N": N, "K": K}, stream, sync, prepare)
 

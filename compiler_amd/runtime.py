@@ -33,6 +33,9 @@ OP_LOGSUMEXP = 10
 OP_DEQUANTIZE = 11
 OP_FLASH_VARLEN = 12
 OP_DEQUANT_MATMUL = 13
+OP_SOFTMAX_INNER = 14
+OP_LAYERNORM_ROW = 15
+OP_GQA = 16
 
 # dtype codes (a100c/runtime/a100rt.h:58-72)
 DT_BOOL, DT_INT8, DT_UINT8, DT_INT16, DT_UINT16, DT_INT32 = 1, 2, 3, 4, 5, 6

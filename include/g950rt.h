@@ -91,13 +91,15 @@ typedef struct g950_scalar {
  *   views   a_ptr[M,K], b_ptr[K,N] (any strides; K-contiguous b = column-major
  *           takes the MFMA path), y_ptr[M,N]
  *   scalars K, M, N
- * G950_OP_MATMUL_I8    int8 tl.dot, int32 accumulate (a100c/plan/tiles.py:118-131)
- *   views   a_ptr i8[M,K], b_ptr i8[K,N], c_ptr i32[M,N]
+ * G950_OP_MATMUL_I8    8-bit integer tl.dot, int32 accumulate modulo 2^32, in the
+ *                      four signedness pairs of the reference's i8 family
+ *                      (a100c/plan/tiles.py:118-131: s x s, u x u, u x s, s x u)
+ *   views   a_ptr i8|u8[M,K], b_ptr i8|u8[K,N], c_ptr i32[M,N]
  *   scalars K, M, N
- * G950_OP_MATMUL_I8_DEQUANT  int8 GEMM + dequant epilogue
+ * G950_OP_MATMUL_I8_DEQUANT  8-bit integer GEMM + dequant epilogue
  *                      (per-column rule of ops/suite/perf/dequantize_matmul.py:29-38
  *                      plus a per-row A scale): y = bf16(acc * sa[m] * sb[n])
- *   views   a_ptr i8[M,K], b_ptr i8[K,N], sa_ptr f32[M], sb_ptr f32[N], y_ptr[M,N]
+ *   views   a_ptr i8|u8[M,K], b_ptr i8|u8[K,N], sa_ptr f32[M], sb_ptr f32[N], y_ptr[M,N]
  *   scalars K, M, N
  * G950_OP_ATTENTION    attn_fwd_causal_kernel (ops/suite/perf/attn_fwd_causal.py:20-55)
  *                      with GQA (K/V may have fewer heads, ops/suite/dev/gqa.py:29)
@@ -146,6 +148,29 @@ typedef struct g950_scalar {
  *   views   a_ptr[M,K] f32 | bf16 | f16, b_ptr i8[K,N] (K-contiguous for the MFMA
  *           path), b_scale_ptr[N] (a's dtype), y_ptr[M,N] float
  *   scalars K, M, N
+ * G950_OP_SOFTMAX_INNER  softmax_kernel_inner (ops/suite/dev/softmax_kernel_inner.py:12-72):
+ *                      row softmax of M rows of N contiguous elements at
+ *                      input_ptr + m*N, written to output_ptr + m*N
+ *   views   input_ptr, output_ptr: flat (any rank, C-contiguous, >= M*N
+ *           elements), one float dtype
+ *   scalars M, N (TILE_N and ONE_TILE_PER_CTA only shape the reference's tiles)
+ * G950_OP_LAYERNORM_ROW  _layer_norm_forward_row (ops/suite/dev/layer_norm_forward_row.py:11-36):
+ *                      mean = sum(x)/n, rstd = 1/sqrt(sum(x^2)/n - mean^2 + eps),
+ *                      x_hat = (x - mean)*rstd rounded to X's dtype, Y = x_hat*W + B
+ *   views   B_ptr, Mean_ptr, RSTD_ptr, W_ptr, X_ptr, Y_ptr: flat (any rank,
+ *           C-contiguous), addressed through the row strides; X/Y/W/B one float
+ *           dtype, Mean/RSTD one float dtype
+ *   scalars Mean_row_stride, RSTD_row_stride, X_row_stride, Y_row_stride, eps,
+ *           n_cols, n_rows (eps, n_cols, n_rows are the kernel's constexprs;
+ *           BLOCK_SIZE only shapes its tile)
+ * G950_OP_GQA          gqa_kernel (ops/suite/dev/gqa.py:20-59): non-causal GQA
+ *                      attention, query head h reads KV head h // GROUP
+ *   views   K[Z,H_KV,N_CTX,D], Out[Z,H_Q,N_CTX,D], Q[Z,H_Q,N_CTX,D],
+ *           V[Z,H_KV,N_CTX,D]; one float dtype; batch stride = heads x head
+ *           stride (the kernel's batch offset, gqa.py:30-33)
+ *   scalars GROUP, HEAD_DIM, H_KV, H_Q, N_CTX, scale, stride_kh, stride_kk,
+ *           stride_kn, stride_oh, stride_om, stride_on, stride_qh, stride_qk,
+ *           stride_qm, stride_vh, stride_vk, stride_vn (BLOCK_N only shapes the tile)
  */
 enum g950_op {
   G950_OP_SOFTMAX = 1,
@@ -160,7 +185,10 @@ enum g950_op {
   G950_OP_LOGSUMEXP = 10,
   G950_OP_DEQUANTIZE = 11,
   G950_OP_FLASH_VARLEN = 12,
-  G950_OP_DEQUANT_MATMUL = 13
+  G950_OP_DEQUANT_MATMUL = 13,
+  G950_OP_SOFTMAX_INNER = 14,
+  G950_OP_LAYERNORM_ROW = 15,
+  G950_OP_GQA = 16
 };
 
 typedef struct g950_module g950_module;

@@ -16,6 +16,13 @@ How each function is pinned (besides restating the formula):
                                 scale invariance; brute-force loop on tiny rows.
   * ``layernorm``            -- per-row output mean == beta, std == gamma when
                                 gamma/beta are constant; brute-force loop.
+  * ``layernorm_row``        -- constant row c -> mean c, rstd 1/sqrt(eps), Y = B;
+                                equals ``layernorm`` on well-conditioned rows
+                                (E[x^2] - mean^2 == var); brute-force loop;
+                                a dropped mean^2 term fails.
+  * ``gqa``                  -- ``attention`` (non-causal) when GROUP = Hq/Hkv;
+                                GROUP > Hq/Hkv maps several groups onto the
+                                first KV heads (brute force); uniform V -> V.
   * ``matmul``               -- reference-held matmul16/128/tail fixtures in 3
                                 dtypes + matmul256 fp16; brute-force triple loop.
   * ``matmul_i8``            -- exact integer brute force on tiny shapes; int32
@@ -45,6 +52,10 @@ __all__ = [
     "logsumexp",
     "dequantize",
     "flash_varlen",
+    "layernorm_row",
+    "gqa",
+    "softmax_inner",
+    "wrap_i32",
 ]
 
 # Shared value tolerances per dtype (ops/harness/opslib/case.py:153-157) and the
@@ -155,6 +166,31 @@ def layernorm(x, w, b, eps):
     return y, mean, rstd
 
 
+def layernorm_row(x, w, b, eps):
+    """Row LayerNorm forward of ``_layer_norm_forward_row``: returns (Y, Mean,
+    Rstd) in float64.
+
+    ops/suite/dev/layer_norm_forward_row.py:65-67: ``mean = x.mean(1)``,
+    ``rstd = 1/sqrt((x*x).mean(1) - mean*mean + eps)`` (the E[x^2] - mean^2
+    form, not the centered variance), ``Y = (x - mean)*rstd*W + B``.
+    """
+    x64 = np.asarray(x, dtype=np.float64)
+    w64 = np.asarray(w, dtype=np.float64)
+    b64 = np.asarray(b, dtype=np.float64)
+    mean = x64.mean(axis=-1)
+    rstd = 1.0 / np.sqrt((x64 * x64).mean(axis=-1) - mean * mean + float(eps))
+    y = (x64 - mean[:, None]) * rstd[:, None] * w64[None, :] + b64[None, :]
+    return y, mean, rstd
+
+
+def softmax_inner(flat, m, n) -> np.ndarray:
+    """``softmax_kernel_inner`` (ops/suite/dev/softmax_kernel_inner.py, ref):
+    the flat buffer's first m*n elements as m rows of n, row softmax in
+    float64, returned flat."""
+    x = np.asarray(flat).reshape(-1)[: m * n].reshape(m, n)
+    return softmax(x).reshape(-1)
+
+
 # -------------------------------------------------------------------- GEMM
 def matmul(a, b) -> np.ndarray:
     """``Y = A @ B`` in float64 (ops/suite/perf/matmul.py:46-50).
@@ -165,18 +201,25 @@ def matmul(a, b) -> np.ndarray:
 
 
 def matmul_i8(a, b) -> np.ndarray:
-    """Exact integer ``C = A @ B`` for int8 operands, returned as int64.
+    """Exact integer ``C = A @ B`` for int8 / uint8 operands, returned as int64.
 
-    Semantics of the i8 dot family: signed operands, 32-bit accumulator
-    (a100c/plan/tiles.py:118-131; a100c/tests/test_matrix_breadth.py:365-452
-    accumulates in int64 and narrows to int32).  float64 BLAS is exact here:
-    every partial sum is an integer below 2**53 (|a*b| <= 127*128, K <= 2**20).
+    Semantics of the i8 dot family: signed or unsigned operands in the four
+    pairs s x s, u x u, u x s, s x u, 32-bit accumulator (a100c/plan/tiles.py:
+    118-131; a100c/tests/test_matrix_breadth.py:365-452 accumulates in int64
+    and narrows to int32, see ``wrap_i32``).  float64 BLAS is exact here:
+    every partial sum is an integer below 2**53 (|a*b| <= 255*255, K <= 2**20).
     """
     a = np.asarray(a)
     b = np.asarray(b)
     if a.shape[1] > (1 << 20):
         raise ValueError("K too large for the exact float64 path")
     return np.rint(a.astype(np.float64) @ b.astype(np.float64)).astype(np.int64)
+
+
+def wrap_i32(acc) -> np.ndarray:
+    """The int64 accumulator narrowed to int32 modulo 2**32, as the reference
+    test narrows it (a100c/tests/test_matrix_breadth.py:389-390)."""
+    return np.asarray(acc, dtype=np.int64).astype(np.int32)
 
 
 def dequant(acc, sa, sb) -> np.ndarray:
@@ -191,14 +234,15 @@ def dequant(acc, sa, sb) -> np.ndarray:
 
 
 # --------------------------------------------------------------- attention
-def attention(q, k, v, scale, causal=True, block_rows=512):
+def attention(q, k, v, scale, causal=True, block_rows=512, group=None):
     """Flash-style attention forward in float64: returns (O, LSE).
 
     Scores and softmax follow ops/suite/perf/attn_fwd_causal.py:63-76 (causal
-    mask ``j <= i``); the GQA head map ``h_kv = h // (Hq // Hkv)`` follows
-    ops/suite/dev/gqa.py:29 and the LSE rule ``rowmax + log(rowsum)`` on scaled
-    scores (natural log, ``+inf`` for an empty or NaN row) follows
-    ops/suite/dev/flash_varlen_fwd_kernel.py:309 and :411-418.
+    mask ``j <= i``); the GQA head map ``h_kv = h // group`` (``group`` =
+    Hq // Hkv unless given) follows ops/suite/dev/gqa.py:29 and the LSE rule
+    ``rowmax + log(rowsum)`` on scaled scores (natural log, ``+inf`` for an
+    empty or NaN row) follows ops/suite/dev/flash_varlen_fwd_kernel.py:309 and
+    :411-418.
 
     q: [Z, Hq, S, D]; k, v: [Z, Hkv, S, D].  Computed per (z, h) in row blocks
     so that the score tensor never exceeds ``block_rows * S`` doubles.
@@ -208,9 +252,12 @@ def attention(q, k, v, scale, causal=True, block_rows=512):
     v = np.asarray(v)
     z_count, hq, s_q, d = q.shape
     hkv = k.shape[1]
-    if hq % hkv:
-        raise ValueError("Hq must be a multiple of Hkv")
-    group = hq // hkv
+    if group is None:
+        if hq % hkv:
+            raise ValueError("Hq must be a multiple of Hkv")
+        group = hq // hkv
+    if (hq - 1) // group >= hkv:
+        raise ValueError("group maps a query head past the KV heads")
     s_k = k.shape[2]
     out = np.empty((z_count, hq, s_q, d), dtype=np.float64)
     lse = np.empty((z_count, hq, s_q), dtype=np.float64)
@@ -237,6 +284,12 @@ def attention(q, k, v, scale, causal=True, block_rows=512):
                     row_lse = (m_safe + np.log(l))[:, 0]
                 lse[z, h, r0:r1] = np.where(empty[:, 0], np.inf, row_lse)
     return out, lse
+
+
+def gqa(q, k, v, scale, group):
+    """``gqa_kernel``'s output in float64 (ops/suite/dev/gqa.py:69-85):
+    non-causal softmax(q k^T * scale) v per (z, h) with KV head h // group."""
+    return attention(q, k, v, scale, causal=False, group=group)[0]
 
 
 # ------------------------------------------------------------- comparison

@@ -397,3 +397,150 @@ def test_attention_selection_and_refusals():
 def test_unknown_operator_refused():
     rc, _, err = validate(99, softmax_args(4, 16, rt.DT_F32), [16])
     assert rc == rt.USAGE and "unknown" in err
+
+
+# ------------------------------------------------------- dev-suite contracts
+def test_softmax_inner_contract():
+    # the reference case (97,): M = 3 rows of C = 32 in a flat buffer
+    a = Args().view([96], rt.DT_F32).view([96], rt.DT_F32, output=True)
+    rc, name, err = validate(rt.OP_SOFTMAX_INNER, a, [3, 32])
+    assert rc == 0 and name == "g950_rr_softmax_f32_v4_i1_b64", err
+    # (17,): M = 3, C = 5 -- not a whole 16-byte vector per row
+    a = Args().view([15], rt.DT_BF16).view([15], rt.DT_BF16, output=True)
+    rc, name, err = validate(rt.OP_SOFTMAX_INNER, a, [3, 5])
+    assert rc == 0 and name == "g950_rr_softmax_bf16_v1_i1_b64", err
+    # C2 scale through the flat contract
+    a = Args().view([8191 * 3000], rt.DT_BF16).view([8191 * 3000], rt.DT_BF16, output=True)
+    rc, name, err = validate(rt.OP_SOFTMAX_INNER, a, [8191, 3000])
+    assert rc == 0 and name == "g950_rr_softmax_bf16_v8_i6_b64", err
+    # a 2-D contiguous view is a flat buffer too
+    a = Args().view([3, 32], rt.DT_F32).view([96], rt.DT_F32, output=True)
+    assert validate(rt.OP_SOFTMAX_INNER, a, [3, 32])[0] == 0
+    # refusals: M x N past the buffer, mixed dtypes, a non-contiguous view, arity
+    a = Args().view([96], rt.DT_F32).view([95], rt.DT_F32, output=True)
+    rc, _, err = validate(rt.OP_SOFTMAX_INNER, a, [3, 32])
+    assert rc == rt.USAGE and "exceed" in err
+    a = Args().view([96], rt.DT_F32).view([96], rt.DT_F16, output=True)
+    assert validate(rt.OP_SOFTMAX_INNER, a, [3, 32])[0] == rt.USAGE
+    a = Args().view([3, 32], rt.DT_F32, strides=[64, 1]).view([96], rt.DT_F32, output=True)
+    rc, _, err = validate(rt.OP_SOFTMAX_INNER, a, [3, 32])
+    assert rc == rt.USAGE and "contiguous" in err
+    a = Args().view([96], rt.DT_F32).view([96], rt.DT_F32, output=True)
+    assert validate(rt.OP_SOFTMAX_INNER, a, [3])[0] == rt.USAGE
+    # nothing to do
+    assert validate(rt.OP_SOFTMAX_INNER, a, [0, 32])[0] == 0
+
+
+def lnrow_args(rows, cols, dt, sdt=None, x2d=True):
+    sdt = sdt or dt
+    a = Args().view([cols], dt).view([rows], sdt, output=True).view([rows], sdt, output=True).view([cols], dt)
+    a.view([rows, cols] if x2d else [rows * cols], dt)
+    return a.view([rows * cols], dt, output=True)
+
+
+def lnrow_scalars(rows, cols, xs=None, ys=None, ms=1, rs=1, eps=1e-5):
+    # sorted: Mean_row_stride RSTD_row_stride X_row_stride Y_row_stride eps n_cols n_rows
+    return [ms, rs, cols if xs is None else xs, cols if ys is None else ys, np.float32(eps), cols, rows]
+
+
+def test_layernorm_row_contract():
+    for rows, cols, dt, kernel in ((3, 16, rt.DT_F32, "g950_rr_lnrow_f32_v4_i1_b64"),
+                                   (5, 128, rt.DT_BF16, "g950_rr_lnrow_bf16_v8_i1_b64"),
+                                   (8191, 3000, rt.DT_BF16, "g950_rr_lnrow_bf16_v8_i6_b64"),
+                                   (7, 67, rt.DT_F16, "g950_rr_lnrow_f16_v1_i2_b64")):
+        rc, name, err = validate(rt.OP_LAYERNORM_ROW, lnrow_args(rows, cols, dt), lnrow_scalars(rows, cols))
+        assert rc == 0 and name == kernel, err
+    # statistics in another float dtype than X (each pair must agree)
+    rc, _, err = validate(rt.OP_LAYERNORM_ROW, lnrow_args(3, 16, rt.DT_BF16, rt.DT_F32), lnrow_scalars(3, 16))
+    assert rc == 0, err
+    # refusals
+    rc, _, err = validate(rt.OP_LAYERNORM_ROW, lnrow_args(3, 16, rt.DT_F32), lnrow_scalars(3, 16, xs=17))
+    assert rc == rt.USAGE and "exceed" in err
+    rc, _, err = validate(rt.OP_LAYERNORM_ROW, lnrow_args(3, 16, rt.DT_F32), lnrow_scalars(3, 16, ys=8))
+    assert rc == rt.USAGE and "overlap" in err
+    rc, _, err = validate(rt.OP_LAYERNORM_ROW, lnrow_args(3, 16, rt.DT_F32), lnrow_scalars(3, 16, ms=2))
+    assert rc == rt.USAGE
+    mixed = (Args().view([16], rt.DT_F32).view([3], rt.DT_F32, output=True).view([3], rt.DT_F32, output=True)
+             .view([16], rt.DT_BF16).view([3, 16], rt.DT_F32).view([48], rt.DT_F32, output=True))
+    assert validate(rt.OP_LAYERNORM_ROW, mixed, lnrow_scalars(3, 16))[0] == rt.USAGE
+    bad = lnrow_scalars(3, 16)
+    bad[5] = 0
+    assert validate(rt.OP_LAYERNORM_ROW, lnrow_args(3, 16, rt.DT_F32), bad)[0] == rt.USAGE
+
+
+def gqa_args(z, hq, hkv, n, d, dt):
+    # sorted views: K, Out, Q, V
+    return (Args().view([z, hkv, n, d], dt).view([z, hq, n, d], dt, output=True).view([z, hq, n, d], dt)
+            .view([z, hkv, n, d], dt))
+
+
+def gqa_scalars(hq, hkv, n, d, group=None):
+    group = hq // hkv if group is None else group
+    # sorted: GROUP HEAD_DIM H_KV H_Q N_CTX scale stride_k(h,k,n) stride_o(h,m,n) stride_q(h,k,m) stride_v(h,k,n)
+    return [group, d, hkv, hq, n, np.float32(d ** -0.5), n * d, 1, d, n * d, d, 1, n * d, 1, d, n * d, d, 1]
+
+
+def test_gqa_contract():
+    for shape, dt, kernel in (((2, 4, 2, 32, 32), rt.DT_F32, "g950_attn_fwd_general"),
+                              ((1, 4, 2, 64, 32), rt.DT_BF16, "g950_attn_fwd_general"),
+                              ((4, 32, 8, 4096, 128), rt.DT_BF16, "g950_attn_fwd_bf16_d128"),
+                              ((2, 8, 2, 500, 64), rt.DT_F16, "g950_attn_fwd_f16_d64")):
+        z, hq, hkv, n, d = shape
+        rc, name, err = validate(rt.OP_GQA, gqa_args(*shape, dt), gqa_scalars(hq, hkv, n, d))
+        assert rc == 0 and name == kernel, err
+    # GROUP larger than Hq/Hkv: all heads on the first KV heads (valid)
+    assert validate(rt.OP_GQA, gqa_args(2, 4, 2, 32, 32, rt.DT_F32), gqa_scalars(4, 2, 32, 32, group=4))[0] == 0
+    # GROUP that sends a head past the KV heads
+    rc, _, err = validate(rt.OP_GQA, gqa_args(2, 4, 2, 32, 32, rt.DT_F32), gqa_scalars(4, 2, 32, 32, group=1))
+    assert rc == rt.USAGE and "GROUP" in err
+    # a stride scalar that disagrees with its view
+    bad = gqa_scalars(4, 2, 32, 32)
+    bad[6] += 1
+    rc, _, err = validate(rt.OP_GQA, gqa_args(2, 4, 2, 32, 32, rt.DT_F32), bad)
+    assert rc == rt.USAGE and "stride_kh" in err
+    # a batch stride other than heads x head stride (the kernel's batch offset)
+    a = (Args().view([2, 2, 32, 32], rt.DT_F32, strides=[4096, 1024, 32, 1])
+         .view([2, 4, 32, 32], rt.DT_F32, output=True).view([2, 4, 32, 32], rt.DT_F32)
+         .view([2, 2, 32, 32], rt.DT_F32))
+    rc, _, err = validate(rt.OP_GQA, a, gqa_scalars(4, 2, 32, 32))
+    assert rc == rt.USAGE and "batch stride" in err
+    # N_CTX disagreeing with the views, and arity
+    bad = gqa_scalars(4, 2, 32, 32)
+    bad[4] = 31
+    assert validate(rt.OP_GQA, gqa_args(2, 4, 2, 32, 32, rt.DT_F32), bad)[0] == rt.USAGE
+    assert validate(rt.OP_GQA, gqa_args(2, 4, 2, 32, 32, rt.DT_F32), gqa_scalars(4, 2, 32, 32)[:17])[0] == rt.USAGE
+
+
+@pytest.mark.parametrize("adt,bdt,kernel", [
+    (rt.DT_INT8, rt.DT_INT8, "g950_gemm_i8_256x256"),
+    (rt.DT_UINT8, rt.DT_INT8, "g950_gemm_u8s8_256x256"),
+    (rt.DT_INT8, rt.DT_UINT8, "g950_gemm_s8u8_256x256"),
+    (rt.DT_UINT8, rt.DT_UINT8, "g950_gemm_u8u8_256x256"),
+])
+def test_int8_signedness_selection(adt, bdt, kernel):
+    a = (Args().view([4096, 8192], adt).view([8192, 8192], bdt, strides=[1, 8192])
+         .view([4096, 8192], rt.DT_INT32, output=True))
+    rc, name, err = validate(rt.OP_MATMUL_I8, a, [8192, 4096, 8192])
+    assert rc == 0 and name == kernel, err
+    # row-major B: the general kernel handles every pair
+    c = Args().view([64, 100], adt).view([100, 64], bdt).view([64, 64], rt.DT_INT32, output=True)
+    rc, name, err = validate(rt.OP_MATMUL_I8, c, [100, 64, 64])
+    assert rc == 0 and name == "g950_gemm_general_i8", err
+
+
+def test_int8_refuses_other_integer_types():
+    a = Args().view([64, 128], rt.DT_INT32).view([128, 64], rt.DT_INT8, strides=[1, 128]) \
+        .view([64, 64], rt.DT_INT32, output=True)
+    rc, _, err = validate(rt.OP_MATMUL_I8, a, [128, 64, 64])
+    assert rc == rt.USAGE and "uint8" in err
+
+
+def test_dequant_matmul_k0_never_takes_the_widened_route():
+    # K = 0 with many output tiles: the 256x256 GEMM would DMA slab 0 of an empty
+    # operand; the fused kernel (no K loop) writes the zero product instead
+    a = (Args().view([4096, 0], rt.DT_BF16).view([0, 4096], rt.DT_INT8, strides=[1, 0])
+         .view([4096], rt.DT_BF16).view([4096, 4096], rt.DT_BF16, output=True))
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, a, [0, 4096, 4096])
+    assert rc == 0, err
+    assert name != "g950_gemm_bf16_256x256"
+    assert name == "g950_gemm_w8a16_bf16_128x128"

@@ -41,6 +41,15 @@ def close(actual, expected, rtol, atol):
     assert ok, f"max abs err {err} exceeds rtol={rtol} atol={atol}"
 
 
+def tile_rows(m, seed, tile=256):
+    """Rows to check at full size: a random row in every 256-row output
+    tile (so a fault confined to one tile row or one XCD's tiles shows), the
+    tile edges, and the ragged last row."""
+    rng = np.random.default_rng(seed)
+    picks = [t + int(rng.integers(0, min(tile, m - t))) for t in range(0, m, tile)]
+    return np.unique(np.r_[0, 1, min(255, m - 1), min(256, m - 1), m // 2, m - 2, m - 1, picks])
+
+
 # ------------------------------------------------------------ reductions
 @pytest.mark.parametrize("rows,cols", [(4096, 4096), (37, 97), (5, 1), (3, 70001)])
 def test_softmax_rmsnorm_fp32(rows, cols):
@@ -318,8 +327,7 @@ def test_gemm_bf16_config3_sampled(m, n, k):
     c = inputs.config3(m, n, k)
     a = dev(c["a"], "bfloat16")
     y = ops.matmul(a, dev(c["bt"], "bfloat16").t(), sync=True)
-    rows = np.unique(np.r_[0, 1, 255, 256, m // 2, m - 2, m - 1,
-                           np.random.default_rng(9).integers(0, m, 24)])
+    rows = tile_rows(m, 9)
     got = host(y[torch.from_numpy(rows).to(DEV)])
     close(got, ref.matmul(c["a"][rows], c["bt"].T), 2e-2, 2e-2)
 
@@ -420,8 +428,7 @@ def test_int8_gemm_exact_and_dequant(m, n, k):
     y = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
     ops.matmul_i8_dequant_kernel(a, bt.t(), torch.from_numpy(c["sa"]).to(DEV),
                                  torch.from_numpy(c["sb"]).to(DEV), y, m, n, k, sync=True)
-    rows = np.arange(m) if m * n <= 1 << 20 else np.unique(
-        np.r_[0, m - 1, np.random.default_rng(11).integers(0, m, 16)])
+    rows = np.arange(m) if m * n <= 1 << 20 else tile_rows(m, 11)
     exact = ref.matmul_i8(c["a"][rows], c["bt"].T)
     assert np.abs(exact).max() < 2 ** 31
     got = acc[torch.from_numpy(rows).to(DEV)].cpu().numpy()
@@ -484,11 +491,15 @@ def test_attention_non_positive_scale_takes_general_kernel(scale):
 
 
 def test_attention_config4_sampled_heads():
-    """Config 4 at full size; three (batch, head) pairs checked in full."""
+    """Config 4 at full size: one query head of every (batch, KV group) pair --
+    32 of 128 heads, each checked in full -- so every KV head's tiles and
+    every XCD's share of the grid is compared."""
     c = inputs.config4()
     o, lse = ops.attention(dev(c["q"], "bfloat16"), dev(c["k"], "bfloat16"), dev(c["v"], "bfloat16"),
                            causal=True, sync=True)
-    for z, h in ((0, 0), (1, 13), (3, 31)):
+    rng = np.random.default_rng(4)
+    pairs = [(z, 4 * g + int(rng.integers(0, 4))) for z in range(4) for g in range(8)]
+    for z, h in pairs:
         eo, el = ref.attention(c["q"][z:z + 1, h:h + 1], c["k"][z:z + 1, h // 4:h // 4 + 1],
                                c["v"][z:z + 1, h // 4:h // 4 + 1], c["scale"], causal=True)
         close(host(o[z, h]), eo[0, 0], 2e-2, 2e-2)
