@@ -49,8 +49,11 @@ def build_code_object() -> Path:
 def build_runtime() -> Path:
     LIB.mkdir(exist_ok=True)
     tmp = RTLIB.with_name(RTLIB.name + ".tmp")
-    _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-I{ROOT / 'include'}",
-          f"-I{CSRC}", "-o", str(tmp), str(CSRC / "g950rt.cpp"), str(CSRC / "g950_bundle.cpp")])
+    # g950_scratch.hip carries the no-alloc entry's static device array: the
+    # library holds one gfx950 code object of its own for it
+    _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"--offload-arch={ARCH}", "-Xclang",
+          "-target-feature", "-Xclang", "-packed-fp32-ops", f"-I{ROOT / 'include'}", f"-I{CSRC}", "-o",
+          str(tmp), str(CSRC / "g950rt.cpp"), str(CSRC / "g950_bundle.cpp"), str(CSRC / "g950_scratch.hip")])
     os.replace(tmp, RTLIB)
     return RTLIB
 

@@ -84,6 +84,11 @@ struct AttnArgs {
   int group;         // query heads per KV head: KV head of query head h is h / group
 };
 
+struct ZeroArgs {
+  int* p;
+  long long n;  // ints to clear
+};
+
 struct CopyArgs {
   const void* x;
   void* y;

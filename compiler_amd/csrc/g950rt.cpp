@@ -44,12 +44,26 @@ struct g950_module {
   // per-stream arrival counters (split-K), zeroed at allocation; every kernel
   // that uses them leaves them zero
   std::unordered_map<void*, std::pair<void*, size_t>> counters;
+  // device address of the library's static scratch array on this device
+  // (g950_launch_noalloc), looked up at open; null with scratch_err set if the
+  // lookup failed
+  char* scratch = nullptr;
+  hipError_t scratch_err = hipSuccess;
 };
+
+// g950_scratch.hip (same library)
+hipError_t g950_scratch_address(int device, void** out);
 
 namespace {
 
 thread_local std::string t_error;
 thread_local std::string t_kernel;
+// Set while a g950_launch_noalloc call is dispatched on this thread: the
+// device address of the module's scratch array, which then serves every
+// workspace and counter request instead of hipMalloc.
+thread_local char* t_scratch = nullptr;
+constexpr size_t kScratchCounterBytes = 64 << 10;
+constexpr size_t kScratchWorkspace = G950_NOALLOC_SCRATCH_BYTES - kScratchCounterBytes;
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -260,6 +274,13 @@ const char* rr_dtype(uint32_t dt) {
 // Device workspace of at least `bytes` for launches on `stream`.  Growing it
 // waits for the stream (the old buffer may still be read by queued work).
 int workspace(g950_module* m, void* stream, size_t bytes, void** out) {
+  if (t_scratch) {
+    if (bytes > kScratchWorkspace)
+      return fail(G950_USAGE, "no-alloc launch: the call needs %zu bytes of workspace, the scratch array holds %zu",
+                  bytes, kScratchWorkspace);
+    *out = t_scratch;
+    return G950_OK;
+  }
   std::lock_guard<std::mutex> lock(m->ws_mu);
   auto& w = m->ws[stream];
   if (w.second < bytes) {
@@ -282,8 +303,23 @@ int workspace(g950_module* m, void* stream, size_t bytes, void** out) {
   return G950_OK;
 }
 
+template <class Args>
+int launch(g950_module* m, const std::string& name, unsigned grid, unsigned block, Args& args, void* stream);
+
 // Zeroed per-stream counters of at least `n` ints for launches on `stream`.
 int tile_counters(g950_module* m, void* stream, size_t n, int** out) {
+  if (t_scratch) {
+    // the scratch's counter region, cleared by a fill kernel on the stream
+    // (a previous call may have been cut short; no memset node for callers
+    // that capture the launch into a graph)
+    if (n * sizeof(int) > kScratchCounterBytes)
+      return fail(G950_USAGE, "no-alloc launch: %zu arrival counters exceed the scratch's %zu", n,
+                  kScratchCounterBytes / sizeof(int));
+    ZeroArgs z{(int*)(t_scratch + kScratchWorkspace), (long long)n};
+    if (int rc = launch(m, "g950_zero_i32", (unsigned)((n + 255) / 256), 256u, z, stream)) return rc;
+    *out = z.p;
+    return G950_OK;
+  }
   std::lock_guard<std::mutex> lock(m->ws_mu);
   auto& w = m->counters[stream];
   const size_t bytes = n * sizeof(int);
@@ -1274,6 +1310,11 @@ int g950_open(const char* path, g950_module** out) {
     delete m;
     return fail(G950_RESOURCE, "g950_open: loading %s failed: %s", path, hipGetErrorString(e));
   }
+  // the no-alloc entry's scratch array on this (current) device; a failed
+  // lookup only disables g950_launch_noalloc
+  void* sp = nullptr;
+  m->scratch_err = g950_scratch_address(m->device, &sp);
+  m->scratch = (char*)sp;
   *out = m;
   return G950_OK;
 }
@@ -1314,6 +1355,18 @@ int g950_launch(g950_module* m, uint32_t op, const g950_view* views, uint32_t nv
                 const g950_scalar* scalars, uint32_t nscalars, void* stream) {
   if (!m) return fail(G950_USAGE, "g950_launch: null module");
   return dispatch(m, op, views, nviews, scalars, nscalars, stream);
+}
+
+int g950_launch_noalloc(g950_module* m, uint32_t op, const g950_view* views, uint32_t nviews,
+                        const g950_scalar* scalars, uint32_t nscalars, void* stream) {
+  if (!m) return fail(G950_USAGE, "g950_launch_noalloc: null module");
+  if (!m->scratch)
+    return fail(G950_RESOURCE, "g950_launch_noalloc: the scratch array's address is unknown: %s",
+                hipGetErrorString(m->scratch_err));
+  t_scratch = m->scratch;
+  const int rc = dispatch(m, op, views, nviews, scalars, nscalars, stream);
+  t_scratch = nullptr;
+  return rc;
 }
 
 int g950_validate(uint32_t op, const g950_view* views, uint32_t nviews, const g950_scalar* scalars,

@@ -41,7 +41,7 @@ OP_GQA = 16
 DT_BOOL, DT_INT8, DT_UINT8, DT_INT16, DT_UINT16, DT_INT32 = 1, 2, 3, 4, 5, 6
 DT_UINT32, DT_INT64, DT_UINT64, DT_F16, DT_BF16, DT_F32, DT_F64 = 7, 8, 9, 10, 11, 12, 13
 
-EXPORTS = ("g950_open", "g950_launch", "g950_validate", "g950_last_kernel", "g950_sync", "g950_strerror",
+EXPORTS = ("g950_open", "g950_launch", "g950_launch_noalloc", "g950_validate", "g950_last_kernel", "g950_sync", "g950_strerror",
            "g950_last_error", "g950_close", "g950_bundle_open", "g950_bundle_check", "g950_bundle_reason",
            "g950_bundle_count", "g950_bundle_view", "g950_bundle_scalar", "g950_bundle_exec",
            "g950_bundle_close")
@@ -69,6 +69,30 @@ assert ctypes.sizeof(View) == 56 and ctypes.sizeof(Scalar) == 16
 _lib = None
 _lib_lock = threading.Lock()
 
+# G950_NOALLOC_SCRATCH_BYTES (include/g950rt.h)
+NOALLOC_SCRATCH_BYTES = 32 << 20
+
+_mode = threading.local()
+
+
+class no_alloc:
+    """Within ``with no_alloc():`` every operator call on this thread goes
+    through ``g950_launch_noalloc``: no device allocation, workspace from the
+    library's static scratch array (calls that need more are refused)."""
+
+    def __enter__(self):
+        self._prev = getattr(_mode, "noalloc", False)
+        _mode.noalloc = True
+        return self
+
+    def __exit__(self, *exc):
+        _mode.noalloc = self._prev
+        return False
+
+
+def noalloc_active() -> bool:
+    return getattr(_mode, "noalloc", False)
+
 
 def load_library():
     """Load libg950rt.so (does not touch the GPU)."""
@@ -85,6 +109,8 @@ def load_library():
                                     ctypes.c_uint32, ctypes.POINTER(Scalar), ctypes.c_uint32,
                                     ctypes.c_void_p]
         lib.g950_launch.restype = ctypes.c_int
+        lib.g950_launch_noalloc.argtypes = lib.g950_launch.argtypes
+        lib.g950_launch_noalloc.restype = ctypes.c_int
         lib.g950_validate.argtypes = [ctypes.c_uint32, ctypes.POINTER(View), ctypes.c_uint32,
                                       ctypes.POINTER(Scalar), ctypes.c_uint32]
         lib.g950_validate.restype = ctypes.c_int
@@ -209,8 +235,8 @@ class Module:
         if stream is None:
             stream = torch.cuda.current_stream(self.device)
         handle = ctypes.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else stream)
-        rc = self._lib.g950_launch(self._handle, op, views.views, len(tensors), sc, len(scalars),
-                                   handle)
+        entry = self._lib.g950_launch_noalloc if noalloc_active() else self._lib.g950_launch
+        rc = entry(self._handle, op, views.views, len(tensors), sc, len(scalars), handle)
         if rc != OK:
             raise G950Error(rc, self._lib.g950_last_error().decode())
         self.last_kernel = self._lib.g950_last_kernel().decode()

@@ -1,0 +1,115 @@
+"""g950_launch_noalloc against g950_launch through the C ABI: every route
+that takes workspace or counters from the library's static scratch array
+gives the regular entry's results (same kernels: bit for bit), on two calls
+in a row with the second smaller; a call that needs more scratch than the
+array holds is refused with G950_USAGE."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from compiler_amd import operators as ops  # noqa: E402
+from compiler_amd import runtime as rt  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def both(call):
+    """(regular result, no-alloc result, kernel the no-alloc call ran)."""
+    ref_out = call()
+    torch.cuda.synchronize()
+    with rt.no_alloc():
+        out = call()
+        kernel = rt.module().last_kernel
+    torch.cuda.synchronize()
+    return ref_out, out, kernel
+
+
+def split_rows_softmax(rows, cols, seed):
+    x = torch.from_numpy(np.random.default_rng(seed).standard_normal((rows, cols), dtype=np.float32)).to(DEV)
+    x = x.to(torch.bfloat16)
+    return lambda: ops.softmax(x, sync=True)
+
+
+def test_split_rows_two_calls():
+    for rows, cols, seed in ((4, 65536, 1), (3, 40000, 2)):   # few long rows: the two-launch split path
+        a, b, kernel = both(split_rows_softmax(rows, cols, seed))
+        assert kernel.startswith("g950_rs_final_softmax_bf16")
+        assert torch.equal(a, b)
+
+
+def w8a16(m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    a = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(DEV).to(torch.bfloat16)
+    bt = torch.from_numpy(rng.integers(-127, 128, (n, k)).astype(np.int8)).to(DEV)
+    s = torch.from_numpy((rng.random(n) / 64).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    return lambda: ops.dequant_matmul(a, bt.t(), s, sync=True)
+
+
+def test_w8a16_split_k_two_calls():
+    # 17..64 rows, few output tiles: split-K partials in the workspace and
+    # per-tile arrival counters cleared by the fill kernel
+    for m, n, k, seed in ((64, 4096, 4096, 3), (48, 2048, 2048, 4)):
+        a, b, kernel = both(w8a16(m, n, k, seed))
+        assert kernel == "g950_gemm_w8a16_bf16_128x128"
+        assert torch.equal(a, b)
+
+
+def test_w8a16_widened_copy_in_scratch_two_calls():
+    # many output tiles, B small enough for its bf16 copy to fit the scratch
+    for m, n, k, seed in ((1100, 8192, 128, 5), (1025, 8192, 64, 6)):
+        a, b, kernel = both(w8a16(m, n, k, seed))
+        assert kernel == "g950_gemm_bf16_256x256"
+        assert torch.equal(a, b)
+
+
+def test_w8a16_widened_copy_too_large_takes_fused_kernel():
+    # the bf16 copy of B (32 MiB) does not fit: the fused kernel (no workspace)
+    # serves the no-alloc call; different kernels, so the GEMM bar (2e-2)
+    a, b, kernel = both(w8a16(1100, 4096, 4096, 7))
+    assert kernel == "g950_gemm_w8a16_bf16_128x128"
+    ok = torch.isclose(b.float(), a.float(), rtol=2e-2, atol=2e-2).all()
+    assert bool(ok)
+
+
+def unsigned_gemm(m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    a = torch.from_numpy(rng.integers(0, 256, (m, k)).astype(np.uint8)).to(DEV)
+    bt = torch.from_numpy(rng.integers(0, 256, (n, k)).astype(np.uint8)).to(DEV)
+
+    def call():
+        c = torch.empty((m, n), dtype=torch.int32, device=DEV)
+        ops.matmul_i8_kernel(a, bt.t(), c, m, n, k, sync=True)
+        return c
+    return call
+
+
+def test_unsigned_int8_sums_two_calls():
+    for m, n, k, seed in ((512, 512, 1024, 8), (300, 260, 256, 9)):
+        a, b, kernel = both(unsigned_gemm(m, n, k, seed))
+        assert kernel == "g950_gemm_u8u8_256x256"
+        assert torch.equal(a, b)
+
+
+def test_no_scratch_route_unchanged():
+    a, b, kernel = both(split_rows_softmax(64, 3000, 10))   # one wave per row, no workspace
+    assert kernel.startswith("g950_rr_softmax_bf16")
+    assert torch.equal(a, b)
+
+
+def test_request_beyond_scratch_is_refused():
+    # uint8 x uint8 with 9M columns: its column sums need 36 MB of workspace,
+    # more than the scratch holds -- refused before any kernel runs
+    n = 9_000_000
+    a = torch.zeros((1, 128), dtype=torch.uint8, device=DEV)
+    bt = torch.empty((n, 128), dtype=torch.uint8, device=DEV)
+    c = torch.full((1, n), 7, dtype=torch.int32, device=DEV)
+    with rt.no_alloc():
+        with pytest.raises(rt.G950Error) as err:
+            ops.matmul_i8_kernel(a, bt.t(), c, 1, n, 128, sync=True)
+    assert err.value.code == rt.USAGE and "scratch" in str(err.value)
+    assert bool((c == 7).all())
+    del bt
+    torch.cuda.empty_cache()
