@@ -12,9 +12,12 @@ The same line carries
     / its average launch time, HIP events on the launch stream) against the
     8 TB/s HBM peak;
   * cpu_baseline: the OpenMP fp32 CPU path (oracle/cpu_baseline.c, the a100c
-    worker-pool restatement) on the same workload, on this host's cores;
+    worker-pool restatement) on the same workload, on this host's cores, with
+    the numpy float64 oracle (the reference ref() semantics) beside it;
   * suite: every other BASELINE config (fp32 RMSNorm/softmax GB/s, bf16 GEMM,
-    causal GQA attention and int8 GEMM TFLOP/s) with its own roofline fraction.
+    causal GQA attention and int8 GEMM TFLOP/s) with its own roofline fraction
+    and, for each BASELINE config, both CPU baselines on a bounded sample
+    (rows of A, query heads, rows of x) sized to about a second each.
 """
 from __future__ import annotations
 
@@ -171,11 +174,69 @@ def cpu_baseline(seconds=10.0):
         if el >= seconds or reps >= 1000:
             break
     nbytes = (2 * rows * cols * 2 + 2 * cols * 2 + 2 * rows * 4) + 2 * rows * cols * 2
+    from oracle import reference as ref
+
+    def f64(nrows):
+        ref.layernorm(c["x"][:nrows], c["gamma"], c["beta"], 1e-5)
+        ref.softmax(c["x"][:nrows])
+    n, t = sized_time(f64, 256, rows)
+    per_row = nbytes / rows
     return {"value": round(nbytes * reps / el / 1e9, 2), "unit": "GB/s", "cores": int(lib.g950o_threads()),
             "kind": "port",
             "sample": f"full config-2 workload (LayerNorm + softmax, bf16 [8191,3000]) x {reps} passes, "
                       f"{el:.1f} s, oracle/cpu_baseline.c OpenMP fp32",
-            "cpu": _cpu_model()}
+            "cpu": _cpu_model(),
+            "numpy_f64": {"value": round(per_row * n / t / 1e9, 3), "unit": "GB/s",
+                          "threads": _blas_threads() or "numpy (reductions single-threaded)",
+                          "sample": f"{n} rows of the same workload, {t:.2f} s, oracle/reference.py float64"}}
+
+
+CPU_TARGET_S = 1.0   # seconds of CPU work per timed baseline sample
+
+
+def _blas_threads():
+    keys = ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS")
+    return {k: os.environ[k] for k in keys if k in os.environ}
+
+
+def sized_time(run, n0, n_max, target_s=CPU_TARGET_S):
+    """Time ``run(n)`` on a bounded sample: a warm-up call with ``n0`` units
+    (first touch, thread-pool start), a probe call with ``n0`` units, then
+    calls with ``n`` scaled so one takes about ``target_s`` (at most
+    ``n_max``, the whole config), repeated until about ``target_s`` has
+    passed.  Returns (units timed, seconds)."""
+    run(n0)
+    t0 = time.perf_counter()
+    run(n0)
+    probe = max(time.perf_counter() - t0, 1e-6)
+    n = int(min(n_max, max(n0, n0 * target_s / probe)))
+    done, t0 = 0, time.perf_counter()
+    while True:
+        run(n)
+        done += n
+        el = time.perf_counter() - t0
+        if el >= target_s or done >= 100 * n:
+            return done, el
+
+
+def cpu_legs(port_run, f64_run, work_per_unit, unit, scale, what, n0, n_max):
+    """Both CPU baselines of one config on a bounded sample of ``what`` units:
+    the OpenMP fp32 port (oracle/cpu_baseline.c, the a100c worker-pool
+    partition) and the numpy float64 oracle (oracle/reference.py restating the
+    reference ``ref()``).  ``work_per_unit`` is bytes or FLOP per unit; the
+    value is work / time / ``scale`` in ``unit``."""
+    from oracle import build as obuild
+    lib = obuild.load()
+    n, t = sized_time(port_run, n0, n_max)
+    out = {"value": round(work_per_unit * n / t / scale, 3), "unit": unit, "cores": int(lib.g950o_threads()),
+           "kind": "port", "sample": f"{n} {what}, {t:.2f} s, oracle/cpu_baseline.c OpenMP fp32",
+           "cpu": _cpu_model()}
+    if f64_run is not None:
+        n, t = sized_time(f64_run, n0, n_max)
+        out["numpy_f64"] = {"value": round(work_per_unit * n / t / scale, 3), "unit": unit,
+                            "threads": _blas_threads() or f"numpy BLAS default ({os.cpu_count()} CPUs visible)",
+                            "sample": f"{n} {what}, {t:.2f} s, oracle/reference.py float64"}
+    return out
 
 
 def _cpu_model():
@@ -188,9 +249,16 @@ def _cpu_model():
     return "unknown"
 
 
-def suite(torch, ops):
-    """Every other BASELINE config, timed per kernel with HIP events."""
+def suite(torch, ops, cpu=True):
+    """Every other BASELINE config, timed per kernel with HIP events; with
+    ``cpu`` each BASELINE config row also carries its CPU baselines (both
+    legs) on a bounded sample of the same inputs."""
+    from oracle import build as obuild
     from oracle import inputs
+    from oracle import reference as ref
+    from oracle.reference import bf16_bits
+    lib = obuild.load() if cpu else None
+    P = lambda a: a.ctypes.data  # noqa: E731
     dev = "cuda:0"
     out = []
 
@@ -216,6 +284,17 @@ def suite(torch, ops):
                     "frac": round(gbs / HBM_PEAK_GBS, 4)})
     del sets
     torch.cuda.empty_cache()
+    if cpu:
+        c1 = inputs.config1()
+        x1, w1 = c1["x"], c1["w"]
+        y1, r1 = np.empty_like(x1), np.empty(4096, np.float32)
+        out[-2]["cpu_baseline"] = cpu_legs(
+            lambda n: lib.g950o_rmsnorm_f32(P(x1), P(w1), P(y1), P(r1), n, 4096, 1e-6),
+            lambda n: ref.rms_layernorm(x1[:n], w1, 1e-6), rb / 4096, "GB/s", 1e9, "rows of [4096,4096]", 256, 4096)
+        out[-1]["cpu_baseline"] = cpu_legs(
+            lambda n: lib.g950o_softmax_f32(P(x1), P(y1), n, 4096),
+            lambda n: ref.softmax(x1[:n]), sb / 4096, "GB/s", 1e9, "rows of [4096,4096]", 256, 4096)
+        del c1, x1, y1
 
     # next-row operators at their BASELINE-sized shapes, 4 rotating sets each:
     # row logsumexp bf16 [8191, 3000] -> fp32, int8 weight dequant [8192, 8192] -> bf16
@@ -245,7 +324,6 @@ def suite(torch, ops):
         c = inputs.config3(m, n, k)
         a = torch.from_numpy(c["a"]).to(dev).to(torch.bfloat16)
         bt = torch.from_numpy(c["bt"]).to(dev).to(torch.bfloat16)
-        del c
         y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         call = ops.matmul_kernel(a, bt.t(), y, m, n, k, prepare=True)
         ms = event_time(torch, lambda i: call(), 20, 3, warm_s=0.5)
@@ -255,12 +333,25 @@ def suite(torch, ops):
                     "frac": round(tf / BF16_PEAK_TFS, 4)})
         del a, bt, y
         torch.cuda.empty_cache()
+        if cpu:
+            # rows of A against all of B (inputs resident: B widened once
+            # outside the timed sample, as the GPU's B is resident in HBM)
+            ab, btb = bf16_bits(c["a"]), bf16_bits(c["bt"])
+            b32 = np.empty(btb.shape, np.float32)
+            lib.g950o_widen_bf16(P(btb), P(b32), btb.size)
+            cbuf = np.empty((m, n), np.uint16)
+            b64 = c["bt"].T.astype(np.float64)
+            a64 = c["a"].astype(np.float64)
+            out[-1]["cpu_baseline"] = cpu_legs(
+                lambda r: lib.g950o_gemm_bf16_wide(P(ab), P(b32), P(cbuf), 0, r, n, k),
+                lambda r: a64[:r] @ b64, 2.0 * n * k, "TFLOP/s", 1e12, f"rows of A ({m}x{n}x{k})", 8, m)
+            del ab, btb, b32, cbuf, b64, a64
+        del c
 
     # C4: causal GQA attention bf16 (4, 32/8, 4096, 128) with LSE
     c = inputs.config4()
     bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
     q, k, v = bf(c["q"]), bf(c["k"]), bf(c["v"])
-    del c
     o = torch.empty_like(q)
     lse = torch.empty((4, 32, 4096), dtype=torch.float32, device=dev)
     call = ops.attn_fwd_causal_kernel(q, k, v, o, 4, 32, 4096, 1 / math.sqrt(128), *q.stride(), *k.stride(),
@@ -273,6 +364,20 @@ def suite(torch, ops):
                 "frac": round(tf / BF16_PEAK_TFS, 4)})
     del q, k, v, o, lse
     torch.cuda.empty_cache()
+    if cpu:
+        # whole (batch 0, head) slices: 4096 causal query rows each
+        qb, kb, vb = (bf16_bits(c[n][0]) for n in ("q", "k", "v"))
+        ob = np.empty((32, 4096, 128), np.uint16)
+        lb = np.empty((32, 4096), np.float32)
+        head_flops = 4.0 * 128 * 4096 * 4096 / 2
+        out[-1]["cpu_baseline"] = cpu_legs(
+            lambda hn: lib.g950o_attention_bf16(P(qb), P(kb), P(vb), P(ob), P(lb), 32, 8, 4096, 128, 0, hn, 0, 4096,
+                                                1 / math.sqrt(128), 1),
+            lambda hn: ref.attention(c["q"][:1, :hn], c["k"][:1, :(hn + 3) // 4], c["v"][:1, :(hn + 3) // 4],
+                                     1 / math.sqrt(128), causal=True, group=4),
+            head_flops, "TFLOP/s", 1e12, "(batch 0, query head) slices of 4096 causal rows", 1, 32)
+        del qb, kb, vb, ob, lb
+    del c
 
     # few long rows (split-row two-phase path): softmax bf16 [4, 2^22]
     xs = [torch.randn((4, 1 << 22), device=dev, generator=g).to(torch.bfloat16) for _ in range(ROTATE)]
@@ -370,7 +475,6 @@ def suite(torch, ops):
     bt = torch.from_numpy(c["bt"]).to(dev)
     sa = torch.from_numpy(c["sa"]).to(dev)
     sbv = torch.from_numpy(c["sb"]).to(dev)
-    del c
     y = torch.empty((4096, 8192), dtype=torch.bfloat16, device=dev)
     call = ops.matmul_i8_dequant_kernel(a, bt.t(), sa, sbv, y, 4096, 8192, 8192, prepare=True)
     ms = event_time(torch, lambda i: call(), 20, 3, warm_s=0.5)
@@ -378,6 +482,17 @@ def suite(torch, ops):
     out.append({"config": "C5 int8 gemm 4096x8192x8192 + dequant", "kernel": call.kernel,
                 "us": round(ms * 1e3, 1), "value": round(tops, 1), "unit": "TOP/s", "bound": "mfma",
                 "frac": round(tops / INT8_PEAK_TOPS, 4)})
+    del a, bt, sa, sbv, y
+    torch.cuda.empty_cache()
+    if cpu:
+        yc = np.empty((4096, 8192), np.uint16)
+        b64 = c["bt"].T.astype(np.float64)
+        a64 = c["a"].astype(np.float64)
+        out[-1]["cpu_baseline"] = cpu_legs(
+            lambda r: lib.g950o_gemm_i8(P(c["a"]), P(c["bt"]), P(c["sa"]), P(c["sb"]), None, P(yc), 0, r, 8192, 8192),
+            lambda r: ref.dequant(np.rint(a64[:r] @ b64), c["sa"][:r], c["sb"]),
+            2.0 * 8192 * 8192, "TOP/s", 1e12, "rows of A (4096x8192x8192, int32 exact + dequant)", 8, 4096)
+        del yc, b64, a64
     return out
 
 
@@ -406,34 +521,65 @@ def pmc_probe(torch, ops):
                      torch.empty(rows, device=dev), torch.empty(rows, device=dev)))
     ln = [ops.layernorm_kernel(x, y, g, b, m, r, cols, cols, 1e-5, prepare=True) for x, g, b, y, m, r in sets]
     sm = [ops.softmax_kernel(x, y, cols, prepare=True) for x, g, b, y, m, r in sets]
+    lr = [ops.layer_norm_forward_row(y.view(-1), cols, x, cols, g, b, m, 1, r, 1, rows, cols, 1e-5, prepare=True)
+          for x, g, b, y, m, r in sets]
     torch.cuda.synchronize()
+    for calls in (ln, sm, lr):
+        for i in range(8):
+            calls[i % ROTATE]()
+        torch.cuda.synchronize()
+    del sets, ln, sm, lr
+    # C1 fp32 [4096, 4096] RMSNorm and softmax, 4 rotating sets
+    c1 = [(torch.randn((4096, 4096), device=dev), torch.rand(4096, device=dev) + 0.5,
+           torch.empty((4096, 4096), device=dev), torch.empty(4096, device=dev)) for _ in range(ROTATE)]
+    rms = [ops.rms_layernorm_forward_kernel(y, 4096, x, 4096, w, 1, r, 1, 4096, 1e-6, prepare=True)
+           for x, w, y, r in c1]
+    smf = [ops.softmax_kernel(x, y, 4096, prepare=True) for x, w, y, r in c1]
+    for calls in (rms, smf):
+        for i in range(8):
+            calls[i % ROTATE]()
+        torch.cuda.synchronize()
+    del c1, rms, smf
+    # int8 weight dequantisation [8192, 8192] -> bf16, 4 rotating sets
+    dq = [(torch.randint(-127, 127, (8192, 8192), device=dev, dtype=torch.int8),
+           torch.rand(8192, device=dev).to(torch.bfloat16),
+           torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)) for _ in range(ROTATE)]
+    dqc = [ops.dequantize_kernel(b, sc, y, 8192, 8192, 8192, 1, 8192, 1, prepare=True) for b, sc, y in dq]
     for i in range(8):
-        ln[i % ROTATE]()
+        dqc[i % ROTATE]()
     torch.cuda.synchronize()
-    for i in range(8):
-        sm[i % ROTATE]()
-    torch.cuda.synchronize()
-    log(f"pmc probe: copy {src.numel() * 2} B read + write; layernorm/softmax x8 each")
+    log(f"pmc probe: copy {src.numel() * 2} B read + write; C2 layernorm/softmax/layer_norm_forward_row, "
+        "C1 rmsnorm/softmax fp32, dequantize int8->bf16 8192^2: x8 each")
 
 
 def mfma_probe(torch, ops):
     """Counter-collection workload for the MFMA-bound kernels (run under
-    rocprofv3 --pmc): C3 bf16 GEMM 8192^3 and C4 causal GQA attention, three
-    launches each after one warm-up launch."""
+    rocprofv3 --pmc): C3 bf16 GEMM 8192^3 and 4097x11008x4096, C4 causal GQA
+    attention and the C5 int8 GEMM, three launches each after one warm-up
+    launch."""
     import math
     from oracle import inputs
     dev = "cuda:0"
-    m = n = k = 8192
-    c = inputs.config3(m, n, k)
-    a = torch.from_numpy(c["a"]).to(dev).to(torch.bfloat16)
-    bt = torch.from_numpy(c["bt"]).to(dev).to(torch.bfloat16)
-    del c
-    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    gemm = ops.matmul_kernel(a, bt.t(), y, m, n, k, prepare=True)
+    for m, n, k in ((8192, 8192, 8192), (4097, 11008, 4096)):
+        c = inputs.config3(m, n, k)
+        a = torch.from_numpy(c["a"]).to(dev).to(torch.bfloat16)
+        bt = torch.from_numpy(c["bt"]).to(dev).to(torch.bfloat16)
+        del c
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        gemm = ops.matmul_kernel(a, bt.t(), y, m, n, k, prepare=True)
+        for _ in range(4):
+            gemm()
+        torch.cuda.synchronize()
+        del a, bt, y
+    c5 = inputs.config5()
+    a8, b8 = torch.from_numpy(c5["a"]).to(dev), torch.from_numpy(c5["bt"]).to(dev)
+    sa, sb = torch.from_numpy(c5["sa"]).to(dev), torch.from_numpy(c5["sb"]).to(dev)
+    y8 = torch.empty((4096, 8192), dtype=torch.bfloat16, device=dev)
+    i8 = ops.matmul_i8_dequant_kernel(a8, b8.t(), sa, sb, y8, 4096, 8192, 8192, prepare=True)
     for _ in range(4):
-        gemm()
+        i8()
     torch.cuda.synchronize()
-    del a, bt, y
+    del a8, b8, y8, c5
     c = inputs.config4()
     bf = lambda x: torch.from_numpy(x).to(dev).to(torch.bfloat16)  # noqa: E731
     q, kk, v = bf(c["q"]), bf(c["k"]), bf(c["v"])
@@ -444,7 +590,7 @@ def mfma_probe(torch, ops):
     for _ in range(4):
         attn()
     torch.cuda.synchronize()
-    log(f"mfma probe: {gemm.kernel} x4, {attn.kernel} x4")
+    log(f"mfma probe: {gemm.kernel} x4 (two shapes), {i8.kernel} x4, {attn.kernel} x4")
 
 
 def traffic_for(kernel):
@@ -467,7 +613,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-suite", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=3.0)
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run only the counter-collection workload (for rocprofv3 --pmc)")
     ap.add_argument("--mfma-probe", action="store_true",
@@ -494,7 +640,7 @@ def main():
     suite_rows = []
     if not args.no_suite:
         log("bench: suite ...")
-        suite_rows = suite(torch, ops)
+        suite_rows = suite(torch, ops, cpu=not args.no_cpu)
         for r in suite_rows:
             log(f"bench:   {r['config']}: {r['value']} {r['unit']} ({r['frac'] * 100:.1f}% of peak)")
     cpu = None

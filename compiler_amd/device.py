@@ -67,65 +67,65 @@ def _kernel_params(kernel):
     return [p for p in inspect.signature(target).parameters if p not in tuned]
 
 
-def _softmax(a):
-    ops.softmax_kernel(a["x_ptr"], a["y_ptr"], a["n_cols"], sync=True)
+def _softmax(a, sync):
+    ops.softmax_kernel(a["x_ptr"], a["y_ptr"], a["n_cols"], sync=sync)
 
 
-def _softmax_inner(a):
+def _softmax_inner(a, sync):
     ops.softmax_kernel_inner(a["output_ptr"], a["input_ptr"], a["M"], a["N"], a.get("TILE_N"),
-                             a.get("ONE_TILE_PER_CTA"), sync=True)
+                             a.get("ONE_TILE_PER_CTA"), sync=sync)
 
 
-def _layer_norm_row(a):
+def _layer_norm_row(a, sync):
     ops.layer_norm_forward_row(a["Y_ptr"], a["Y_row_stride"], a["X_ptr"], a["X_row_stride"], a["W_ptr"],
                                a["B_ptr"], a["Mean_ptr"], a["Mean_row_stride"], a["RSTD_ptr"],
                                a["RSTD_row_stride"], a["n_rows"], a["n_cols"], a["eps"], a.get("BLOCK_SIZE"),
-                               sync=True)
+                               sync=sync)
 
 
-def _gqa(a):
+def _gqa(a, sync):
     names = ["stride_qh", "stride_qm", "stride_qk", "stride_kh", "stride_kn", "stride_kk", "stride_vh",
              "stride_vk", "stride_vn", "stride_oh", "stride_om", "stride_on"]
     ops.gqa_kernel(a["Q"], a["K"], a["V"], a["Out"], *[a[n] for n in names], a["H_Q"], a["H_KV"], a["N_CTX"],
-                   a["scale"], a["GROUP"], a.get("HEAD_DIM"), sync=True)
+                   a["scale"], a["GROUP"], a.get("HEAD_DIM"), sync=sync)
 
 
-def _logsumexp(a):
-    ops.logsumexp_kernel(a["x_ptr"], a["y_ptr"], a["n_cols"], sync=True)
+def _logsumexp(a, sync):
+    ops.logsumexp_kernel(a["x_ptr"], a["y_ptr"], a["n_cols"], sync=sync)
 
 
-def _dequantize(a):
+def _dequantize(a, sync):
     ops.dequantize_kernel(a["b_ptr"], a["b_scale_ptr"], a["fpb_ptr"], a["K"], a["N"], a["stride_bk"],
-                          a["stride_bn"], a["stride_fpbk"], a["stride_fpbn"], sync=True)
+                          a["stride_bn"], a["stride_fpbk"], a["stride_fpbn"], sync=sync)
 
 
-def _flash_varlen(a):
+def _flash_varlen(a, sync):
     from .operators import _VARLEN_SCALARS, _VARLEN_VIEWS
-    ops.flash_varlen_fwd_kernel(**{n: a[n] for n in _VARLEN_VIEWS + _VARLEN_SCALARS}, sync=True)
+    ops.flash_varlen_fwd_kernel(**{n: a[n] for n in _VARLEN_VIEWS + _VARLEN_SCALARS}, sync=sync)
 
 
-def _rms(a):
+def _rms(a, sync):
     ops.rms_layernorm_forward_kernel(a["Y"], a["Y_row_stride"], a["X"], a["X_row_stride"], a["W"],
                                      a["W_row_stride"], a["r"], a["r_row_stride"], a["n_cols"],
-                                     a["eps"], sync=True)
+                                     a["eps"], sync=sync)
 
 
-def _layernorm(a):
+def _layernorm(a, sync):
     ops.layernorm_kernel(a["X"], a["Y"], a["W"], a["B"], a["Mean"], a["Rstd"], a["stride"], a["N"],
-                         a["eps"], sync=True)
+                         a["eps"], sync=sync)
 
 
-def _matmul(a):
-    ops.matmul_kernel(a["a_ptr"], a["b_ptr"], a["y_ptr"], a["M"], a["N"], a["K"], sync=True)
+def _matmul(a, sync):
+    ops.matmul_kernel(a["a_ptr"], a["b_ptr"], a["y_ptr"], a["M"], a["N"], a["K"], sync=sync)
 
 
-def _attention(a, causal_default):
+def _attention(a, causal_default, sync):
     names = ["stride_qz", "stride_qh", "stride_qm", "stride_qk", "stride_kz", "stride_kh",
              "stride_kn", "stride_kk", "stride_vz", "stride_vh", "stride_vk", "stride_vn",
              "stride_oz", "stride_oh", "stride_om", "stride_on"]
     ops.attn_fwd_causal_kernel(a["q_ptr"], a["k_ptr"], a["v_ptr"], a["out_ptr"], a["Z"], a["H"],
                                a["N_CTX"], a["scale"], *[a[n] for n in names],
-                               CAUSAL=bool(a.get("CAUSAL", causal_default)), sync=True)
+                               CAUSAL=bool(a.get("CAUSAL", causal_default)), sync=sync)
 
 
 # reference kernel name -> operator (hot path only)
@@ -140,9 +140,39 @@ KERNELS = {
     "rms_layernorm_forward_kernel": _rms,
     "layernorm_kernel": _layernorm,
     "matmul_kernel": _matmul,
-    "attn_fwd_causal_kernel": lambda a: _attention(a, True),
-    "attention_forward_kernel": lambda a: _attention(a, False),
+    "attn_fwd_causal_kernel": lambda a, sync: _attention(a, True, sync),
+    "attention_forward_kernel": lambda a, sync: _attention(a, False, sync),
 }
+
+
+class G950Timer:
+    """``with timer: launch()`` brackets the launch with two HIP events on
+    the launch stream.  Inside the block the device launches without a host
+    wait, so the end event lands right behind the kernels; leaving the block
+    waits for it, so the launch has finished when the block ends (the
+    contract of COMPILE_CONTRACT.md:73-74).  ``seconds`` is the elapsed GPU
+    time between the events."""
+
+    def __init__(self, device):
+        torch = device.torch
+        self._device = device
+        self._start = torch.cuda.Event(enable_timing=True)
+        self._end = torch.cuda.Event(enable_timing=True)
+        self.seconds = None
+
+    def __enter__(self):
+        torch = self._device.torch
+        self._stream = torch.cuda.current_stream(self._device.device)
+        self._start.record(self._stream)
+        self._device._timing = True
+        return self
+
+    def __exit__(self, *exc):
+        self._device._timing = False
+        self._end.record(self._stream)
+        self._end.synchronize()
+        self.seconds = self._start.elapsed_time(self._end) / 1000.0
+        return False
 
 
 class G950Device:
@@ -156,6 +186,7 @@ class G950Device:
             raise RuntimeError("G950Device needs an MI355X (gfx950) GPU")
         self.torch = torch
         self.device = torch.device(device)
+        self._timing = False   # inside a timer: launches stay asynchronous
 
     # -- memory -----------------------------------------------------------
     def _tdtype(self, name):
@@ -192,6 +223,21 @@ class G950Device:
     def compare(self, buffer, expected, policy):
         return None  # host comparison by the harness
 
+    def timer(self):
+        """Device-event timing for the reference benchmark
+        (ops/harness/benchmark/run.py:126-133,255): ``with timer: launch()``
+        then ``timer.seconds``."""
+        return G950Timer(self)
+
+    def release(self, buffers):
+        """Free buffers (a dict or iterable of G950Buffer) the reference
+        benchmark is done with (benchmark/run.py:126-133); their memory goes
+        back to torch's allocator for the next entry."""
+        items = buffers.values() if isinstance(buffers, dict) else buffers
+        for b in items:
+            if isinstance(b, G950Buffer):
+                b.tensor = None
+
     def properties(self):
         p = self.torch.cuda.get_device_properties(self.device)
         return {"name": p.name, "gcn_arch": getattr(p, "gcnArchName", ""),
@@ -207,4 +253,4 @@ class G950Device:
         values.update(keywords or {})
         args = {k: (v.tensor if isinstance(v, G950Buffer) else v) for k, v in values.items()}
         with self.torch.cuda.device(self.device):
-            KERNELS[name](args)
+            KERNELS[name](args, not self._timing)

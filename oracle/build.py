@@ -43,6 +43,8 @@ def load():
     lib.g950o_softmax_bf16.argtypes = [P, P, L, L]
     lib.g950o_layernorm_bf16.argtypes = [P, P, P, P, P, P, L, L, F]
     lib.g950o_gemm_bf16.argtypes = [P, P, P, L, L, L, L]
+    lib.g950o_gemm_bf16_wide.argtypes = [P, P, P, L, L, L, L]
+    lib.g950o_widen_bf16.argtypes = [P, P, L]
     lib.g950o_gemm_i8.argtypes = [P, P, P, P, P, P, L, L, L, L]
     lib.g950o_attention_bf16.argtypes = [P, P, P, P, P, L, L, L, L, L, L, L, L, F, ctypes.c_int]
     return lib

@@ -131,13 +131,17 @@ void g950o_layernorm_bf16(const uint16_t *x, const uint16_t *w, const uint16_t *
   }
 }
 
-/* C[m, n] = sum_k A[m, k] * Bt[n, k] for rows [m0, m1) of A; fp32 accumulate,
- * bf16 output.  Tiles of 4 output rows x 4 output columns are the programs. */
-void g950o_gemm_bf16(const uint16_t *a, const uint16_t *bt, uint16_t *c, long m0, long m1, long N,
-                     long K) {
-  float *bf32 = (float *)malloc(sizeof(float) * (size_t)N * (size_t)K);
+/* bf16 bits -> fp32 values (exact widening), n elements. */
+void g950o_widen_bf16(const uint16_t *src, float *dst, long n) {
 #pragma omp parallel for schedule(static)
-  for (long i = 0; i < N * K; ++i) bf32[i] = bf(bt[i]);
+  for (long i = 0; i < n; ++i) dst[i] = bf(src[i]);
+}
+
+/* C[m, n] = sum_k A[m, k] * Bt[n, k] for rows [m0, m1) of bf16 A, with Bt
+ * already widened to fp32; fp32 accumulate, bf16 output.  Tiles of 4 output
+ * rows x 4 output columns are the programs. */
+void g950o_gemm_bf16_wide(const uint16_t *a, const float *bf32, uint16_t *c, long m0, long m1, long N,
+                          long K) {
   const long mt = (m1 - m0 + 3) / 4, nt = (N + 3) / 4;
 #pragma omp parallel
   {
@@ -159,6 +163,14 @@ void g950o_gemm_bf16(const uint16_t *a, const uint16_t *bt, uint16_t *c, long m0
     }
     free(arow);
   }
+}
+
+/* The same with Bt in bf16 (widened here first). */
+void g950o_gemm_bf16(const uint16_t *a, const uint16_t *bt, uint16_t *c, long m0, long m1, long N,
+                     long K) {
+  float *bf32 = (float *)malloc(sizeof(float) * (size_t)N * (size_t)K);
+  g950o_widen_bf16(bt, bf32, N * K);
+  g950o_gemm_bf16_wide(a, bf32, c, m0, m1, N, K);
   free(bf32);
 }
 

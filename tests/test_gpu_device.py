@@ -181,3 +181,108 @@ def test_device_refuses_other_kernels():
     xb, yb = d.upload(np.zeros(8, np.float32)), d.alloc((8,), np.float32)
     with pytest.raises(NotImplementedError):
         d.launch(gelu_kernel, (1,), (xb, yb, 8), {})
+
+
+# stand-ins with the reference kernels' names and parameter lists
+def attn_fwd_causal_kernel(q_ptr, k_ptr, v_ptr, out_ptr, Z, H, N_CTX, scale,  # noqa: N803
+                           stride_qz, stride_qh, stride_qm, stride_qk, stride_kz, stride_kh, stride_kn, stride_kk,
+                           stride_vz, stride_vh, stride_vk, stride_vn, stride_oz, stride_oh, stride_om, stride_on,
+                           BLOCK_M, BLOCK_N, HEAD_DIM, CAUSAL):
+    raise AssertionError("dispatched by name, never called")
+
+
+def softmax_kernel_inner(output_ptr, input_ptr, M, N, TILE_N, ONE_TILE_PER_CTA):  # noqa: N803
+    raise AssertionError("dispatched by name, never called")
+
+
+def _layer_norm_forward_row(Y_ptr, Y_row_stride, X_ptr, X_row_stride, W_ptr, B_ptr, Mean_ptr,  # noqa: N803
+                            Mean_row_stride, RSTD_ptr, RSTD_row_stride, n_rows, n_cols, eps, BLOCK_SIZE):
+    raise AssertionError("dispatched by name, never called")
+
+
+def gqa_kernel(Q, K, V, Out, stride_qh, stride_qm, stride_qk, stride_kh, stride_kn, stride_kk,  # noqa: N803
+               stride_vh, stride_vk, stride_vn, stride_oh, stride_om, stride_on, H_Q, H_KV, N_CTX, scale, GROUP,
+               HEAD_DIM, BLOCK_N):
+    raise AssertionError("dispatched by name, never called")
+
+
+def test_device_attn_fwd_causal_kernel_perf_lane():
+    """The perf-suite name BASELINE config 4 maps to (ops/suite/perf/attn_fwd_causal.py),
+    causal, bf16, GQA-free shape as the suite runs it."""
+    d = G950Device()
+    rng = np.random.default_rng(21)
+    z, h, n, hd = 2, 4, 300, 128
+    q, k, v = (rng.standard_normal((z, h, n, hd)).astype(np.float32) for _ in range(3))
+    qb, kb, vb = (d.upload(a, "bfloat16") for a in (q, k, v))
+    ob = d.alloc(q.shape, "bfloat16")
+    st = (h * n * hd, n * hd, hd, 1)
+    d.launch(attn_fwd_causal_kernel, (3, z * h), (qb, kb, vb, ob, z, h, n, np.float32(hd ** -0.5), *st, *st, *st, *st),
+             {"BLOCK_M": 128, "BLOCK_N": 64, "HEAD_DIM": hd, "CAUSAL": True})
+    assert rt.module().last_kernel == "g950_attn_fwd_bf16_d128"
+    qr, kr, vr = (ref.bf16_round(a) for a in (q, k, v))
+    eo, _ = ref.attention(qr, kr, vr, hd ** -0.5, causal=True)
+    ok, err = ref.isclose_verdict(d.download(ob), eo, 2e-2, 2e-2)
+    assert ok, err
+
+
+def test_device_dev_suite_kernels():
+    """softmax_kernel_inner, _layer_norm_forward_row and gqa_kernel as the
+    reference case layer calls them (flat buffers, the 2-D X_ptr, 4-D GQA
+    arrays, constexprs in the keywords)."""
+    d = G950Device()
+    rng = np.random.default_rng(22)
+    x = rng.normal(0, 0.8, 96)
+    xb, yb = d.upload(x.astype(np.float32)), d.upload(np.full(96, -7.0, np.float32))
+    d.launch(softmax_kernel_inner, (3,), (yb, xb, 3, 32), {"TILE_N": 128, "ONE_TILE_PER_CTA": False})
+    assert np.allclose(d.download(yb), ref.softmax_inner(x.astype(np.float32), 3, 32), rtol=1e-5, atol=1e-7)
+
+    r, c = 5, 128
+    xs = rng.normal(0, 0.7, (r, c)).astype(np.float32)
+    w = rng.uniform(0.7, 1.3, c).astype(np.float32)
+    b = rng.normal(0, 0.1, c).astype(np.float32)
+    bufs = {"Y": d.upload(np.full(r * c, -7.0, np.float32)), "X": d.upload(xs), "W": d.upload(w),
+            "B": d.upload(b), "M": d.upload(np.full(r, -7.0, np.float32)), "R": d.upload(np.full(r, -7.0, np.float32))}
+    d.launch(_layer_norm_forward_row, (r,), (bufs["Y"], c, bufs["X"], c, bufs["W"], bufs["B"], bufs["M"], 1,
+                                             bufs["R"], 1),
+             {"n_rows": r, "n_cols": c, "eps": 1e-5, "BLOCK_SIZE": c})
+    ey, em, es = ref.layernorm_row(xs, w, b, 1e-5)
+    assert np.allclose(d.download(bufs["Y"]).reshape(r, c), ey, rtol=1e-4, atol=1e-4)
+    assert np.allclose(d.download(bufs["M"]), em, rtol=1e-4, atol=1e-6)
+    assert np.allclose(d.download(bufs["R"]), es, rtol=1e-4)
+
+    z, hq, hkv, n, hd = 2, 4, 2, 64, 32
+    q = rng.standard_normal((z, hq, n, hd)).astype(np.float32)
+    k = rng.standard_normal((z, hkv, n, hd)).astype(np.float32)
+    v = rng.standard_normal((z, hkv, n, hd)).astype(np.float32)
+    qb, kb, vb = d.upload(q), d.upload(k), d.upload(v)
+    ob = d.alloc(q.shape, np.float32)
+    st = (n * hd, hd, 1)
+    d.launch(gqa_kernel, (2, z * hq), (qb, kb, vb, ob, *st, *st, *st, *st, hq, hkv, n, np.float32(hd ** -0.5)),
+             {"GROUP": 2, "HEAD_DIM": hd, "BLOCK_N": 32})
+    ok, err = ref.isclose_verdict(d.download(ob), ref.gqa(q, k, v, hd ** -0.5, 2), 2e-2, 2e-2)
+    assert ok, err
+
+
+def test_device_timer_and_release():
+    """timer(): device events around one launch, the way the reference
+    benchmark measures (benchmark/run.py:155-170); the launch has finished
+    when the block ends.  release() frees the entry's buffers."""
+    d = G950Device()
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((8191, 3000)).astype(np.float32)
+    xb, yb = d.upload(x, "bfloat16"), d.alloc(x.shape, "bfloat16")
+    timer = d.timer()
+    times = []
+    for _ in range(5):
+        with timer:
+            d.launch(softmax_kernel, (8191,), (xb, yb, 3000), {"BLOCK_SIZE": 4096})
+        times.append(timer.seconds)
+    # the result is complete at the end of the block
+    ok, err = ref.isclose_verdict(d.download(yb)[:4], ref.softmax(ref.bf16_round(x[:4])), 2e-2, 2e-2)
+    assert ok, err
+    # 98 MB through HBM: tens of microseconds, far below a host round trip of milliseconds
+    assert all(0 < t < 5e-3 for t in times), times
+    before = torch.cuda.memory_allocated()
+    d.release({"x_ptr": xb, "y_ptr": yb})
+    assert xb.tensor is None and yb.tensor is None
+    assert torch.cuda.memory_allocated() < before
