@@ -388,6 +388,14 @@ int launch_rows(g950_module* m, const char* op, RowArgs& a, uint32_t dt, const V
   // long: split them (two or more chunks each) instead
   const long long cus = m ? m->cus : 256;
   const bool few = (long long)a.rows * 2 < cus && nvec > kRsChunkVecs;
+  // LayerNorm over many rows of at most 512 vectors: parameters staged in LDS
+  // once per 4-wave workgroup of 8 rows (g950_rw_*) instead of once per
+  // one-row wave
+  const bool ln = !strcmp(op, "layernorm") || !strcmp(op, "lnrow");
+  if (ln && vec && pick && pick->block == 64 && pick->items <= 8 && (long long)a.rows >= 16 * cus) {
+    snprintf(name, sizeof name, "g950_rw_%s_%s_v%d_i%d", op, rr_dtype(dt), v, pick->items);
+    return launch(m, name, (unsigned)((a.rows + 7) / 8), 256u, a, stream);
+  }
   if (pick && !few) {
     snprintf(name, sizeof name, "g950_rr_%s_%s_v%d_i%d_b%d", op, rr_dtype(dt), v, pick->items,
              pick->block);

@@ -218,6 +218,154 @@ __device__ __forceinline__ float lse_finish(float m, float s, bool nan) {
   return m + logf(s);
 }
 
+// The per-row work once the row is in registers as fp32 (v, padding lanes
+// holding the op's identity): the reductions, statistics and y.  pw(i) /
+// pb(i) return lane's packed weight / bias vector i (registers or LDS).
+template <int OP, typename T, int VEC, int ITEMS, int BLOCK, class PW, class PB>
+__device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)[ITEMS][VEC], int tid, int nvec,
+                                           void* yrow, float* scratch, PW pw, PB pb) {
+  using IO = RawIO<T, VEC>;
+  if constexpr (OP == ROW_LOGSUMEXP) {
+    // max ignores NaN (fmaxf), a separate flag carries it
+    float m = -__builtin_huge_valf(), nan = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        m = fmaxf(m, v[i][e]);
+        nan = (v[i][e] != v[i][e]) ? 1.0f : nan;
+      }
+    m = block_reduce<OpMax, BLOCK>(m, scratch);
+    nan = block_reduce<OpMax, BLOCK>(nan, scratch);
+    float s = 0.0f;
+    if (__builtin_fabsf(m) != __builtin_huge_valf()) {
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s += row_exp<T>(v[i][e] - m);  // tail: exp(-inf) = 0
+    }
+    s = block_reduce<OpSum, BLOCK>(s, scratch);
+    if (tid == 0)
+      store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, lse_finish(m, s, nan != 0.0f));
+  } else if constexpr (OP == ROW_SOFTMAX) {
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) m = fmaxf(m, v[i][e]);
+    m = block_reduce<OpMax, BLOCK>(m, scratch);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        v[i][e] = row_exp<T>(v[i][e] - m);  // masked lanes: exp(-inf) = 0
+        s += v[i][e];
+      }
+    s = block_reduce<OpSum, BLOCK>(s, scratch);
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = tid + i * BLOCK;
+      if (j < nvec) {
+        float o[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * inv;
+        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+      }
+    }
+  } else if constexpr (OP == ROW_RMSNORM) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ss = fmaf(v[i][e], v[i][e], ss);
+    ss = block_reduce<OpSum, BLOCK>(ss, scratch);
+    const float inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+    if (tid == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, inv);
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = tid + i * BLOCK;
+      if (j < nvec) {
+        float o[VEC], w[VEC];
+        IO::unpack(pw(i), w);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] * inv) * w[e];
+        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+      }
+    }
+  } else if constexpr (OP == ROW_LNROW) {
+    // both sums in one pass (the reference's E[x^2] - mean^2 form)
+    float s = 0.0f, q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        s += v[i][e];
+        q = fmaf(v[i][e], v[i][e], q);
+      }
+    s = block_reduce<OpSum, BLOCK>(s, scratch);
+    q = block_reduce<OpSum, BLOCK>(q, scratch);
+    const float inv_n = 1.0f / (float)a.cols;
+    const float mean = s * inv_n;
+    const float rstd = 1.0f / sqrtf(q * inv_n - mean * mean + a.eps);
+    if (tid == 0) {
+      store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mean);
+      store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, rstd);
+    }
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = tid + i * BLOCK;
+      if (j < nvec) {
+        float o[VEC], w[VEC], bb[VEC];
+        IO::unpack(pw(i), w);
+        IO::unpack(pb(i), bb);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = lnrow_affine<T>(v[i][e], mean, rstd, w[e], bb[e]);
+        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+      }
+    }
+  } else {  // LayerNorm, centered two-pass from registers
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += v[i][e];
+    s = block_reduce<OpSum, BLOCK>(s, scratch);
+    const float mean = s / (float)a.cols;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = tid + i * BLOCK;
+      if (j < nvec) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          v[i][e] -= mean;
+          q = fmaf(v[i][e], v[i][e], q);
+        }
+      }
+    }
+    q = block_reduce<OpSum, BLOCK>(q, scratch);
+    const float rstd = 1.0f / sqrtf(q / (float)a.cols + a.eps);
+    if (tid == 0) {
+      store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mean);
+      store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, rstd);
+    }
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = tid + i * BLOCK;
+      if (j < nvec) {
+        float o[VEC], w[VEC], bb[VEC];
+        IO::unpack(pw(i), w);
+        IO::unpack(pb(i), bb);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * rstd * w[e] + bb[e];
+        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+      }
+    }
+  }
+}
+
 // Persistent register-resident row kernel.  Workgroup g handles rows
 // g, g + G, g + 2G, ... (the reference's persistent form
 // tl.range(pid, n_rows, num_progs), ops/suite/dev/layer_norm_forward_row.py);
@@ -289,147 +437,75 @@ __device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
       }
     }
 
-    if constexpr (OP == ROW_LOGSUMEXP) {
-      // max ignores NaN (fmaxf), a separate flag carries it
-      float m = -__builtin_huge_valf(), nan = 0.0f;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          m = fmaxf(m, v[i][e]);
-          nan = (v[i][e] != v[i][e]) ? 1.0f : nan;
-        }
-      m = block_reduce<OpMax, BLOCK>(m, scratch);
-      nan = block_reduce<OpMax, BLOCK>(nan, scratch);
-      float s = 0.0f;
-      if (__builtin_fabsf(m) != __builtin_huge_valf()) {
-#pragma unroll
-        for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) s += row_exp<T>(v[i][e] - m);  // tail: exp(-inf) = 0
-      }
-      s = block_reduce<OpSum, BLOCK>(s, scratch);
-      if (tid == 0)
-        store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, lse_finish(m, s, nan != 0.0f));
-    } else if constexpr (OP == ROW_SOFTMAX) {
-      float m = -__builtin_huge_valf();
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) m = fmaxf(m, v[i][e]);
-      m = block_reduce<OpMax, BLOCK>(m, scratch);
-      float s = 0.0f;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          v[i][e] = row_exp<T>(v[i][e] - m);  // masked lanes: exp(-inf) = 0
-          s += v[i][e];
-        }
-      s = block_reduce<OpSum, BLOCK>(s, scratch);
-      const float inv = 1.0f / s;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i) {
-        const int j = tid + i * BLOCK;
-        if (j < nvec) {
-          float o[VEC];
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * inv;
-          store_vec<T, VEC>(yrow, (long long)j * VEC, o);
-        }
-      }
-    } else if constexpr (OP == ROW_RMSNORM) {
-      float ss = 0.0f;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) ss = fmaf(v[i][e], v[i][e], ss);
-      ss = block_reduce<OpSum, BLOCK>(ss, scratch);
-      const float inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
-      if (tid == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, inv);
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i) {
-        const int j = tid + i * BLOCK;
-        if (j < nvec) {
-          float o[VEC], w[VEC];
-          IO::unpack(wr[i], w);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] * inv) * w[e];
-          store_vec<T, VEC>(yrow, (long long)j * VEC, o);
-        }
-      }
-    } else if constexpr (OP == ROW_LNROW) {
-      // both sums in one pass (the reference's E[x^2] - mean^2 form)
-      float s = 0.0f, q = 0.0f;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          s += v[i][e];
-          q = fmaf(v[i][e], v[i][e], q);
-        }
-      s = block_reduce<OpSum, BLOCK>(s, scratch);
-      q = block_reduce<OpSum, BLOCK>(q, scratch);
-      const float inv_n = 1.0f / (float)a.cols;
-      const float mean = s * inv_n;
-      const float rstd = 1.0f / sqrtf(q * inv_n - mean * mean + a.eps);
-      if (tid == 0) {
-        store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mean);
-        store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, rstd);
-      }
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i) {
-        const int j = tid + i * BLOCK;
-        if (j < nvec) {
-          float o[VEC], w[VEC], bb[VEC];
-          IO::unpack(wr[i], w);
-          IO::unpack(br[i], bb);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) o[e] = lnrow_affine<T>(v[i][e], mean, rstd, w[e], bb[e]);
-          store_vec<T, VEC>(yrow, (long long)j * VEC, o);
-        }
-      }
-    } else {  // LayerNorm, centered two-pass from registers
-      float s = 0.0f;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) s += v[i][e];
-      s = block_reduce<OpSum, BLOCK>(s, scratch);
-      const float mean = s / (float)a.cols;
-      float q = 0.0f;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i) {
-        const int j = tid + i * BLOCK;
-        if (j < nvec) {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            v[i][e] -= mean;
-            q = fmaf(v[i][e], v[i][e], q);
-          }
-        }
-      }
-      q = block_reduce<OpSum, BLOCK>(q, scratch);
-      const float rstd = 1.0f / sqrtf(q / (float)a.cols + a.eps);
-      if (tid == 0) {
-        store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, mean);
-        store_from_f32(a.stat1, (long long)row * a.stat1_stride, a.stat_dtype, rstd);
-      }
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i) {
-        const int j = tid + i * BLOCK;
-        if (j < nvec) {
-          float o[VEC], w[VEC], bb[VEC];
-          IO::unpack(wr[i], w);
-          IO::unpack(br[i], bb);
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * rstd * w[e] + bb[e];
-          store_vec<T, VEC>(yrow, (long long)j * VEC, o);
-        }
-      }
-    }
+    row_finish<OP, T, VEC, ITEMS, BLOCK>(a, row, v, tid, nvec, yrow, scratch, [&](int i) { return wr[i]; },
+                                         [&](int i) { return br[i]; });
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) cur[i] = nxt[i];
+  }
+}
+
+// Row kernel for many rows of an op with per-column parameters, each row
+// short enough for one wavefront: the parameters are staged in LDS once per
+// workgroup of WAVES waves instead of once per wave, and each wave reduces
+// RPW rows (its first row's loads are in flight while the parameters are
+// staged, its next row's while the current one is reduced).  Workgroup g
+// takes rows g*WAVES*RPW + wave + k*WAVES.  Measured on MI355X for C2
+// LayerNorm (bf16 [8191, 3000]): 19.2 us against 20.2 for the one-row
+// workgroups with parameters in registers (146 -> 107 VGPRs, and one
+// parameter fetch per 8 rows instead of per row).
+template <int OP, typename T, int VEC, int ITEMS, int WAVES, int RPW>
+__device__ __forceinline__ void rw_body(const RowArgs& a) {
+  using IO = RawIO<T, VEC>;
+  using R = typename IO::type;
+  __shared__ R wl[row_has_w(OP) ? ITEMS * 64 : 1];
+  __shared__ R bl[row_has_b(OP) ? ITEMS * 64 : 1];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nvec = a.cols / VEC;  // host guarantees cols % VEC == 0 and nvec <= ITEMS * 64
+  const long long xstride = a.x_row * (long long)sizeof(T);
+  const long long ystride = a.y_row * (long long)sizeof(T);
+  const int row0 = blockIdx.x * WAVES * RPW + wave;
+  R cur[ITEMS], nxt[ITEMS];
+  auto load = [&](int row, R (&dst)[ITEMS]) {
+    const char* xrow = (const char*)a.x + (long long)row * xstride;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = lane + i * 64;
+      if (j < nvec) dst[i] = IO::load(xrow, (long long)j * VEC);
+    }
+  };
+  if (row0 < a.rows) load(row0, cur);
+  if constexpr (row_has_w(OP)) {
+    for (int j = threadIdx.x; j < nvec; j += WAVES * 64) {
+      wl[j] = IO::load_cached(a.w, (long long)j * VEC);
+      if constexpr (row_has_b(OP)) bl[j] = IO::load_cached(a.b, (long long)j * VEC);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int row = row0 + k * WAVES;
+    if (row >= a.rows) break;
+    if (k + 1 < RPW && row + WAVES < a.rows) load(row + WAVES, nxt);
+    float v[ITEMS][VEC];
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = lane + i * 64;
+      if (j < nvec) {
+        IO::unpack(cur[i], v[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          v[i][e] = (OP == ROW_SOFTMAX || OP == ROW_LOGSUMEXP) ? -__builtin_huge_valf() : 0.0f;
+      }
+    }
+    row_finish<OP, T, VEC, ITEMS, 64>(a, row, v, lane, nvec, (char*)a.y + (long long)row * ystride, nullptr,
+                                      [&](int i) { return wl[row_has_w(OP) ? lane + i * 64 : 0]; },
+                                      [&](int i) { return bl[row_has_b(OP) ? lane + i * 64 : 0]; });
+    if (k + 1 < RPW) {
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) cur[i] = nxt[i];
+    }
   }
 }
 
@@ -728,6 +804,26 @@ G950_RR_ALL(rmsnorm, g950::ROW_RMSNORM)
 G950_RR_ALL(layernorm, g950::ROW_LAYERNORM)
 G950_RR_ALL(logsumexp, g950::ROW_LOGSUMEXP)
 G950_RR_ALL(lnrow, g950::ROW_LNROW)
+
+// Parameter rows in LDS (rw_body): g950_rw_<op>_<dtype>_v<VEC>_i<ITEMS>,
+// 4 waves x 2 rows per workgroup, vector forms only.
+#define G950_RW(OPNAME, OP, TNAME, T, VEC, ITEMS)                                        \
+  extern "C" __global__ __launch_bounds__(256) void                                      \
+      g950_rw_##OPNAME##_##TNAME##_v##VEC##_i##ITEMS(const g950::RowArgs a) {            \
+    g950::rw_body<OP, T, VEC, ITEMS, 4, 2>(a);                                           \
+  }
+#define G950_RW_SET(OPNAME, OP, TNAME, T, VEC) \
+  G950_RW(OPNAME, OP, TNAME, T, VEC, 1)        \
+  G950_RW(OPNAME, OP, TNAME, T, VEC, 2)        \
+  G950_RW(OPNAME, OP, TNAME, T, VEC, 4)        \
+  G950_RW(OPNAME, OP, TNAME, T, VEC, 6)        \
+  G950_RW(OPNAME, OP, TNAME, T, VEC, 8)
+#define G950_RW_ALL(OPNAME, OP)                  \
+  G950_RW_SET(OPNAME, OP, f32, float, 4)         \
+  G950_RW_SET(OPNAME, OP, bf16, g950::bf16_t, 8) \
+  G950_RW_SET(OPNAME, OP, f16, g950::f16_t, 8)
+G950_RW_ALL(layernorm, g950::ROW_LAYERNORM)
+G950_RW_ALL(lnrow, g950::ROW_LNROW)
 
 // ------------------------------------------------------------- stream copy
 // y = x for n 16-byte vectors, grid-stride, nontemporal loads and stores --

@@ -315,7 +315,12 @@ def test_rms_and_layernorm_contracts():
           .view([8191, 3000], rt.DT_BF16).view([8191, 3000], rt.DT_BF16, output=True))
     rc, name, err = validate(rt.OP_LAYERNORM, ln, [3000, np.float32(1e-5), 3000])
     assert rc == 0, err
-    assert name == "g950_rr_layernorm_bf16_v8_i6_b64"
+    assert name == "g950_rw_layernorm_bf16_v8_i6"    # many rows: parameters in LDS, 8 rows per workgroup
+    few = (Args().view([3000], rt.DT_BF16).view([64], rt.DT_F32, output=True)
+           .view([64], rt.DT_F32, output=True).view([3000], rt.DT_BF16)
+           .view([64, 3000], rt.DT_BF16).view([64, 3000], rt.DT_BF16, output=True))
+    rc, name, err = validate(rt.OP_LAYERNORM, few, [3000, np.float32(1e-5), 3000])
+    assert rc == 0 and name == "g950_rr_layernorm_bf16_v8_i6_b64", err
     assert validate(rt.OP_LAYERNORM, ln, [3000, np.float32(1e-5), 3001])[0] == rt.USAGE
 
 
@@ -446,7 +451,7 @@ def lnrow_scalars(rows, cols, xs=None, ys=None, ms=1, rs=1, eps=1e-5):
 def test_layernorm_row_contract():
     for rows, cols, dt, kernel in ((3, 16, rt.DT_F32, "g950_rr_lnrow_f32_v4_i1_b64"),
                                    (5, 128, rt.DT_BF16, "g950_rr_lnrow_bf16_v8_i1_b64"),
-                                   (8191, 3000, rt.DT_BF16, "g950_rr_lnrow_bf16_v8_i6_b64"),
+                                   (8191, 3000, rt.DT_BF16, "g950_rw_lnrow_bf16_v8_i6"),
                                    (7, 67, rt.DT_F16, "g950_rr_lnrow_f16_v1_i2_b64")):
         rc, name, err = validate(rt.OP_LAYERNORM_ROW, lnrow_args(rows, cols, dt), lnrow_scalars(rows, cols))
         assert rc == 0 and name == kernel, err

@@ -86,6 +86,36 @@ def test_layernorm_softmax_bf16_masked_tail(rows, cols):
 
 
 @pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("rows,cols", [(4099, 64), (4096, 1000), (4097, 2048), (4100, 3000), (4096, 4096)])
+def test_layernorm_parameters_in_lds(rows, cols, dt):
+    """Many rows of at most 512 vectors: the LDS-parameter kernels
+    (g950_rw_*, every row width class 1..8 vectors per lane) for both
+    LayerNorm forms, against the float64 oracle (fp32 <= 1e-5 relative,
+    16-bit <= 1e-2); the rows past the last full 8-row workgroup included."""
+    c = inputs.config2(rows, cols)
+    x = dev(c["x"], dt)
+    g, b = dev(c["gamma"], dt), dev(c["beta"], dt)
+    xr, gr, br = host(x), host(g), host(b)
+    y, mean, rstd = ops.layernorm(x, g, b, c["eps"], sync=True)
+    vec = 4 if dt == "float32" else 8
+    if (cols // vec) <= 512 and cols % vec == 0:
+        assert rt.module().last_kernel.startswith("g950_rw_layernorm_")
+    ey, em, es = ref.layernorm(xr, gr, br, c["eps"])
+    bar = 1e-5 if dt == "float32" else 1e-2
+    close(host(y), ey, bar, bar)
+    close(host(mean), em, 1e-5, 1e-6)
+    assert rel_err(host(rstd), es, 1e-30) <= 1e-5
+    yl = torch.empty_like(x)
+    ml = torch.empty(rows, device=DEV)
+    sl = torch.empty(rows, device=DEV)
+    ops.layer_norm_forward_row(yl, cols, x, cols, g, b, ml, 1, sl, 1, rows, cols, c["eps"], sync=True)
+    ey, em, es = ref.layernorm_row(xr, gr, br, c["eps"])
+    close(host(yl), ey, bar, bar)
+    close(host(ml), em, 1e-5, 1e-6)
+    assert rel_err(host(sl), es, 1e-30) <= 1e-5
+
+
+@pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
 @pytest.mark.parametrize("rows,cols", [(4, 16), (4, 97), (64, 1024), (8191, 3000), (2, 100000)])
 def test_logsumexp(rows, cols, dt):
     """ops/suite/perf/logsumexp.py: x ~ 3 N(0,1), expected from the inputs as
