@@ -348,6 +348,22 @@ def suite(torch, ops, cpu=True):
             del ab, btb, b32, cbuf, b64, a64
         del c
 
+    # the reference matmul's own layout: row-major B [K, N] (ops/suite/perf/matmul.py:33);
+    # one K-contiguous copy of B, then the MFMA GEMM (both launches timed)
+    c = inputs.config3(8192, 8192, 8192)
+    a = torch.from_numpy(c["a"]).to(dev).to(torch.bfloat16)
+    b = torch.from_numpy(np.ascontiguousarray(c["bt"].T)).to(dev).to(torch.bfloat16)
+    del c
+    y = torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)
+    call = ops.matmul_kernel(a, b, y, 8192, 8192, 8192, prepare=True)
+    ms = event_time(torch, lambda i: call(), 20, 3, warm_s=0.5)
+    tf = 2.0 * 8192 ** 3 / (ms * 1e-3) / 1e12
+    out.append({"config": "F gemm bf16 8192^3, row-major B (reference layout)",
+                "kernel": "g950_transpose_b16 + " + call.kernel, "us": round(ms * 1e3, 1), "value": round(tf, 1),
+                "unit": "TFLOP/s", "bound": "mfma", "frac": round(tf / BF16_PEAK_TFS, 4)})
+    del a, b, y
+    torch.cuda.empty_cache()
+
     # C4: causal GQA attention bf16 (4, 32/8, 4096, 128) with LSE
     c = inputs.config4()
     bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731

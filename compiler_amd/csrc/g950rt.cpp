@@ -616,12 +616,24 @@ int gemm_tiles(GemmArgs& g) {
   return (int)(tm * tn);
 }
 
-// A[M,K] and B[K,N] both K-contiguous, 16-byte rows, K a whole number of
-// 128-byte slabs: the MFMA kernel applies.
+// A[M,K] and B[K,N] both K-contiguous with 16-byte rows (K a whole number of
+// 16-byte chunks): the MFMA kernels apply -- the plain ones when K is a whole
+// number of 128-byte slabs, else the _kt ones (gemm_ktail).
 bool gemm_fast_ok(const View& a, const View& b, int K, int esz) {
-  return a.stride[1] == 1 && b.stride[0] == 1 && (K * esz) % 128 == 0 && K > 0 &&
+  return a.stride[1] == 1 && b.stride[0] == 1 && (K * esz) % 16 == 0 && K > 0 &&
          aligned16(a.addr()) && aligned16(b.addr()) && (a.stride[0] * esz) % 16 == 0 &&
          (b.stride[1] * esz) % 16 == 0 && a.shape[0] > 0 && b.shape[1] > 0;
+}
+
+bool gemm_ktail(int K, int esz) { return (K * esz) % 128 != 0; }
+
+// Row-major B[K,N] (N-contiguous, the reference matmul's layout,
+// ops/suite/perf/matmul.py:33) with A K-contiguous: B is copied once into a
+// K-contiguous Bt in the workspace (g950_transpose_b16) for the MFMA kernels.
+bool gemm_rowb_ok(const View& a, const View& b, int K, int N, int esz) {
+  return esz == 2 && a.stride[1] == 1 && b.stride[1] == 1 && K % 8 == 0 && N % 8 == 0 && K > 0 &&
+         aligned16(a.addr()) && aligned16(b.addr()) &&
+         (a.stride[0] * esz) % 16 == 0 && (b.stride[0] * esz) % 16 == 0 && a.shape[0] > 0 && N > 0;
 }
 
 int gemm_views(const View& a, const View& b, const View& y, const g950_scalar* sc, long long& M,
@@ -654,13 +666,34 @@ int op_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g95
   g.c_s0 = y.stride[0]; g.c_s1 = y.stride[1];
   if (M == 0 || N == 0) return launch(m, "g950_gemm_general", 0, 256, g, stream);
   const bool same16 = a.v->dtype == b.v->dtype && is_float16ish(a.v->dtype);
-  if (same16 && gemm_fast_ok(a, b, (int)K, 2) && y.stride[1] == 1 && aligned16(y.addr())) {
+  const bool out16 = y.stride[1] == 1 && aligned16(y.addr());
+  const char* mfma_name = a.v->dtype == G950_DTYPE_BFLOAT16
+                              ? (gemm_ktail((int)K, 2) ? "g950_gemm_bf16_256x256_kt" : "g950_gemm_bf16_256x256")
+                              : (gemm_ktail((int)K, 2) ? "g950_gemm_f16_256x256_kt" : "g950_gemm_f16_256x256");
+  if (same16 && gemm_fast_ok(a, b, (int)K, 2) && out16) {
     g.a_s0 = a.stride[0];
     g.b_s0 = b.stride[1];  // Bt row (n) stride
     const int tiles = gemm_tiles(g);
     if (tiles < 0) return fail(G950_USAGE, "matmul: too many tiles");
-    return launch(m, a.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_gemm_bf16_256x256" : "g950_gemm_f16_256x256",
-                  (unsigned)tiles, 512u, g, stream);
+    return launch(m, mfma_name, (unsigned)tiles, 512u, g, stream);
+  }
+  void* bt = nullptr;
+  const size_t bt_bytes = (size_t)N * (size_t)K * 2;
+  bool rowb = same16 && out16 && gemm_rowb_ok(a, b, (int)K, (int)N, 2) && bt_bytes <= ((size_t)1 << 31);
+  // without the workspace for the copy, the general kernel serves the call
+  if (rowb && m && workspace(m, stream, bt_bytes, &bt) != G950_OK) rowb = false;
+  if (rowb) {
+    GemmArgs t{};
+    t.b = g.b; t.b_s0 = b.stride[0]; t.c = bt; t.N = (int)N; t.K = (int)K;
+    const long long tblocks = ((K + 63) / 64) * ((N + 63) / 64);
+    if (tblocks > 0x7FFFFFFF) return fail(G950_USAGE, "matmul: too many tiles");
+    if (int rc = launch(m, "g950_transpose_b16", (unsigned)tblocks, 256u, t, stream)) return rc;
+    g.b = bt;
+    g.a_s0 = a.stride[0];
+    g.b_s0 = K;
+    const int tiles = gemm_tiles(g);
+    if (tiles < 0) return fail(G950_USAGE, "matmul: too many tiles");
+    return launch(m, mfma_name, (unsigned)tiles, 512u, g, stream);
   }
   g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
   g.b_s0 = b.stride[0]; g.b_s1 = b.stride[1];
@@ -715,13 +748,16 @@ int op_matmul_i8(g950_module* m, const g950_view* views, uint32_t nviews, const 
   }
   if (M == 0 || N == 0) return launch(m, "g950_gemm_general_i8", 0, 256, g, stream);
   const bool out_ok = dequant ? (y.stride[1] == 1 && aligned16(y.addr())) : aligned16(y.addr());
-  if (gemm_fast_ok(a, b, (int)K, 1) && out_ok) {
+  // an unsigned operand's flipped bytes would read the zero tail as -128:
+  // the signedness variants need whole 128-byte K slabs
+  if (gemm_fast_ok(a, b, (int)K, 1) && out_ok && (umask == 0 || !gemm_ktail((int)K, 1))) {
     g.a_s0 = a.stride[0];
     g.b_s0 = b.stride[1];
     const int tiles = gemm_tiles(g);
     if (tiles < 0) return fail(G950_USAGE, "matmul_i8: too many tiles");
     static const char* const names[4] = {"g950_gemm_i8_256x256", "g950_gemm_u8s8_256x256",
                                          "g950_gemm_s8u8_256x256", "g950_gemm_u8u8_256x256"};
+    const bool ktail = gemm_ktail((int)K, 1);
     if (umask) {
       // the MFMA multiplies u - 128 for an unsigned operand: first the sums
       // over k its correction needs (A's rows if B is unsigned, B's columns
@@ -742,7 +778,7 @@ int op_matmul_i8(g950_module* m, const g950_view* views, uint32_t nviews, const 
       g.csum = (umask & 1) ? sa.out + sa.a_rows : nullptr;
       if (int rc = launch(m, "g950_i8_sums", (unsigned)((rows + 3) / 4), 256u, sa, stream)) return rc;
     }
-    return launch(m, names[umask], (unsigned)tiles, 512u, g, stream);
+    return launch(m, ktail ? "g950_gemm_i8_256x256_kt" : names[umask], (unsigned)tiles, 512u, g, stream);
   }
   if (!dequant && N > 1 && y.stride[1] != 1) return fail(G950_USAGE, "matmul_i8: c_ptr layout");
   g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];

@@ -46,6 +46,11 @@ enum GemmMode : int { GEMM_BF16 = 0, GEMM_F16 = 1, GEMM_I8 = 2 };
 constexpr int BM = 256, BN = 256;  // workgroup tile
 constexpr int SLAB = 128;          // bytes of K per row per LDS stage (two stages)
 
+// 128 zero bytes: the DMA source of every 16-byte chunk past K in the last
+// (partial) K slab, so the tail multiplies zeros instead of reading past a
+// row (K % 64 != 0 kernels only)
+__device__ __attribute__((aligned(128))) const uint32_t g950_zero_line[32] = {};
+
 // Map the linear workgroup id to a (tile_m, tile_n): XCD-contiguous, then
 // grouped by 4 tile-rows.
 __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -167,7 +172,7 @@ __device__ __forceinline__ void mfma_step(const u32x4& bfrag, const u32x4& afrag
 // UMASK (int8): bit 0 A unsigned, bit 1 B unsigned.  An unsigned operand's
 // bytes are flipped (XOR 0x80: u - 128, a signed int8) as its fragments enter
 // the MFMA; the epilogue adds the exact correction.
-template <int MODE, int WM, int WN, int UMASK = 0>
+template <int MODE, int WM, int WN, int UMASK = 0, bool KTAIL = false>
 __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   constexpr int NW = WM * WN;
   constexpr int FM = BM / WM / 32;
@@ -193,7 +198,10 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   const char* bbase = (const char*)p.b + (long long)n0 * ldb_b;
   const int a_lim = p.M - 1 - m0;
   const int b_lim = p.N - 1 - n0;
-  const int kslabs = (p.K * ES) / SLAB;
+  // KTAIL: K need only be a whole number of 16-byte chunks; the last slab's
+  // chunks past K come from g950_zero_line
+  const int kbytes = p.K * ES;
+  const int kslabs = KTAIL ? (kbytes + SLAB - 1) / SLAB : kbytes / SLAB;
   const int last = kslabs - 1;
 
   f32x16 accf[FM][FN];
@@ -224,6 +232,8 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
       const int chunk = dslot ^ ((row >> 1) & 7);
       const char* src = (is_a ? abase : bbase) + (long long)grow * (is_a ? lda_b : ldb_b) + kb +
                         chunk * 16;
+      if constexpr (KTAIL)
+        if (kb + chunk * 16 >= kbytes) src = (const char*)g950_zero_line;
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                        (__attribute__((address_space(3))) void*)(st + rg * 1024),
                                        16, 0, 0);
@@ -316,6 +326,40 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   gemm_epilogue<MODE, FM, FN, UMASK>(p, accf, acci, m0 + wm * (BM / WM), n0 + wn * (BN / WN), r, g);
+}
+
+// Bt[n][k] = B[k][n] for 16-bit elements: B [K, N] row-major with row stride
+// b_s0 elements (16-byte aligned rows, N % 8 == 0), Bt contiguous [N, K] at
+// p.c (K % 8 == 0).  64 x 64 tiles through LDS, one 32-bit slot per element
+// with a 65-slot row pitch, so the column reads of the transposition and the
+// row writes are both conflict-free; 16-byte loads and stores.
+__device__ __forceinline__ void transpose16_body(const GemmArgs& p) {
+  __shared__ uint32_t t[64][65];
+  const int tiles_n = (p.N + 63) / 64;
+  const int k0 = (blockIdx.x / tiles_n) * 64, n0 = (blockIdx.x % tiles_n) * 64;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = threadIdx.x + 256 * i, k = c >> 3, n8 = (c & 7) * 8;
+    if (k0 + k < p.K && n0 + n8 < p.N) {
+      const u32x4 w = *(const u32x4*)((const uint16_t*)p.b + (long long)(k0 + k) * p.b_s0 + n0 + n8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        t[k][n8 + 2 * e] = w[e] & 0xFFFFu;
+        t[k][n8 + 2 * e + 1] = w[e] >> 16;
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = threadIdx.x + 256 * i, n = c >> 3, k8 = (c & 7) * 8;
+    if (n0 + n < p.N && k0 + k8 < p.K) {
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = t[k8 + 2 * e][n] | (t[k8 + 2 * e + 1][n] << 16);
+      *(u32x4*)((uint16_t*)p.c + (long long)(n0 + n) * p.K + k0 + k8) = w;
+    }
+  }
 }
 
 // Row sums over k of int8 / uint8 operands (I8SumArgs), modulo 2^32: one wave
@@ -764,18 +808,25 @@ __device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
 
 }  // namespace g950
 
-#define G950_GEMM_MFMA(NAME, MODE, WM, WN, UMASK)                                            \
+#define G950_GEMM_MFMA(NAME, MODE, WM, WN, UMASK, KT)                                        \
   extern "C" __global__ __launch_bounds__(WM * WN * 64) void NAME(const g950::GemmArgs p) {  \
-    g950::gemm_mfma_body<MODE, WM, WN, UMASK>(p);                                          \
+    g950::gemm_mfma_body<MODE, WM, WN, UMASK, KT>(p);                                      \
   }
-G950_GEMM_MFMA(g950_gemm_bf16_256x256, g950::GEMM_BF16, 4, 2, 0)
-G950_GEMM_MFMA(g950_gemm_f16_256x256, g950::GEMM_F16, 4, 2, 0)
-G950_GEMM_MFMA(g950_gemm_i8_256x256, g950::GEMM_I8, 4, 2, 0)
+G950_GEMM_MFMA(g950_gemm_bf16_256x256, g950::GEMM_BF16, 4, 2, 0, false)
+G950_GEMM_MFMA(g950_gemm_f16_256x256, g950::GEMM_F16, 4, 2, 0, false)
+G950_GEMM_MFMA(g950_gemm_i8_256x256, g950::GEMM_I8, 4, 2, 0, false)
+// K not a whole 128-byte slab (16-byte rows): the last slab's tail reads zeros
+G950_GEMM_MFMA(g950_gemm_bf16_256x256_kt, g950::GEMM_BF16, 4, 2, 0, true)
+G950_GEMM_MFMA(g950_gemm_f16_256x256_kt, g950::GEMM_F16, 4, 2, 0, true)
+G950_GEMM_MFMA(g950_gemm_i8_256x256_kt, g950::GEMM_I8, 4, 2, 0, true)
+extern "C" __global__ __launch_bounds__(256) void g950_transpose_b16(const g950::GemmArgs p) {
+  g950::transpose16_body(p);
+}
 // int8 signedness variants of the reference family (a100c/plan/tiles.py:121-126):
 // uint8 A x int8 B, int8 A x uint8 B, uint8 x uint8
-G950_GEMM_MFMA(g950_gemm_u8s8_256x256, g950::GEMM_I8, 4, 2, 1)
-G950_GEMM_MFMA(g950_gemm_s8u8_256x256, g950::GEMM_I8, 4, 2, 2)
-G950_GEMM_MFMA(g950_gemm_u8u8_256x256, g950::GEMM_I8, 4, 2, 3)
+G950_GEMM_MFMA(g950_gemm_u8s8_256x256, g950::GEMM_I8, 4, 2, 1, false)
+G950_GEMM_MFMA(g950_gemm_s8u8_256x256, g950::GEMM_I8, 4, 2, 2, false)
+G950_GEMM_MFMA(g950_gemm_u8u8_256x256, g950::GEMM_I8, 4, 2, 3, false)
 extern "C" __global__ __launch_bounds__(256) void g950_i8_sums(const g950::I8SumArgs p) {
   g950::i8_sums_body(p);
 }

@@ -336,14 +336,33 @@ def gemm_args(m, n, k, dtype, col_major_b=True, out=rt.DT_BF16):
 @pytest.mark.parametrize("m,n,k,colb,kernel", [
     (8192, 8192, 8192, True, "g950_gemm_bf16_256x256"),
     (4097, 11008, 4096, True, "g950_gemm_bf16_256x256"),
-    (128, 128, 128, False, "g950_gemm_general"),   # row-major B (the corpus fixtures)
-    (64, 64, 96, True, "g950_gemm_general"),       # K not a whole 64-element (128-byte) slab
-    (33, 65, 64, True, "g950_gemm_bf16_256x256"),  # a single slab
+    (8192, 8192, 8192, False, "g950_gemm_bf16_256x256"),  # row-major B (matmul.py:33): copied K-contiguous
+    (128, 128, 128, False, "g950_gemm_bf16_256x256"),   # the corpus fixtures' layout
+    (8, 24, 32, False, "g950_gemm_bf16_256x256_kt"),     # matmul-tail fixture shape [8,32,24]: K tail
+    (64, 64, 96, True, "g950_gemm_bf16_256x256_kt"),    # K not a whole 64-element (128-byte) slab
+    (64, 64, 100, True, "g950_gemm_general"),           # K rows not 16-byte multiples
+    (64, 60, 64, False, "g950_gemm_general"),           # row-major B rows not 16-byte multiples
+    (33, 65, 64, True, "g950_gemm_bf16_256x256"),       # a single slab
 ])
 def test_matmul_selection(m, n, k, colb, kernel):
     rc, name, err = validate(rt.OP_MATMUL, gemm_args(m, n, k, rt.DT_BF16, colb), [k, m, n])
     assert rc == 0, err
     assert name == kernel
+
+
+def test_matmul_fp32_and_int8_tails():
+    # fp32 operands stay on the general kernel; int8 with a K tail takes the _kt kernel
+    rc, name, err = validate(rt.OP_MATMUL, gemm_args(128, 128, 128, rt.DT_F32, False, out=rt.DT_F32), [128, 128, 128])
+    assert rc == 0 and name == "g950_gemm_general", err
+    c = (Args().view([300, 208], rt.DT_INT8).view([208, 200], rt.DT_INT8, strides=[1, 208])
+         .view([300, 200], rt.DT_INT32, output=True))
+    rc, name, err = validate(rt.OP_MATMUL_I8, c, [208, 300, 200])
+    assert rc == 0 and name == "g950_gemm_i8_256x256_kt", err
+    # an unsigned operand with a K tail: the zero tail would flip to -128, so the general kernel
+    c = (Args().view([300, 208], rt.DT_UINT8).view([208, 200], rt.DT_INT8, strides=[1, 208])
+         .view([300, 200], rt.DT_INT32, output=True))
+    rc, name, err = validate(rt.OP_MATMUL_I8, c, [208, 300, 200])
+    assert rc == 0 and name == "g950_gemm_general_i8", err
 
 
 def test_matmul_refusals():

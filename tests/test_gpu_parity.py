@@ -426,6 +426,57 @@ def test_gemm_f16_and_general_paths():
     close(host(out), expect, 1e-3, 1e-3)
 
 
+@pytest.mark.parametrize("dt", ["bfloat16", "float16"])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (300, 264, 256), (513, 1000, 1024), (1, 8, 64), (8, 24, 32),
+                                   (257, 136, 200), (130, 72, 8), (4096, 4096, 4096)])
+def test_gemm_row_major_b_on_mfma(m, n, k, dt):
+    """The reference matmul's own layout (row-major B, ops/suite/perf/matmul.py:33):
+    B copied once K-contiguous, then the MFMA kernel (the _kt form when K is not
+    a whole 64-element slab: the last slab's tail multiplies zeros).  Bar 2e-2
+    (bf16) / 1e-2 (fp16) against float64; rows sampled at 4096^3."""
+    c = inputs.config3(m, n, k)
+    a, b = dev(c["a"], dt), dev(np.ascontiguousarray(c["bt"].T), dt)   # b: [K, N] row-major
+    y = torch.zeros((m, n), dtype=TD[dt], device=DEV)
+    ops.matmul_kernel(a, b, y, m, n, k, sync=True)
+    short = "bf16" if dt == "bfloat16" else "f16"
+    assert rt.module().last_kernel == f"g950_gemm_{short}_256x256" + ("_kt" if k % 64 else "")
+    rows = np.arange(m) if m <= 1024 else tile_rows(m, 3)
+    bar = 2e-2 if dt == "bfloat16" else 1e-2
+    close(host(y)[rows], ref.matmul(host(a)[rows], host(b)), bar, bar)
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 72), (300, 260, 200), (64, 64, 8), (1000, 513, 4104)])
+def test_gemm_k_tail_k_contiguous(m, n, k):
+    """K-contiguous operands with K a multiple of 8 but not of 64: the _kt
+    kernel's zero-filled last slab; the guard columns of a strided output and
+    a run-twice bit identity."""
+    c = inputs.config3(m, n, k)
+    a, bt = dev(c["a"], "bfloat16"), dev(c["bt"], "bfloat16")
+    out = torch.full((m, n + 8), -7.0, dtype=torch.bfloat16, device=DEV)
+    y = out[:, :n]
+    ops.matmul_kernel(a, bt.t(), y, m, n, k, sync=True)
+    assert rt.module().last_kernel == "g950_gemm_bf16_256x256_kt"
+    close(host(y), ref.matmul(c["a"], c["bt"].T), 2e-2, 2e-2)
+    assert bool((out[:, n:] == -7.0).all())
+    y2 = torch.empty_like(y)
+    ops.matmul_kernel(a, bt.t(), y2, m, n, k, sync=True)
+    assert torch.equal(y.contiguous(), y2)
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 200, 208), (65, 33, 48), (4096, 8192, 8176)])
+def test_int8_k_tail_exact(m, n, k):
+    """Signed int8 with K a multiple of 16 but not of 128: the _kt kernel,
+    int32 bit-exact (zeros add nothing)."""
+    c = inputs.config5(m, n, k)
+    a, bt = torch.from_numpy(c["a"]).to(DEV), torch.from_numpy(c["bt"]).to(DEV)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    ops.matmul_i8_kernel(a, bt.t(), acc, m, n, k, sync=True)
+    assert rt.module().last_kernel == "g950_gemm_i8_256x256_kt"
+    rows = np.arange(m) if m <= 512 else tile_rows(m, 13)
+    got = acc[torch.from_numpy(rows).to(DEV)].cpu().numpy()
+    assert np.array_equal(got, ref.matmul_i8(c["a"][rows], c["bt"].T))
+
+
 @pytest.mark.parametrize("case", golden_cases("matmul"))
 def test_matmul_reference_fixture(case):
     b = load(case)
@@ -434,9 +485,12 @@ def test_matmul_reference_fixture(case):
     m, k = a.shape
     n = bb.shape[1]
     rtol, atol = ref.TOLERANCES[dt]
-    # the fixture layout (row-major B) ...
+    # the fixture layout (row-major B): the MFMA kernel for 16-bit operands
     y = torch.zeros((m, n), dtype=TD[dt], device=DEV)
     ops.matmul_kernel(dev(a, dt), dev(bb, dt), y, m, n, k, sync=True)
+    if dt != "float32" and k % 8 == 0 and n % 8 == 0:
+        assert rt.module().last_kernel.startswith("g950_gemm_"), rt.module().last_kernel
+        assert "general" not in rt.module().last_kernel
     close(host(y), values(b, "y_ptr"), rtol, atol)
     # ... and the same values column-major, which takes the MFMA kernel when K allows
     if dt != "float32":
