@@ -37,6 +37,7 @@ METRIC = "GEMM/attn TFLOP/s + norm/softmax HBM GB/s vs roofline, 1×MI355X"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFS = 2516.6   # dense, 256 CU x 2.4 GHz x 4096 FLOP/clk
 INT8_PEAK_TOPS = 5033.2  # dense, 8192 OP/clk/CU
+FP32_PEAK_TFS = 157.3    # dense fp32 MFMA
 ROTATE = 4
 
 
@@ -361,6 +362,21 @@ def suite(torch, ops, cpu=True):
     out.append({"config": "F gemm bf16 8192^3, row-major B (reference layout)",
                 "kernel": "g950_transpose_b16 + " + call.kernel, "us": round(ms * 1e3, 1), "value": round(tf, 1),
                 "unit": "TFLOP/s", "bound": "mfma", "frac": round(tf / BF16_PEAK_TFS, 4)})
+    del a, b, y
+    torch.cuda.empty_cache()
+
+    # fp32 operands (the matmul corpus's base dtype) on the fp32 MFMA kernel
+    g32 = torch.Generator(device=dev)
+    g32.manual_seed(5)
+    a = torch.randn((4096, 4096), device=dev, generator=g32)
+    b = torch.randn((4096, 4096), device=dev, generator=g32)
+    y = torch.empty((4096, 4096), device=dev)
+    call = ops.matmul_kernel(a, b, y, 4096, 4096, 4096, prepare=True)
+    ms = event_time(torch, lambda i: call(), 10, 2, warm_s=0.3)
+    tf = 2.0 * 4096 ** 3 / (ms * 1e-3) / 1e12
+    out.append({"config": "F gemm fp32 4096^3, row-major B", "kernel": "g950_transpose_b32 + " + call.kernel,
+                "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
+                "frac": round(tf / FP32_PEAK_TFS, 4)})
     del a, b, y
     torch.cuda.empty_cache()
 

@@ -631,8 +631,9 @@ bool gemm_ktail(int K, int esz) { return (K * esz) % 128 != 0; }
 // ops/suite/perf/matmul.py:33) with A K-contiguous: B is copied once into a
 // K-contiguous Bt in the workspace (g950_transpose_b16) for the MFMA kernels.
 bool gemm_rowb_ok(const View& a, const View& b, int K, int N, int esz) {
-  return esz == 2 && a.stride[1] == 1 && b.stride[1] == 1 && K % 8 == 0 && N % 8 == 0 && K > 0 &&
-         aligned16(a.addr()) && aligned16(b.addr()) &&
+  const int per16 = 16 / esz;  // elements per 16-byte vector
+  return (esz == 2 || esz == 4) && a.stride[1] == 1 && b.stride[1] == 1 && K % per16 == 0 && N % per16 == 0 &&
+         K > 0 && aligned16(a.addr()) && aligned16(b.addr()) &&
          (a.stride[0] * esz) % 16 == 0 && (b.stride[0] * esz) % 16 == 0 && a.shape[0] > 0 && N > 0;
 }
 
@@ -665,12 +666,15 @@ int op_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g95
   g.a_dtype = (int)a.v->dtype; g.b_dtype = (int)b.v->dtype; g.c_dtype = (int)y.v->dtype;
   g.c_s0 = y.stride[0]; g.c_s1 = y.stride[1];
   if (M == 0 || N == 0) return launch(m, "g950_gemm_general", 0, 256, g, stream);
-  const bool same16 = a.v->dtype == b.v->dtype && is_float16ish(a.v->dtype);
+  // both operands of one dtype: bf16 / f16 (v_mfma_f32_32x32x16) or fp32
+  // (v_mfma_f32_32x32x2_f32) on the 256x256 MFMA kernel
+  const bool same16 = a.v->dtype == b.v->dtype && is_float(a.v->dtype);
+  const int esz = a.isz;
   const bool out16 = y.stride[1] == 1 && aligned16(y.addr());
-  const char* mfma_name = a.v->dtype == G950_DTYPE_BFLOAT16
-                              ? (gemm_ktail((int)K, 2) ? "g950_gemm_bf16_256x256_kt" : "g950_gemm_bf16_256x256")
-                              : (gemm_ktail((int)K, 2) ? "g950_gemm_f16_256x256_kt" : "g950_gemm_f16_256x256");
-  if (same16 && gemm_fast_ok(a, b, (int)K, 2) && out16) {
+  char mfma_name[48];
+  snprintf(mfma_name, sizeof mfma_name, "g950_gemm_%s_256x256%s", rr_dtype(a.v->dtype),
+           gemm_ktail((int)K, esz) ? "_kt" : "");
+  if (same16 && gemm_fast_ok(a, b, (int)K, esz) && out16) {
     g.a_s0 = a.stride[0];
     g.b_s0 = b.stride[1];  // Bt row (n) stride
     const int tiles = gemm_tiles(g);
@@ -678,8 +682,8 @@ int op_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g95
     return launch(m, mfma_name, (unsigned)tiles, 512u, g, stream);
   }
   void* bt = nullptr;
-  const size_t bt_bytes = (size_t)N * (size_t)K * 2;
-  bool rowb = same16 && out16 && gemm_rowb_ok(a, b, (int)K, (int)N, 2) && bt_bytes <= ((size_t)1 << 31);
+  const size_t bt_bytes = (size_t)N * (size_t)K * esz;
+  bool rowb = same16 && out16 && gemm_rowb_ok(a, b, (int)K, (int)N, esz) && bt_bytes <= ((size_t)1 << 31);
   // without the workspace for the copy, the general kernel serves the call
   if (rowb && m && workspace(m, stream, bt_bytes, &bt) != G950_OK) rowb = false;
   if (rowb) {
@@ -687,7 +691,9 @@ int op_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g95
     t.b = g.b; t.b_s0 = b.stride[0]; t.c = bt; t.N = (int)N; t.K = (int)K;
     const long long tblocks = ((K + 63) / 64) * ((N + 63) / 64);
     if (tblocks > 0x7FFFFFFF) return fail(G950_USAGE, "matmul: too many tiles");
-    if (int rc = launch(m, "g950_transpose_b16", (unsigned)tblocks, 256u, t, stream)) return rc;
+    if (int rc = launch(m, esz == 2 ? "g950_transpose_b16" : "g950_transpose_b32", (unsigned)tblocks, 256u, t,
+                        stream))
+      return rc;
     g.b = bt;
     g.a_s0 = a.stride[0];
     g.b_s0 = K;

@@ -41,7 +41,12 @@
 
 namespace g950 {
 
-enum GemmMode : int { GEMM_BF16 = 0, GEMM_F16 = 1, GEMM_I8 = 2 };
+enum GemmMode : int { GEMM_BF16 = 0, GEMM_F16 = 1, GEMM_I8 = 2, GEMM_F32 = 3 };
+
+// MFMAs per 16-byte operand chunk: the 16-bit and int8 forms consume a whole
+// chunk per lane in one v_mfma (K 16 / 32); fp32 (v_mfma_f32_32x32x2_f32,
+// one value per lane) takes the chunk's four values in four MFMAs
+constexpr int mfma_per_chunk(int mode) { return mode == GEMM_F32 ? 4 : 1; }
 
 constexpr int BM = 256, BN = 256;  // workgroup tile
 constexpr int SLAB = 128;          // bytes of K per row per LDS stage (two stages)
@@ -153,10 +158,20 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
   }
 }
 
+// One operand chunk into the accumulator.  fp32: lane half h of both
+// operands holds k = 4c + e (c the chunk index of the half), so MFMA e sums
+// A[m][k] B[k][n] over the two halves' k -- every k of the slab exactly once,
+// in an order both operands share.
 template <int MODE>
 __device__ __forceinline__ void mfma_step(const u32x4& bfrag, const u32x4& afrag, f32x16& accf,
                                           i32x16& acci) {
-  if constexpr (MODE == GEMM_BF16) {
+  if constexpr (MODE == GEMM_F32) {
+    // bit-cast the whole vectors, then index: this compiler reads element 0
+    // for every __builtin_bit_cast of a single ext_vector element
+    const f32x4 bv = __builtin_bit_cast(f32x4, bfrag), av = __builtin_bit_cast(f32x4, afrag);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) accf = __builtin_amdgcn_mfma_f32_32x32x2f32(bv[e], av[e], accf, 0, 0, 0);
+  } else if constexpr (MODE == GEMM_BF16) {
     accf = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, bfrag),
                                                    __builtin_bit_cast(bf16x8, afrag), accf, 0, 0, 0);
   } else if constexpr (MODE == GEMM_F16) {
@@ -191,7 +206,7 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * BM;
   const int n0 = tn * BN;
-  constexpr int ES = (MODE == GEMM_I8) ? 1 : 2;  // element bytes
+  constexpr int ES = (MODE == GEMM_I8) ? 1 : (MODE == GEMM_F32) ? 4 : 2;  // element bytes
   const long long lda_b = p.a_s0 * ES;
   const long long ldb_b = p.b_s0 * ES;  // Bt row stride (n) in bytes
   const char* abase = (const char*)p.a + (long long)m0 * lda_b;
@@ -278,13 +293,14 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   // slots; ndma DMA instructions spread evenly over the slots.  The compiler
   // cannot count LDS reads issued behind a DMA, so each k-step ends with an
   // explicit lgkmcnt(0), by when its reads are long done.
+  constexpr int NMF = FM * FN * mfma_per_chunk(MODE);  // MFMAs per k-step
   auto kstep = [&](int buf, int ndma) {
     mfmas(buf);
 #pragma unroll
-    for (int i = 0; i < FM * FN; ++i) {
+    for (int i = 0; i < NMF; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       if (i < FM + FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (ndma && i % ((FM * FN) / ndma) == 0 && i / ((FM * FN) / ndma) < ndma)
+      if (ndma && i % (NMF / ndma) == 0 && i / (NMF / ndma) < ndma)
         __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -358,6 +374,31 @@ __device__ __forceinline__ void transpose16_body(const GemmArgs& p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) w[e] = t[k8 + 2 * e][n] | (t[k8 + 2 * e + 1][n] << 16);
       *(u32x4*)((uint16_t*)p.c + (long long)(n0 + n) * p.K + k0 + k8) = w;
+    }
+  }
+}
+
+// The same for 32-bit elements (N % 4 == 0, K % 4 == 0): 16-byte vectors of 4.
+__device__ __forceinline__ void transpose32_body(const GemmArgs& p) {
+  __shared__ uint32_t t[64][65];
+  const int tiles_n = (p.N + 63) / 64;
+  const int k0 = (blockIdx.x / tiles_n) * 64, n0 = (blockIdx.x % tiles_n) * 64;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = threadIdx.x + 256 * i, k = c >> 4, n4 = (c & 15) * 4;
+    if (k0 + k < p.K && n0 + n4 < p.N) {
+      const u32x4 w = *(const u32x4*)((const uint32_t*)p.b + (long long)(k0 + k) * p.b_s0 + n0 + n4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[k][n4 + e] = w[e];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = threadIdx.x + 256 * i, n = c >> 4, k4 = (c & 15) * 4;
+    if (n0 + n < p.N && k0 + k4 < p.K) {
+      const u32x4 w = {t[k4][n], t[k4 + 1][n], t[k4 + 2][n], t[k4 + 3][n]};
+      *(u32x4*)((uint32_t*)p.c + (long long)(n0 + n) * p.K + k0 + k4) = w;
     }
   }
 }
@@ -822,6 +863,12 @@ G950_GEMM_MFMA(g950_gemm_i8_256x256_kt, g950::GEMM_I8, 4, 2, 0, true)
 extern "C" __global__ __launch_bounds__(256) void g950_transpose_b16(const g950::GemmArgs p) {
   g950::transpose16_body(p);
 }
+extern "C" __global__ __launch_bounds__(256) void g950_transpose_b32(const g950::GemmArgs p) {
+  g950::transpose32_body(p);
+}
+// fp32 on v_mfma_f32_32x32x2_f32 (the matmul corpus's base dtype)
+G950_GEMM_MFMA(g950_gemm_f32_256x256, g950::GEMM_F32, 4, 2, 0, false)
+G950_GEMM_MFMA(g950_gemm_f32_256x256_kt, g950::GEMM_F32, 4, 2, 0, true)
 // int8 signedness variants of the reference family (a100c/plan/tiles.py:121-126):
 // uint8 A x int8 B, int8 A x uint8 B, uint8 x uint8
 G950_GEMM_MFMA(g950_gemm_u8s8_256x256, g950::GEMM_I8, 4, 2, 1, false)

@@ -351,9 +351,21 @@ def test_matmul_selection(m, n, k, colb, kernel):
 
 
 def test_matmul_fp32_and_int8_tails():
-    # fp32 operands stay on the general kernel; int8 with a K tail takes the _kt kernel
+    # fp32 operands (the corpus base dtype) take the fp32 MFMA kernel in both B
+    # layouts; mixed operand dtypes and unaligned rows the general kernel
     rc, name, err = validate(rt.OP_MATMUL, gemm_args(128, 128, 128, rt.DT_F32, False, out=rt.DT_F32), [128, 128, 128])
+    assert rc == 0 and name == "g950_gemm_f32_256x256", err
+    rc, name, err = validate(rt.OP_MATMUL, gemm_args(16, 16, 16, rt.DT_F32, True, out=rt.DT_F32), [16, 16, 16])
+    assert rc == 0 and name == "g950_gemm_f32_256x256_kt", err
+    rc, name, err = validate(rt.OP_MATMUL, gemm_args(8, 32, 24, rt.DT_F32, False, out=rt.DT_F32), [24, 8, 32])
+    assert rc == 0 and name == "g950_gemm_f32_256x256_kt", err
+    rc, name, err = validate(rt.OP_MATMUL, gemm_args(8, 30, 24, rt.DT_F32, False, out=rt.DT_F32), [24, 8, 30])
     assert rc == 0 and name == "g950_gemm_general", err
+    mixed = Args().view([64, 64], rt.DT_F32).view([64, 64], rt.DT_BF16, strides=[1, 64]) \
+        .view([64, 64], rt.DT_F32, output=True)
+    rc, name, err = validate(rt.OP_MATMUL, mixed, [64, 64, 64])
+    assert rc == 0 and name == "g950_gemm_general", err
+    # int8 with a K tail takes the _kt kernel
     c = (Args().view([300, 208], rt.DT_INT8).view([208, 200], rt.DT_INT8, strides=[1, 208])
          .view([300, 200], rt.DT_INT32, output=True))
     rc, name, err = validate(rt.OP_MATMUL_I8, c, [208, 300, 200])

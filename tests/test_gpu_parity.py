@@ -445,6 +445,39 @@ def test_gemm_row_major_b_on_mfma(m, n, k, dt):
     close(host(y)[rows], ref.matmul(host(a)[rows], host(b)), bar, bar)
 
 
+@pytest.mark.parametrize("colb", [True, False])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 32), (300, 260, 256), (513, 1000, 1024), (16, 16, 16), (8, 32, 24),
+                                   (4096, 4096, 4096)])
+def test_gemm_fp32_mfma(m, n, k, colb):
+    """fp32 operands (the matmul corpus's base dtype, ops/suite/perf/matmul.py)
+    on v_mfma_f32_32x32x2_f32, both B layouts, K tails included: fp32
+    accumulation against float64 within 1e-5 (np.isclose form)."""
+    rng = np.random.default_rng(m * 3 + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    bt = rng.standard_normal((n, k)).astype(np.float32)
+    ad = torch.from_numpy(a).to(DEV)
+    bd = torch.from_numpy(bt).to(DEV).t() if colb else torch.from_numpy(np.ascontiguousarray(bt.T)).to(DEV)
+    y = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    ops.matmul_kernel(ad, bd, y, m, n, k, sync=True)
+    assert rt.module().last_kernel == "g950_gemm_f32_256x256" + ("_kt" if k % 32 else "")
+    rows = np.arange(m) if m <= 1024 else tile_rows(m, 5)
+    close(y.cpu().numpy()[rows], ref.matmul(a[rows], bt.T), 1e-5, 1e-5 * np.sqrt(k))
+
+
+def test_gemm_fp32_ieee_exact_grid():
+    """The reference's IEEE check (a100c/tests/test_matrix_breadth.py:454):
+    operands on a 1/16 grid make every product and partial sum exact in fp32,
+    so the MFMA result must equal the exact (float64) product bit for bit."""
+    rng = np.random.default_rng(454)
+    a = (rng.integers(-16, 17, (300, 256)) / 16.0).astype(np.float32)
+    b = (rng.integers(-16, 17, (256, 200)) / 16.0).astype(np.float32)
+    y = torch.empty((300, 200), dtype=torch.float32, device=DEV)
+    ops.matmul_kernel(torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV), y, 300, 200, 256, sync=True)
+    assert rt.module().last_kernel == "g950_gemm_f32_256x256"
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.array_equal(y.cpu().numpy(), exact.astype(np.float32))
+
+
 @pytest.mark.parametrize("m,n,k", [(256, 256, 72), (300, 260, 200), (64, 64, 8), (1000, 513, 4104)])
 def test_gemm_k_tail_k_contiguous(m, n, k):
     """K-contiguous operands with K a multiple of 8 but not of 64: the _kt
