@@ -411,6 +411,22 @@ def suite(torch, ops, cpu=True):
         del qb, kb, vb, ob, lb
     del c
 
+    # the same causal GQA attention in fp32 (the fp32 MFMA kernel)
+    c = inputs.config4()
+    q, k, v = (torch.from_numpy(c[n]).to(dev) for n in ("q", "k", "v"))
+    del c
+    o = torch.empty_like(q)
+    lse = torch.empty((4, 32, 4096), dtype=torch.float32, device=dev)
+    call = ops.attn_fwd_causal_kernel(q, k, v, o, 4, 32, 4096, 1 / math.sqrt(128), *q.stride(), *k.stride(),
+                                      *v.stride(), *o.stride(), CAUSAL=True, lse_ptr=lse, prepare=True)
+    ms = event_time(torch, lambda i: call(), 3, 1, warm_s=0.3)
+    tf = 4.0 * 4 * 32 * 128 * 4096 * 4096 / 2 / (ms * 1e-3) / 1e12
+    out.append({"config": "F causal GQA attention fp32 (4,32/8,4096,128)", "kernel": call.kernel,
+                "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
+                "frac": round(tf / FP32_PEAK_TFS, 4)})
+    del q, k, v, o, lse
+    torch.cuda.empty_cache()
+
     # few long rows (split-row two-phase path): softmax bf16 [4, 2^22]
     xs = [torch.randn((4, 1 << 22), device=dev, generator=g).to(torch.bfloat16) for _ in range(ROTATE)]
     ys = [torch.empty_like(x) for x in xs]

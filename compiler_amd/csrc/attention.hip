@@ -664,8 +664,133 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   }
 }
 
+// ------------------------------------------------------------ fp32 MFMA path
+// Flash-style attention on v_mfma_f32_32x32x2_f32 for fp32 inputs (and for
+// 16-bit inputs the 16-bit kernel does not take: head dim 32, a scale <= 0):
+// every score is computed once.  Workgroup = 4 waves x 32 queries of one
+// (z, head); key tiles of 64 staged in LDS as fp32 (converted on load, keys
+// past Sk as zeros), 129-float rows so the per-key column reads hit distinct
+// banks.  Per wave and tile:
+//   * S^T = K.Q^T: the K tile (LDS) on the A port, Q (registers, lane half
+//     h holding d = 2s + h of its query) on the B port; each lane then holds
+//     16 scores of ONE query per 32-key block (keys 8(v/4) + 4h + v%4), so
+//     the online softmax state is per lane, the two halves of a query
+//     combining their tile maxima with one lane swap;
+//   * scores are scaled (log2 units) before the maximum, which holds for any
+//     sign of the scale;
+//   * O^T += V^T.P^T: step (q, e) of a 32-key block takes key 8q + 4h + e
+//     for lane half h -- exactly the keys that half's score registers hold,
+//     so P feeds the B port from the score registers in fp32, unrounded.
+constexpr int AF_BQ = 128;  // queries per workgroup (4 waves x 32)
+constexpr int AF_BK = 64;   // keys per tile
+
+template <int D>
+__device__ __forceinline__ void attn_f32_body(const AttnGenArgs& g) {
+  const AttnArgs& p = g.a;
+  __shared__ float Ks[AF_BK][D + 1];
+  __shared__ float Vs[AF_BK][D + 1];
+  if (blockDim.x != 256) return;  // launch shape must match the kernel
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hh = lane >> 5, r = lane & 31;
+  const int per_qb = p.Z * p.Hq;
+  const int qb = p.nqb - 1 - (int)(blockIdx.x / per_qb);  // longest (causal) first
+  const int zh = blockIdx.x % per_qb;
+  const int z = zh / p.Hq, h = zh % p.Hq, hk = h / p.group;
+  const int q0 = qb * AF_BQ;
+  const int qw = q0 + wave * 32;
+  const int my_q = qw + r;
+  const long long qoff = (long long)z * p.q_sz + (long long)h * p.q_sh;
+  const long long koff = (long long)z * p.k_sz + (long long)hk * p.k_sh;
+  const long long voff = (long long)z * p.v_sz + (long long)hk * p.v_sh;
+  float qr[D / 2];
+  {
+    const long long row = qoff + (long long)min(my_q, p.Sq - 1) * p.q_ss;
+#pragma unroll
+    for (int s = 0; s < D / 2; ++s) qr[s] = load_as_f32(p.q, row + 2 * s + hh, g.dtype);
+  }
+  int kend = p.Sk;
+  if (p.causal) kend = min(kend, min(q0 + AF_BQ, p.Sq));
+  const int ntiles = (kend + AF_BK - 1) / AF_BK;
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int b = 0; b < D / 32; ++b) o[b] = (f32x16){};
+  float m = -__builtin_huge_valf(), l = 0.0f;
+  for (int t = 0; t < ntiles; ++t) {
+    const int kv0 = t * AF_BK;
+    __syncthreads();  // every wave is done with the previous tile
+    for (int idx = tid; idx < AF_BK * D; idx += 256) {
+      const int key = idx / D, d = idx - key * D;
+      const int j = kv0 + key;
+      const bool in = j < p.Sk;
+      Ks[key][d] = in ? load_as_f32(p.k, koff + (long long)j * p.k_ss + d, g.dtype) : 0.0f;
+      Vs[key][d] = in ? load_as_f32(p.v, voff + (long long)j * p.v_ss + d, g.dtype) : 0.0f;
+    }
+    __syncthreads();
+    // the whole wave past Sq, or (causal) every query of the wave before the tile
+    if (qw >= p.Sq || (p.causal && kv0 > qw + 31)) continue;
+    f32x16 sc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sc[kb] = (f32x16){};
+#pragma unroll
+      for (int s = 0; s < D / 2; ++s)
+        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[kb * 32 + r][2 * s + hh], qr[s], sc[kb], 0, 0, 0);
+    }
+    float tmax = -__builtin_huge_valf();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = kv0 + kb * 32 + 8 * (v >> 2) + 4 * hh + (v & 3);
+        float x = sc[kb][v] * p.scale_log2;
+        if (key >= p.Sk || (p.causal && key > my_q)) x = -__builtin_huge_valf();
+        sc[kb][v] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m, tmax);
+    // a query without a visible key so far keeps m = -inf: base 0 gives
+    // exp2(-inf) = 0 instead of inf - inf
+    const float mb = (m_new == -__builtin_huge_valf()) ? 0.0f : m_new;
+    const float alpha = exp2f(m - mb);
+    l *= alpha;
+#pragma unroll
+    for (int b = 0; b < D / 32; ++b) o[b] *= alpha;
+    m = m_new;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        sc[kb][v] = exp2f(sc[kb][v] - mb);
+        l += sc[kb][v];
+      }
+#pragma unroll
+    for (int b = 0; b < D / 32; ++b)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[kb * 32 + 8 * (v >> 2) + 4 * hh + (v & 3)][32 * b + r],
+                                                      sc[kb][v], o[b], 0, 0, 0);
+  }
+  const float l_tot = l + __shfl_xor(l, 32);
+  if (my_q >= p.Sq) return;
+  const bool empty = !(l_tot > 0.0f);
+  const float inv = empty ? 0.0f : 1.0f / l_tot;
+  const long long orow = (long long)z * p.o_sz + (long long)h * p.o_sh + (long long)my_q * p.o_ss;
+#pragma unroll
+  for (int b = 0; b < D / 32; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      store_from_f32(p.o, orow + 32 * b + 8 * (v >> 2) + 4 * hh + (v & 3), g.dtype, o[b][v] * inv);
+  if (p.lse && hh == 0) {
+    const float lse = empty ? __builtin_huge_valf() : (m + __log2f(l_tot)) * 0.69314718055994530942f;
+    p.lse[(long long)z * p.lse_sz + (long long)h * p.lse_sh + (long long)my_q * p.lse_ss] = lse;
+  }
+}
+
 // ------------------------------------------------------------- general path
-// fp32 (or any float dtype) attention for small problems: one thread per
+// Any float dtype and head dim the MFMA kernels do not take: one thread per
 // query row, two passes over the keys (max, then exp-sum and P.V).
 
 
@@ -786,6 +911,15 @@ G950_ATTN(g950_attn_fwd_f16_d128, 128, true, G950_ATT_WAVES)
 G950_ATTN(g950_attn_fwd_f16_d64, 64, true, G950_ATT_WAVES)
 extern "C" __global__ __launch_bounds__(64) void g950_attn_fwd_general(const g950::AttnGenArgs p) {
   g950::attn_general_body(p);
+}
+extern "C" __global__ __launch_bounds__(256) void g950_attn_fwd_f32mfma_d32(const g950::AttnGenArgs p) {
+  g950::attn_f32_body<32>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void g950_attn_fwd_f32mfma_d64(const g950::AttnGenArgs p) {
+  g950::attn_f32_body<64>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void g950_attn_fwd_f32mfma_d128(const g950::AttnGenArgs p) {
+  g950::attn_f32_body<128>(p);
 }
 extern "C" __global__ __launch_bounds__(64) void g950_attn_varlen_general(const g950::AttnVarArgs p) {
   g950::attn_varlen_general_body(p);

@@ -1071,6 +1071,16 @@ int launch_attention(g950_module* m, AttnArgs& a, uint32_t dt, long long D, cons
   ga.a = a;
   ga.D = (int)D;
   ga.dtype = (int)dt;
+  if (D == 32 || D == 64 || D == 128) {
+    // fp32 (and 16-bit inputs the kernel above does not take) on the fp32
+    // MFMA: 4 waves x 32 queries per workgroup, any scale
+    char name[48];
+    snprintf(name, sizeof name, "g950_attn_fwd_f32mfma_d%lld", D);
+    ga.a.nqb = (int)((S + 127) / 128);
+    const long long grid = (long long)ga.a.nqb * Z * H;
+    if (grid > 0x7FFFFFFF) return fail(G950_USAGE, "attention: grid too large");
+    return launch(m, name, (unsigned)grid, 256u, ga, stream);
+  }
   const long long rows = Z * H * S;
   return launch(m, "g950_attn_fwd_general", (unsigned)((rows + 63) / 64), 64u, ga, stream);
 }

@@ -419,7 +419,17 @@ def test_attention_selection_and_refusals():
     assert name == "g950_attn_fwd_bf16_d128"
     rc, name, err = validate(rt.OP_ATTENTION_LSE, attn_args(4, 4, 4, 32, 64, rt.DT_F32),
                              attn_scalars(4, 4, 4, 32, 64, causal=False))
-    assert rc == 0 and name == "g950_attn_fwd_general", err
+    assert rc == 0 and name == "g950_attn_fwd_f32mfma_d64", err   # fp32: the fp32 MFMA kernel
+    rc, name, err = validate(rt.OP_ATTENTION_LSE, attn_args(4, 32, 8, 4096, 128, rt.DT_F32),
+                             attn_scalars(4, 32, 8, 4096, 128))
+    assert rc == 0 and name == "g950_attn_fwd_f32mfma_d128", err
+    rc, name, err = validate(rt.OP_ATTENTION_LSE, attn_args(1, 2, 2, 40, 48, rt.DT_F32),
+                             attn_scalars(1, 2, 2, 40, 48))
+    assert rc == 0 and name == "g950_attn_fwd_general", err        # head dim 48: the general kernel
+    neg = attn_scalars(1, 2, 1, 70, 64)
+    neg[4] = np.float32(-0.125)                                      # scale <= 0: not the 16-bit kernel
+    rc, name, err = validate(rt.OP_ATTENTION_LSE, attn_args(1, 2, 1, 70, 64, rt.DT_BF16), neg)
+    assert rc == 0 and name == "g950_attn_fwd_f32mfma_d64", err
     bad = attn_scalars(4, 32, 8, 4096, 128)
     bad[5] += 1  # stride_kh disagrees with the k view
     rc, _, err = validate(rt.OP_ATTENTION_LSE, attn_args(4, 32, 8, 4096, 128, rt.DT_BF16), bad)
@@ -517,8 +527,8 @@ def gqa_scalars(hq, hkv, n, d, group=None):
 
 
 def test_gqa_contract():
-    for shape, dt, kernel in (((2, 4, 2, 32, 32), rt.DT_F32, "g950_attn_fwd_general"),
-                              ((1, 4, 2, 64, 32), rt.DT_BF16, "g950_attn_fwd_general"),
+    for shape, dt, kernel in (((2, 4, 2, 32, 32), rt.DT_F32, "g950_attn_fwd_f32mfma_d32"),
+                              ((1, 4, 2, 64, 32), rt.DT_BF16, "g950_attn_fwd_f32mfma_d32"),
                               ((4, 32, 8, 4096, 128), rt.DT_BF16, "g950_attn_fwd_bf16_d128"),
                               ((2, 8, 2, 500, 64), rt.DT_F16, "g950_attn_fwd_f16_d64")):
         z, hq, hkv, n, d = shape

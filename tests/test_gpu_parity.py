@@ -595,16 +595,50 @@ def test_attention_every_mfma_instantiation(dt, d, causal):
 
 
 @pytest.mark.parametrize("scale", [-0.125, 0.0])
-def test_attention_non_positive_scale_takes_general_kernel(scale):
-    """The MFMA kernel's running maximum needs scale > 0; other scales run the
-    general kernel and still match the oracle's softmax of the scaled scores."""
+def test_attention_non_positive_scale_takes_fp32_kernel(scale):
+    """The 16-bit kernel's running maximum needs scale > 0; other scales run
+    the fp32 MFMA kernel (which scales before the maximum) and still match the
+    oracle's softmax of the scaled scores."""
     c = inputs.config4(1, 2, 1, 70, 64)
     o, lse = ops.attention(dev(c["q"], "bfloat16"), dev(c["k"], "bfloat16"), dev(c["v"], "bfloat16"),
                            scale=scale, causal=True, sync=True)
-    assert rt.module().last_kernel == "g950_attn_fwd_general"
+    assert rt.module().last_kernel == "g950_attn_fwd_f32mfma_d64"
     eo, el = ref.attention(c["q"], c["k"], c["v"], scale, causal=True)
     close(host(o), eo, 2e-2, 2e-2)
     close(lse.cpu().numpy(), el, 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("z,h,hkv,s,d,causal", [
+    (1, 4, 2, 200, 128, True), (2, 2, 1, 333, 64, True), (1, 2, 2, 130, 128, False), (1, 1, 1, 1, 128, True),
+    (2, 4, 2, 64, 32, False), (1, 8, 8, 257, 32, True), (1, 2, 1, 1000, 64, False)])
+def test_attention_fp32(z, h, hkv, s, d, causal):
+    """fp32 attention (attn_fwd_causal / attention_forward_triton list float32)
+    on the fp32 MFMA kernel: every score once, fp32 probabilities; against
+    float64 within 1e-4 (O) and 1e-5 (LSE), np.isclose form."""
+    c = inputs.config4(z, h, hkv, s, d)
+    q, k, v = (torch.from_numpy(c[n]).to(DEV) for n in ("q", "k", "v"))
+    o, lse = ops.attention(q, k, v, causal=causal, sync=True)
+    assert rt.module().last_kernel == f"g950_attn_fwd_f32mfma_d{d}"
+    eo, el = ref.attention(c["q"], c["k"], c["v"], c["scale"], causal=causal)
+    close(o.cpu().numpy(), eo, 1e-4, 1e-5)
+    close(lse.cpu().numpy(), el, 1e-5, 1e-5)
+
+
+def test_attention_fp32_config4_scale():
+    """C4's shape in fp32 ([4, 32, 4096, 128], 8 KV heads, causal): one query
+    head of every KV group of batches 0 and 3 checked in full."""
+    c = inputs.config4()
+    q, k, v = (torch.from_numpy(c[n]).to(DEV) for n in ("q", "k", "v"))
+    o, lse = ops.attention(q, k, v, causal=True, sync=True)
+    assert rt.module().last_kernel == "g950_attn_fwd_f32mfma_d128"
+    rng = np.random.default_rng(8)
+    for zz in (0, 3):
+        for g in range(8):
+            hh = 4 * g + int(rng.integers(0, 4))
+            eo, el = ref.attention(c["q"][zz:zz + 1, hh:hh + 1], c["k"][zz:zz + 1, g:g + 1],
+                                   c["v"][zz:zz + 1, g:g + 1], c["scale"], causal=True)
+            close(o[zz, hh].cpu().numpy(), eo[0, 0], 1e-4, 1e-5)
+            close(lse[zz, hh].cpu().numpy(), el[0, 0], 1e-5, 1e-5)
 
 
 def test_attention_config4_sampled_heads():
