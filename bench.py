@@ -427,6 +427,25 @@ def suite(torch, ops, cpu=True):
     del q, k, v, o, lse
     torch.cuda.empty_cache()
 
+    # rows whose length is not a whole number of 16-byte vectors: bf16 [8191, 3001]
+    # (C2's distribution), LayerNorm and softmax, 4 rotating sets
+    odd = []
+    for sidx in range(ROTATE):
+        c = inputs.config2(8191, 3001, seed=inputs.SEEDS["c2"] + 10 + sidx)
+        bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
+        odd.append((bf(c["x"]), bf(c["gamma"]), bf(c["beta"]), torch.empty((8191, 3001), dtype=torch.bfloat16, device=dev),
+                    torch.empty(8191, device=dev), torch.empty(8191, device=dev)))
+    lno = [ops.layernorm_kernel(x, y, g_, b_, mm, rr, 3001, 3001, 1e-5, prepare=True) for x, g_, b_, y, mm, rr in odd]
+    smo = [ops.softmax_kernel(x, y, 3001, prepare=True) for x, g_, b_, y, mm, rr in odd]
+    for name, calls, nbytes in (("F layernorm bf16 [8191,3001] (odd rows)", lno, 2 * 8191 * 3001 * 2 + 2 * 3001 * 2 + 2 * 8191 * 4),
+                                ("F softmax bf16 [8191,3001] (odd rows)", smo, 2 * 8191 * 3001 * 2)):
+        ms = event_time(torch, lambda i: calls[i % ROTATE](), 100, 10, warm_s=0.3)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"config": name, "kernel": calls[0].kernel, "us": round(ms * 1e3, 2), "value": round(gbs, 1),
+                    "unit": "GB/s", "bound": "hbm", "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    del odd, lno, smo
+    torch.cuda.empty_cache()
+
     # few long rows (split-row two-phase path): softmax bf16 [4, 2^22]
     xs = [torch.randn((4, 1 << 22), device=dev, generator=g).to(torch.bfloat16) for _ in range(ROTATE)]
     ys = [torch.empty_like(x) for x in xs]

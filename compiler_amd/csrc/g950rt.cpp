@@ -378,9 +378,22 @@ int launch_rows(g950_module* m, const char* op, RowArgs& a, uint32_t dt, const V
              ((a.x_row * isz) % 16 == 0) && ((a.y_row * isz) % 16 == 0);
   if (p0) vec = vec && aligned16(p0->addr());
   if (p1) vec = vec && aligned16(p1->addr());
+  char name[128];
+  // rows that are not whole aligned 16-byte vectors: masked aligned vectors
+  // when one wave holds a row at any phase and y's rows share x's phase
+  // (empty rows never: their start address need not lie in any allocation)
+  if (!vec && a.cols > 0 && (isz == 2 || isz == 4) && ((x.addr() - y.addr()) % 16) == 0 &&
+      (((a.x_row - a.y_row) * isz) % 16) == 0 && (x.addr() % isz) == 0) {
+    static const int kItems[] = {1, 2, 4, 6, 8};
+    for (int items : kItems) {
+      if ((long long)items * 64 * vmax >= (long long)a.cols + vmax - 1) {
+        snprintf(name, sizeof name, "g950_rm_%s_%s_v%d_i%d", op, rr_dtype(dt), vmax, items);
+        return launch(m, name, (unsigned)((a.rows + 7) / 8), 256u, a, stream);
+      }
+    }
+  }
   const int v = vec ? vmax : 1;
   const int nvec = a.cols / v;
-  char name[128];
   const RowCfg* pick = nullptr;
   for (const RowCfg& c : kRowCfgs)
     if (c.items * c.block >= nvec) { pick = &c; break; }

@@ -32,6 +32,8 @@
 //               workspace and a second launch merges them and writes y.
 #include "g950_common.h"
 
+#include <type_traits>
+
 namespace g950 {
 
 enum RowOp : int { ROW_SOFTMAX = 0, ROW_RMSNORM = 1, ROW_LAYERNORM = 2, ROW_LOGSUMEXP = 3, ROW_LNROW = 4 };
@@ -218,13 +220,29 @@ __device__ __forceinline__ float lse_finish(float m, float s, bool nan) {
   return m + logf(s);
 }
 
-// The per-row work once the row is in registers as fp32 (v, padding lanes
-// holding the op's identity): the reductions, statistics and y.  pw(i) /
-// pb(i) return lane's packed weight / bias vector i (registers or LDS).
-template <int OP, typename T, int VEC, int ITEMS, int BLOCK, class PW, class PB>
-__device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)[ITEMS][VEC], int tid, int nvec,
-                                           void* yrow, float* scratch, PW pw, PB pb) {
-  using IO = RawIO<T, VEC>;
+// How a row kernel's lane vectors meet the row: live(i) -- vector i of the
+// lane holds row elements; ok(i, e) -- element e of it is one; params(i, w,
+// b) -- the weight / bias of its elements; store(i, o) -- write its row
+// elements of y.  The aligned kernels' vectors are whole row vectors (ok is
+// always true); the masked kernel's start at the 16-byte boundary below the
+// row, so its edge vectors hold elements of the neighbouring rows.
+template <class L, class O, class P, class S>
+struct RowEdge {
+  L live;
+  O ok;
+  P params;
+  S store;
+};
+template <class L, class O, class P, class S>
+__device__ __forceinline__ RowEdge<L, O, P, S> row_edge(L l, O o, P p, S s) {
+  return {l, o, p, s};
+}
+
+// The per-row work once the row is in registers as fp32 (v, elements outside
+// the row holding the op's identity): the reductions, statistics and y.
+template <int OP, typename T, int VEC, int ITEMS, int BLOCK, class EG>
+__device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)[ITEMS][VEC], int tid, float* scratch,
+                                           const EG& eg) {
   if constexpr (OP == ROW_LOGSUMEXP) {
     // max ignores NaN (fmaxf), a separate flag carries it
     float m = -__builtin_huge_valf(), nan = 0.0f;
@@ -266,12 +284,11 @@ __device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)
     const float inv = 1.0f / s;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      const int j = tid + i * BLOCK;
-      if (j < nvec) {
+      if (eg.live(i)) {
         float o[VEC];
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * inv;
-        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+        eg.store(i, o);
       }
     }
   } else if constexpr (OP == ROW_RMSNORM) {
@@ -285,13 +302,12 @@ __device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)
     if (tid == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, inv);
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      const int j = tid + i * BLOCK;
-      if (j < nvec) {
-        float o[VEC], w[VEC];
-        IO::unpack(pw(i), w);
+      if (eg.live(i)) {
+        float o[VEC], w[VEC], bb[VEC];
+        eg.params(i, w, bb);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o[e] = (v[i][e] * inv) * w[e];
-        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+        eg.store(i, o);
       }
     }
   } else if constexpr (OP == ROW_LNROW) {
@@ -315,14 +331,12 @@ __device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)
     }
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      const int j = tid + i * BLOCK;
-      if (j < nvec) {
+      if (eg.live(i)) {
         float o[VEC], w[VEC], bb[VEC];
-        IO::unpack(pw(i), w);
-        IO::unpack(pb(i), bb);
+        eg.params(i, w, bb);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o[e] = lnrow_affine<T>(v[i][e], mean, rstd, w[e], bb[e]);
-        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+        eg.store(i, o);
       }
     }
   } else {  // LayerNorm, centered two-pass from registers
@@ -336,12 +350,13 @@ __device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      const int j = tid + i * BLOCK;
-      if (j < nvec) {
+      if (eg.live(i)) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          v[i][e] -= mean;
-          q = fmaf(v[i][e], v[i][e], q);
+          if (eg.ok(i, e)) {
+            v[i][e] -= mean;
+            q = fmaf(v[i][e], v[i][e], q);
+          }
         }
       }
     }
@@ -353,14 +368,12 @@ __device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)
     }
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-      const int j = tid + i * BLOCK;
-      if (j < nvec) {
+      if (eg.live(i)) {
         float o[VEC], w[VEC], bb[VEC];
-        IO::unpack(pw(i), w);
-        IO::unpack(pb(i), bb);
+        eg.params(i, w, bb);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o[e] = v[i][e] * rstd * w[e] + bb[e];
-        store_vec<T, VEC>(yrow, (long long)j * VEC, o);
+        eg.store(i, o);
       }
     }
   }
@@ -437,8 +450,14 @@ __device__ __forceinline__ void rr_regs_body(const RowArgs& a) {
       }
     }
 
-    row_finish<OP, T, VEC, ITEMS, BLOCK>(a, row, v, tid, nvec, yrow, scratch, [&](int i) { return wr[i]; },
-                                         [&](int i) { return br[i]; });
+    row_finish<OP, T, VEC, ITEMS, BLOCK>(
+        a, row, v, tid, scratch,
+        row_edge([&](int i) { return tid + i * BLOCK < nvec; }, [](int, int) { return true; },
+                 [&](int i, float* w, float* bb) {
+                   if constexpr (row_has_w(OP)) IO::unpack(wr[i], w);
+                   if constexpr (row_has_b(OP)) IO::unpack(br[i], bb);
+                 },
+                 [&](int i, const float* o) { store_vec<T, VEC>(yrow, (long long)(tid + i * BLOCK) * VEC, o); }));
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) cur[i] = nxt[i];
   }
@@ -499,12 +518,121 @@ __device__ __forceinline__ void rw_body(const RowArgs& a) {
           v[i][e] = (OP == ROW_SOFTMAX || OP == ROW_LOGSUMEXP) ? -__builtin_huge_valf() : 0.0f;
       }
     }
-    row_finish<OP, T, VEC, ITEMS, 64>(a, row, v, lane, nvec, (char*)a.y + (long long)row * ystride, nullptr,
-                                      [&](int i) { return wl[row_has_w(OP) ? lane + i * 64 : 0]; },
-                                      [&](int i) { return bl[row_has_b(OP) ? lane + i * 64 : 0]; });
+    char* yrow = (char*)a.y + (long long)row * ystride;
+    row_finish<OP, T, VEC, ITEMS, 64>(
+        a, row, v, lane, nullptr,
+        row_edge([&](int i) { return lane + i * 64 < nvec; }, [](int, int) { return true; },
+                 [&](int i, float* w, float* bb) {
+                   if constexpr (row_has_w(OP)) IO::unpack(wl[lane + i * 64], w);
+                   if constexpr (row_has_b(OP)) IO::unpack(bl[lane + i * 64], bb);
+                 },
+                 [&](int i, const float* o) { store_vec<T, VEC>(yrow, (long long)(lane + i * 64) * VEC, o); }));
     if (k + 1 < RPW) {
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) cur[i] = nxt[i];
+    }
+  }
+}
+
+// Rows whose length is not a whole number of 16-byte vectors, or whose
+// starts are not 16-byte aligned (e.g. bf16 [8191, 3001]): 16-byte aligned
+// vector loads still, from the boundary at or below the row start, with a
+// per-element mask at the two edge vectors -- elements of the neighbouring
+// rows read as the op's identity, and the edge vectors' row elements are
+// stored one by one (y's rows must share x's 16-byte phase).  An aligned
+// 16-byte block holding a row element lies within the same page as that
+// element, so the edge reads stay inside mapped memory.  The per-column
+// parameters are staged in LDS element by element and read at the element's
+// column, whatever the row's phase.  Same workgroup shape as rw_body: WAVES
+// waves, RPW rows each, one row per wave at a time.
+template <int OP, typename T, int VEC, int ITEMS, int WAVES, int RPW>
+__device__ __forceinline__ void rm_body(const RowArgs& a) {
+  using IO = RawIO<T, VEC>;
+  using R = typename IO::type;
+  using S = typename std::conditional<sizeof(T) == 4, float, uint16_t>::type;  // storage element
+  constexpr int MAXC = ITEMS * 64 * VEC;
+  __shared__ S wl[row_has_w(OP) ? MAXC : 1];
+  __shared__ S bl[row_has_b(OP) ? MAXC : 1];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int cols = a.cols;  // host guarantees 0 < cols and ph + cols <= ITEMS * 64 * VEC
+  if (cols <= 0) return;    // no row element: no vector may be read
+  const int row0 = blockIdx.x * WAVES * RPW + wave;
+  auto to_f = [](S x) -> float {
+    if constexpr (sizeof(T) == 4) return x;
+    else return Elem<T>::to_f32(x);
+  };
+  // 16-byte boundary at or below a row start and the start's phase (elements)
+  auto base = [&](const void* p, long long row, long long stride, int& ph) -> char* {
+    const uintptr_t at = (uintptr_t)p + (uintptr_t)(row * stride * (long long)sizeof(T));
+    ph = (int)((at & 15) / sizeof(T));
+    return (char*)(at & ~(uintptr_t)15);
+  };
+  R cur[ITEMS], nxt[ITEMS];
+  int cph = 0, nph = 0;
+  auto load = [&](int row, R (&dst)[ITEMS], int& ph) {
+    const char* xlo = base(a.x, row, a.x_row, ph);
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int j = lane + i * 64;
+      if (j * VEC - ph < cols) dst[i] = IO::load(xlo, (long long)j * VEC);
+    }
+  };
+  if (row0 < a.rows) load(row0, cur, cph);
+  if constexpr (row_has_w(OP)) {
+    for (int c = threadIdx.x; c < cols; c += WAVES * 64) {
+      wl[c] = ((const S*)a.w)[c];
+      if constexpr (row_has_b(OP)) bl[c] = ((const S*)a.b)[c];
+    }
+    __syncthreads();
+  }
+  constexpr float ident = (OP == ROW_SOFTMAX || OP == ROW_LOGSUMEXP) ? -__builtin_huge_valf() : 0.0f;
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int row = row0 + k * WAVES;
+    if (row >= a.rows) break;
+    if (k + 1 < RPW && row + WAVES < a.rows) load(row + WAVES, nxt, nph);
+    const int ph = cph;
+    auto col = [&](int i, int e) { return (lane + i * 64) * VEC + e - ph; };
+    auto ok = [&](int i, int e) {
+      const int c = col(i, e);
+      return c >= 0 && c < cols;
+    };
+    float v[ITEMS][VEC];
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      float t[VEC];
+      if ((lane + i * 64) * VEC - ph < cols) IO::unpack(cur[i], t);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[i][e] = ok(i, e) ? t[e] : ident;
+    }
+    int yph;
+    char* ylo = base(a.y, row, a.y_row, yph);  // yph == ph (host-checked)
+    row_finish<OP, T, VEC, ITEMS, 64>(
+        a, row, v, lane, nullptr,
+        row_edge([&](int i) { return (lane + i * 64) * VEC - ph < cols; }, ok,
+                 [&](int i, float* w, float* bb) {
+#pragma unroll
+                   for (int e = 0; e < VEC; ++e) {
+                     const int c = min(max(col(i, e), 0), cols - 1);
+                     if constexpr (row_has_w(OP)) w[e] = to_f(wl[c]);
+                     if constexpr (row_has_b(OP)) bb[e] = to_f(bl[c]);
+                   }
+                 },
+                 [&](int i, const float* o) {
+                   const long long j = lane + i * 64;
+                   if (j * VEC - ph >= 0 && j * VEC - ph + VEC <= cols) {
+                     store_vec<T, VEC>(ylo, j * VEC, o);
+                   } else {
+#pragma unroll
+                     for (int e = 0; e < VEC; ++e)
+                       if (ok(i, e)) store_vec<T, 1>(ylo, j * VEC + e, &o[e]);
+                   }
+                 }));
+    if (k + 1 < RPW) {
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) cur[i] = nxt[i];
+      cph = nph;
     }
   }
 }
@@ -824,6 +952,29 @@ G950_RR_ALL(lnrow, g950::ROW_LNROW)
   G950_RW_SET(OPNAME, OP, f16, g950::f16_t, 8)
 G950_RW_ALL(layernorm, g950::ROW_LAYERNORM)
 G950_RW_ALL(lnrow, g950::ROW_LNROW)
+
+// Masked aligned vectors (rm_body) for rows that are not whole, aligned
+// 16-byte vectors: g950_rm_<op>_<dtype>_v<VEC>_i<ITEMS>, 4 waves x 2 rows.
+#define G950_RM(OPNAME, OP, TNAME, T, VEC, ITEMS)                                        \
+  extern "C" __global__ __launch_bounds__(256) void                                      \
+      g950_rm_##OPNAME##_##TNAME##_v##VEC##_i##ITEMS(const g950::RowArgs a) {            \
+    g950::rm_body<OP, T, VEC, ITEMS, 4, 2>(a);                                           \
+  }
+#define G950_RM_SET(OPNAME, OP, TNAME, T, VEC) \
+  G950_RM(OPNAME, OP, TNAME, T, VEC, 1)        \
+  G950_RM(OPNAME, OP, TNAME, T, VEC, 2)        \
+  G950_RM(OPNAME, OP, TNAME, T, VEC, 4)        \
+  G950_RM(OPNAME, OP, TNAME, T, VEC, 6)        \
+  G950_RM(OPNAME, OP, TNAME, T, VEC, 8)
+#define G950_RM_ALL(OPNAME, OP)                  \
+  G950_RM_SET(OPNAME, OP, f32, float, 4)         \
+  G950_RM_SET(OPNAME, OP, bf16, g950::bf16_t, 8) \
+  G950_RM_SET(OPNAME, OP, f16, g950::f16_t, 8)
+G950_RM_ALL(softmax, g950::ROW_SOFTMAX)
+G950_RM_ALL(logsumexp, g950::ROW_LOGSUMEXP)
+G950_RM_ALL(rmsnorm, g950::ROW_RMSNORM)
+G950_RM_ALL(layernorm, g950::ROW_LAYERNORM)
+G950_RM_ALL(lnrow, g950::ROW_LNROW)
 
 // ------------------------------------------------------------- stream copy
 // y = x for n 16-byte vectors, grid-stride, nontemporal loads and stores --

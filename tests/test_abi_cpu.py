@@ -98,7 +98,8 @@ def softmax_args(rows, cols, dtype):
 @pytest.mark.parametrize("rows,cols,dtype,kernel", [
     (4096, 4096, rt.DT_F32, "g950_rr_softmax_f32_v4_i16_b64"),
     (8191, 3000, rt.DT_BF16, "g950_rr_softmax_bf16_v8_i6_b64"),
-    (4, 97, rt.DT_F32, "g950_rr_softmax_f32_v1_i2_b64"),
+    (4, 97, rt.DT_F32, "g950_rm_softmax_f32_v4_i1"),      # odd rows: masked aligned vectors
+    (8191, 3001, rt.DT_BF16, "g950_rm_softmax_bf16_v8_i6"),
     (4, 16, rt.DT_F16, "g950_rr_softmax_f16_v8_i1_b64"),
     (2, 100000, rt.DT_F32, "g950_rs_final_softmax_f32_v4"),
     (3, 70001, rt.DT_F32, "g950_rs_final_softmax_f32_v1"),
@@ -111,6 +112,17 @@ def test_softmax_kernel_selection(rows, cols, dtype, kernel):
     rc, name, err = validate(rt.OP_SOFTMAX, softmax_args(rows, cols, dtype), [cols])
     assert rc == 0, err
     assert name == kernel
+
+
+def test_odd_rows_masked_vectors_need_a_shared_phase():
+    # y rows in another 16-byte phase than x rows: the element-wise v1 kernel
+    a = Args().view([300, 3001], rt.DT_BF16).view([300, 3001], rt.DT_BF16, strides=[3004, 1], output=True)
+    rc, name, err = validate(rt.OP_SOFTMAX, a, [3001])
+    assert rc == 0 and name.startswith("g950_rr_softmax_bf16_v1"), err
+    # rows longer than one wave's eight vectors per lane: the v1 kernels / split rows
+    a = softmax_args(64, 4097, rt.DT_BF16)
+    rc, name, err = validate(rt.OP_SOFTMAX, a, [4097])
+    assert rc == 0 and "_v1" in name, err
 
 
 def test_softmax_refusals():
@@ -129,7 +141,7 @@ def test_softmax_refusals():
 @pytest.mark.parametrize("rows,cols,dtype,ydt,kernel", [
     (4, 16, rt.DT_F32, rt.DT_F32, "g950_rr_logsumexp_f32_v4_i1_b64"),
     (64, 1024, rt.DT_BF16, rt.DT_F32, "g950_rr_logsumexp_bf16_v8_i2_b64"),
-    (4, 97, rt.DT_F16, rt.DT_F16, "g950_rr_logsumexp_f16_v1_i2_b64"),
+    (4, 97, rt.DT_F16, rt.DT_F16, "g950_rm_logsumexp_f16_v8_i1"),
     (2, 100000, rt.DT_F32, rt.DT_F32, "g950_rs_final_logsumexp_f32_v4"),
 ])
 def test_logsumexp_contract(rows, cols, dtype, ydt, kernel):
@@ -293,6 +305,18 @@ def test_empty_views_may_be_null_nonempty_may_not():
     assert rc == rt.REJECTED and "null" in err
 
 
+def test_empty_rows_never_take_the_masked_kernels():
+    # a [3, 0] view whose data pointer is not 16-byte aligned: the masked
+    # kernels would read the aligned block at or below an address no
+    # allocation backs; empty rows keep the element-wise kernel (no loads)
+    a = Args().view([3, 0], rt.DT_F32).view([3], rt.DT_F32, output=True)
+    shape, strides, dtype, out, data, storage, size = a.specs[0]
+    a.specs[0] = (shape, strides, dtype, out, BASE + 8, BASE + 8, 0)
+    rc, name, err = validate(rt.OP_LOGSUMEXP, a, [0])
+    assert rc == 0, err
+    assert not name.startswith("g950_rm_"), name
+
+
 def test_view_reach_outside_storage_is_rejected():
     a = softmax_args(4, 97, rt.DT_F32)
     shape, strides, dtype, out, data, storage, size = a.specs[0]
@@ -454,7 +478,7 @@ def test_softmax_inner_contract():
     # (17,): M = 3, C = 5 -- not a whole 16-byte vector per row
     a = Args().view([15], rt.DT_BF16).view([15], rt.DT_BF16, output=True)
     rc, name, err = validate(rt.OP_SOFTMAX_INNER, a, [3, 5])
-    assert rc == 0 and name == "g950_rr_softmax_bf16_v1_i1_b64", err
+    assert rc == 0 and name == "g950_rm_softmax_bf16_v8_i1", err
     # C2 scale through the flat contract
     a = Args().view([8191 * 3000], rt.DT_BF16).view([8191 * 3000], rt.DT_BF16, output=True)
     rc, name, err = validate(rt.OP_SOFTMAX_INNER, a, [8191, 3000])
@@ -493,7 +517,7 @@ def test_layernorm_row_contract():
     for rows, cols, dt, kernel in ((3, 16, rt.DT_F32, "g950_rr_lnrow_f32_v4_i1_b64"),
                                    (5, 128, rt.DT_BF16, "g950_rr_lnrow_bf16_v8_i1_b64"),
                                    (8191, 3000, rt.DT_BF16, "g950_rw_lnrow_bf16_v8_i6"),
-                                   (7, 67, rt.DT_F16, "g950_rr_lnrow_f16_v1_i2_b64")):
+                                   (7, 67, rt.DT_F16, "g950_rm_lnrow_f16_v8_i1")):
         rc, name, err = validate(rt.OP_LAYERNORM_ROW, lnrow_args(rows, cols, dt), lnrow_scalars(rows, cols))
         assert rc == 0 and name == kernel, err
     # statistics in another float dtype than X (each pair must agree)

@@ -116,6 +116,66 @@ def test_layernorm_parameters_in_lds(rows, cols, dt):
 
 
 @pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("rows,cols,pad", [(8191, 3001, 0), (37, 97, 0), (5, 1, 0), (7, 67, 5), (1000, 1001, 3),
+                                           (64, 4089, 0), (33, 1023, 1), (300, 2047, 9)])
+def test_masked_row_vectors(rows, cols, pad, dt):
+    """Rows that are not whole 16-byte vectors or start off a 16-byte boundary
+    (row stride cols + pad): the masked aligned-vector kernels for all five row
+    ops, against float64 (fp32 <= 1e-5 relative, 16-bit <= 1e-2); y shares x's
+    row stride, and the gap elements between y's rows (sentinels) stay
+    untouched by the edge vectors' stores."""
+    c = inputs.config2(rows, cols + pad)
+    stride = cols + pad
+    xd = dev(c["x"], dt)[:, :cols]
+    xr = host(xd)
+    g, b = dev(c["gamma"][:cols], dt), dev(c["beta"][:cols], dt)
+    gr, br = host(g), host(b)
+    vec = 4 if dt == "float32" else 8
+    masked = (cols % vec != 0 or stride % vec != 0) and cols + vec - 1 <= 8 * 64 * vec
+
+    def out():
+        return torch.full((rows, stride), -7.0, dtype=TD[dt], device=DEV)[:, :cols]
+
+    def gaps_intact(y):
+        if pad:
+            full = torch.as_strided(y, (rows, stride), (stride, 1))
+            assert bool((full[:, cols:] == -7.0).all())
+
+    bar = (1e-5, 1e-6) if dt == "float32" else (1e-2, 1e-2)
+    y = out()
+    ops.softmax_kernel(xd, y, cols, sync=True)
+    if masked:
+        assert rt.module().last_kernel.startswith("g950_rm_softmax_")
+    close(host(y), ref.softmax(xr), *bar)
+    gaps_intact(y)
+    lse = torch.empty(rows, device=DEV)
+    ops.logsumexp_kernel(xd, lse, cols, sync=True)
+    close(host(lse), ref.logsumexp(xr), 3e-5, 3e-6)
+    y, r = out(), torch.empty(rows, device=DEV)
+    ops.rms_layernorm_forward_kernel(y, stride, xd, stride, g, 1, r, 1, cols, 1e-6, sync=True)
+    ey, er = ref.rms_layernorm(xr, gr, 1e-6)
+    close(host(y), ey, *bar)
+    close(host(r), er, 1e-5, 1e-6)
+    gaps_intact(y)
+    y, mean, rstd = ops.layernorm(xd, g, b, 1e-5, out=out(), sync=True)
+    ey, em, es = ref.layernorm(xr, gr, br, 1e-5)
+    close(host(y), ey, *(bar if dt != "float32" else (1e-5, 1e-5)))
+    close(host(mean), em, 1e-5, 1e-6)
+    assert rel_err(host(rstd), es, 1e-30) <= 1e-5
+    gaps_intact(y)
+    # the row form takes flat buffers addressed by its row-stride scalars
+    yfull = torch.full((rows, stride), -7.0, dtype=TD[dt], device=DEV)
+    y = yfull[:, :cols]
+    ml, sl = torch.empty(rows, device=DEV), torch.empty(rows, device=DEV)
+    ops.layer_norm_forward_row(yfull, stride, dev(c["x"], dt), stride, g, b, ml, 1, sl, 1, rows, cols, 1e-5,
+                               sync=True)
+    ey, em, es = ref.layernorm_row(xr, gr, br, 1e-5)
+    close(host(y), ey, *(bar if dt != "float32" else (1e-5, 1e-5)))
+    close(host(ml), em, 1e-5, 1e-6)
+    gaps_intact(y)
+
+
+@pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
 @pytest.mark.parametrize("rows,cols", [(4, 16), (4, 97), (64, 1024), (8191, 3000), (2, 100000)])
 def test_logsumexp(rows, cols, dt):
     """ops/suite/perf/logsumexp.py: x ~ 3 N(0,1), expected from the inputs as
