@@ -637,6 +637,12 @@ def mfma_probe(torch, ops):
         for _ in range(4):
             gemm()
         torch.cuda.synchronize()
+        if m == 8192:
+            # comparator, not the product: hipBLASLt (torch.matmul) on the
+            # same operands, for its counters beside this kernel's
+            for _ in range(4):
+                torch.matmul(a, bt.t())
+            torch.cuda.synchronize()
         del a, bt, y
     c5 = inputs.config5()
     a8, b8 = torch.from_numpy(c5["a"]).to(dev), torch.from_numpy(c5["bt"]).to(dev)

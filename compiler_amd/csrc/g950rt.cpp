@@ -692,7 +692,7 @@ int op_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g95
     g.b_s0 = b.stride[1];  // Bt row (n) stride
     const int tiles = gemm_tiles(g);
     if (tiles < 0) return fail(G950_USAGE, "matmul: too many tiles");
-    return launch(m, mfma_name, (unsigned)tiles, 512u, g, stream);
+    return launch(m, mfma_name, (unsigned)tiles, (unsigned)kernel_threads(m, mfma_name, 512), g, stream);
   }
   void* bt = nullptr;
   const size_t bt_bytes = (size_t)N * (size_t)K * esz;
@@ -712,7 +712,7 @@ int op_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g95
     g.b_s0 = K;
     const int tiles = gemm_tiles(g);
     if (tiles < 0) return fail(G950_USAGE, "matmul: too many tiles");
-    return launch(m, mfma_name, (unsigned)tiles, 512u, g, stream);
+    return launch(m, mfma_name, (unsigned)tiles, (unsigned)kernel_threads(m, mfma_name, 512), g, stream);
   }
   g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
   g.b_s0 = b.stride[0]; g.b_s1 = b.stride[1];
@@ -797,7 +797,10 @@ int op_matmul_i8(g950_module* m, const g950_view* views, uint32_t nviews, const 
       g.csum = (umask & 1) ? sa.out + sa.a_rows : nullptr;
       if (int rc = launch(m, "g950_i8_sums", (unsigned)((rows + 3) / 4), 256u, sa, stream)) return rc;
     }
-    return launch(m, ktail ? "g950_gemm_i8_256x256_kt" : names[umask], (unsigned)tiles, 512u, g, stream);
+    {
+      const char* name = ktail ? "g950_gemm_i8_256x256_kt" : names[umask];
+      return launch(m, name, (unsigned)tiles, (unsigned)kernel_threads(m, name, 512), g, stream);
+    }
   }
   if (!dequant && N > 1 && y.stride[1] != 1) return fail(G950_USAGE, "matmul_i8: c_ptr layout");
   g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
@@ -940,7 +943,10 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
     g.cscale = s.v->data; g.cscale_dtype = (int)s.v->dtype;
     const int tiles = gemm_tiles(g);
     if (tiles < 0) return fail(G950_USAGE, "dequant_matmul: too many tiles");
-    return launch(m, bf16 ? "g950_gemm_bf16_256x256" : "g950_gemm_f16_256x256", (unsigned)tiles, 512u, g, stream);
+    {
+      const char* name = bf16 ? "g950_gemm_bf16_256x256" : "g950_gemm_f16_256x256";
+      return launch(m, name, (unsigned)tiles, (unsigned)kernel_threads(m, name, 512), g, stream);
+    }
   }
   if (fast) {
     g.a_s0 = a.stride[0];
