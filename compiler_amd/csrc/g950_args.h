@@ -40,10 +40,6 @@ struct GemmArgs {
   int a_dtype, b_dtype, c_dtype;
   const void* bscale; // fused weight dequantisation: per-column scale of an int8 B
   int bscale_dtype;   //   (float dtype code), applied to the fp32 accumulator
-  int splits;         // split-K: K ranges per output tile (1: none)
-  int kchunk;         // split-K: K elements per range (multiple of the K tile)
-  float* part;        // split-K: [splits, M, N] fp32 partial products
-  int* tile_count;    // split-K: per-tile arrival counters, zero between calls
   const void* cscale; // bf16/f16 MFMA GEMM: optional per-column output scale
   int cscale_dtype;   //   (float dtype code), applied in the epilogue
   // int8 MFMA GEMM with an unsigned operand: the kernel multiplies u - 128
@@ -82,11 +78,6 @@ struct AttnArgs {
   int causal;
   int nqb;           // query blocks
   int group;         // query heads per KV head: KV head of query head h is h / group
-};
-
-struct ZeroArgs {
-  int* p;
-  long long n;  // ints to clear
 };
 
 struct CopyArgs {

@@ -1,5 +1,5 @@
 // The library's static device scratch for g950_launch_noalloc: workspace
-// and arrival counters for callers that cannot allocate device memory (code
+// for callers that cannot allocate device memory (code
 // under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
 //
 // Each GPU the library runs on holds its own copy of the array at its own

@@ -37,13 +37,11 @@ struct g950_module {
   int cus = 256;  // compute units of the device (persistent grid sizing)
   std::mutex mu;
   std::unordered_map<std::string, hipFunction_t> fns;
-  // per-stream device workspace (split-row and split-K partials); launches on
-  // one stream are ordered, so each stream owns one buffer, grown on demand
+  // per-stream device workspace (split-row partials, the widened and
+  // transposed copies of B, unsigned int8 sums); launches on one stream are
+  // ordered, so each stream owns one buffer, grown on demand
   std::mutex ws_mu;
   std::unordered_map<void*, std::pair<void*, size_t>> ws;
-  // per-stream arrival counters (split-K), zeroed at allocation; every kernel
-  // that uses them leaves them zero
-  std::unordered_map<void*, std::pair<void*, size_t>> counters;
   // device address of the library's static scratch array on this device
   // (g950_launch_noalloc), looked up at open; null with scratch_err set if the
   // lookup failed
@@ -60,10 +58,9 @@ thread_local std::string t_error;
 thread_local std::string t_kernel;
 // Set while a g950_launch_noalloc call is dispatched on this thread: the
 // device address of the module's scratch array, which then serves every
-// workspace and counter request instead of hipMalloc.
+// workspace request instead of hipMalloc.
 thread_local char* t_scratch = nullptr;
-constexpr size_t kScratchCounterBytes = 64 << 10;
-constexpr size_t kScratchWorkspace = G950_NOALLOC_SCRATCH_BYTES - kScratchCounterBytes;
+constexpr size_t kScratchWorkspace = G950_NOALLOC_SCRATCH_BYTES;
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -305,46 +302,6 @@ int workspace(g950_module* m, void* stream, size_t bytes, void** out) {
 
 template <class Args>
 int launch(g950_module* m, const std::string& name, unsigned grid, unsigned block, Args& args, void* stream);
-
-// Zeroed per-stream counters of at least `n` ints for launches on `stream`.
-int tile_counters(g950_module* m, void* stream, size_t n, int** out) {
-  if (t_scratch) {
-    // the scratch's counter region, cleared by a fill kernel on the stream
-    // (a previous call may have been cut short; no memset node for callers
-    // that capture the launch into a graph)
-    if (n * sizeof(int) > kScratchCounterBytes)
-      return fail(G950_USAGE, "no-alloc launch: %zu arrival counters exceed the scratch's %zu", n,
-                  kScratchCounterBytes / sizeof(int));
-    ZeroArgs z{(int*)(t_scratch + kScratchWorkspace), (long long)n};
-    if (int rc = launch(m, "g950_zero_i32", (unsigned)((n + 255) / 256), 256u, z, stream)) return rc;
-    *out = z.p;
-    return G950_OK;
-  }
-  std::lock_guard<std::mutex> lock(m->ws_mu);
-  auto& w = m->counters[stream];
-  const size_t bytes = n * sizeof(int);
-  if (w.second < bytes) {
-    if (w.first) {
-      if (hipError_t e = hipStreamSynchronize((hipStream_t)stream))
-        return fail(G950_SYNC, "counters: %s", hipGetErrorString(e));
-      (void)hipFree(w.first);
-      w = {nullptr, 0};
-    }
-    const size_t nb = ((bytes < (size_t)4096 ? (size_t)4096 : bytes * 2) + 255) & ~(size_t)255;
-    if (hipError_t e = hipMalloc(&w.first, nb)) {
-      w = {nullptr, 0};
-      return fail(G950_RESOURCE, "counters: hipMalloc(%zu): %s", nb, hipGetErrorString(e));
-    }
-    if (hipError_t e = hipMemsetAsync(w.first, 0, nb, (hipStream_t)stream)) {
-      (void)hipFree(w.first);
-      w = {nullptr, 0};
-      return fail(G950_RESOURCE, "counters: hipMemsetAsync: %s", hipGetErrorString(e));
-    }
-    w.second = nb;
-  }
-  *out = (int*)w.first;
-  return G950_OK;
-}
 
 // Split rows (rowreduce.hip, rs_*): chunks of 1024 vectors (RS_BLOCK 256 x
 // RS_ITEMS 4), one workgroup per (row, chunk), two launches.
@@ -903,15 +860,18 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
   const bool fast = is_float16ish(a.v->dtype) && K % 16 == 0 && (K < 2 || (a.stride[1] == 1 && b.stride[0] == 1)) &&
                     a.stride[0] % 8 == 0 && b.stride[1] % 16 == 0 && aligned16(a.addr()) && aligned16(b.addr()) &&
                     y.stride[1] == 1 && aligned16(y.addr());
-  if (fast && M <= 16) {
-    // decode shapes: the 16-row kernel streams B, 32 columns and all of K per
-    // workgroup (8 waves, one K range each, summed in LDS)
+  if (fast && M <= 64) {
+    // decode shapes: the few-row kernels stream B, 32 columns and all of K
+    // per workgroup (8 waves, one K range each, summed in LDS), for up to 16,
+    // 32 or 64 rows of A
     g.a_s0 = a.stride[0];
     g.b_s0 = b.stride[1];
     const long long blocks = (N + 31) / 32;
     if (blocks > 0x7FFFFFFF) return fail(G950_USAGE, "dequant_matmul: too many tiles");
-    return launch(m, a.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_gemm_w8a16_skinny_bf16" : "g950_gemm_w8a16_skinny_f16",
-                  (unsigned)blocks, 512u, g, stream);
+    char name[48];
+    snprintf(name, sizeof name, "g950_gemm_w8a16_skinny%s_%s", M <= 16 ? "" : M <= 32 ? "32" : "64",
+             a.v->dtype == G950_DTYPE_BFLOAT16 ? "bf16" : "f16");
+    return launch(m, name, (unsigned)blocks, 512u, g, stream);
   }
   // Many output tiles: widen B once into an exact bf16 / f16 copy in the
   // workspace and run the 256x256 GEMM with the column scale in its epilogue.
@@ -955,29 +915,8 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
     g.tiles_n = (int)((N + 127) / 128);
     const long long tiles = (long long)g.tiles_m * g.tiles_n;
     if (tiles > 0x7FFFFFFF) return fail(G950_USAGE, "dequant_matmul: too many tiles");
-    // split-K when the output tiles cannot fill the chip and A has few rows
-    // (the partial tiles are then small next to B): about two workgroups per
-    // CU, K ranges of whole 64-element tiles, at least 512 long.  Measured on
-    // MI355X at N = K = 8192: M = 16 163 -> 59 us, M = 1 162 -> 42 us; at
-    // M = 128 the partial traffic made it slower (165 -> 212 us).
-    long long splits = 1;
-    if (tiles * 2 < cus && K >= 1024 && M <= 64) {
-      splits = std::min((2 * cus + tiles - 1) / tiles, K / 512);
-      const long long kchunk = ((K + splits - 1) / splits + 63) / 64 * 64;
-      splits = (K + kchunk - 1) / kchunk;
-      g.kchunk = (int)kchunk;
-    }
-    g.splits = (int)splits;
-    if (splits == 1) g.kchunk = (int)K;
-    if (splits > 1 && m) {
-      void* ws = nullptr;
-      // + one tile row of padding: the merge reads whole 128-column tile rows
-      if (int rc = workspace(m, stream, (size_t)((splits * M * N + 128) * 4), &ws)) return rc;
-      g.part = (float*)ws;
-      if (int rc = tile_counters(m, stream, (size_t)tiles, &g.tile_count)) return rc;
-    }
     return launch(m, a.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_gemm_w8a16_bf16_128x128" : "g950_gemm_w8a16_f16_128x128",
-                  (unsigned)(tiles * splits), 256u, g, stream);
+                  (unsigned)tiles, 256u, g, stream);
   }
   g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
   g.b_s0 = b.stride[0]; g.b_s1 = b.stride[1];
@@ -1476,12 +1415,11 @@ const char* g950_last_error(void) { return t_error.c_str(); }
 
 void g950_close(g950_module* m) {
   if (!m) return;
-  for (auto* pool : {&m->ws, &m->counters})
-    for (auto& kv : *pool)
-      if (kv.second.first) {
-        (void)hipStreamSynchronize((hipStream_t)kv.first);
-        (void)hipFree(kv.second.first);
-      }
+  for (auto& kv : m->ws)
+    if (kv.second.first) {
+      (void)hipStreamSynchronize((hipStream_t)kv.first);
+      (void)hipFree(kv.second.first);
+    }
   if (m->mod) (void)hipModuleUnload(m->mod);
   delete m;
 }

@@ -449,12 +449,6 @@ __device__ __forceinline__ void i8_sums_body(const I8SumArgs& p) {
 //     matters where the product is bandwidth-bound (few rows of A)
 //   * K must be a multiple of 16 (whole 16-byte B vectors); a K tile past K
 //     is zero-filled; M/N edges clamp loads and mask stores
-//   * split-K for few output tiles (few rows of A, the decode shape): each
-//     workgroup multiplies one K range and stores its fp32 partial tile with
-//     device-coherent stores; the workgroup that arrives last at its tile's
-//     counter (one atomic increment after the stores completed; nobody waits)
-//     sums all partials in range order, scales, stores and resets the counter
-//     to zero for the next call
 template <bool F16>
 __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
   constexpr int TM = 128, TN = 128, TK = 64;
@@ -465,21 +459,18 @@ __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int split = blockIdx.x % p.splits;
-  const int tile = blockIdx.x / p.splits;
   int tm, tn;
-  tile_of(tile, p.tiles_m, p.tiles_n, tm, tn);
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * TM, n0 = tn * TN;
   const long long lda = p.a_s0 * 2, ldb = p.b_s0;  // bytes
-  const int kbeg = split * p.kchunk;
-  const int kend = min(p.K, kbeg + p.kchunk);
-  const int nk = kend > kbeg ? (kend - kbeg + TK - 1) / TK : 0;
+  const int kend = p.K;
+  const int nk = (p.K + TK - 1) / TK;
 
   // register staging: A vector i (of 4): row (tid + 256 i) >> 3, chunk & 7;
   // B vector i (of 2): row (tid + 256 i) >> 2, 16-int8 part & 3
   u32x4 ra[4], rb[2];
   auto load = [&](int kt) {
-    const int k0 = kbeg + kt * TK;
+    const int k0 = kt * TK;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int v = tid + 256 * i, row = v >> 3, ch = v & 7;
@@ -566,67 +557,6 @@ __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
     cur ^= 1;
   }
   const int wm0 = m0 + wm * 64, wn0 = n0 + wn * 64;
-  if (p.splits > 1) {
-    // This range's partial tile goes out with device-coherent stores (agent
-    // scope: written through to the point where every XCD reads, no L2
-    // write-back needed); once they have completed, one atomic counts the
-    // arrival.  The last range to arrive reads the others' partials with
-    // device-coherent loads.
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi) {
-      const int m = wm0 + mi * 32 + r;
-      if (m >= p.M) continue;
-      float* row = p.part + ((long long)split * p.M + m) * p.N;
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int n = wn0 + ni * 32 + q * 8 + g * 4 + e;
-            if (n < p.N)
-              __hip_atomic_store(row + n, acc[mi][ni][q * 4 + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores complete
-    __syncthreads();
-    __shared__ int arrival;
-    if (tid == 0)
-      arrival = __hip_atomic_fetch_add(p.tile_count + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (arrival != p.splits - 1) return;  // another range's workgroup finishes the tile
-    // sum every range's partial in range order (the result does not depend
-    // on which workgroup arrived last); each range's loads issued together,
-    // at constant offsets from one row pointer per fragment row; columns past
-    // N read the workspace's padding and feed only outputs never stored
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = (f32x16){};
-    for (int sp = 0; sp < p.splits; ++sp) {
-      float v[2][2][16];
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) {
-        const int m = min(wm0 + mi * 32 + r, p.M - 1);
-        const float* row = p.part + ((long long)sp * p.M + m) * p.N + wn0 + g * 4;
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              v[mi][ni][q * 4 + e] =
-                  __hip_atomic_load(row + ni * 32 + q * 8 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) acc[mi][ni][e] += v[mi][ni][e];
-    }
-    if (tid == 0) __hip_atomic_store(p.tile_count + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
   // scale the accumulator by its column's scale (lane layout of gemm_epilogue)
 #pragma unroll
   for (int ni = 0; ni < 2; ++ni)
@@ -643,19 +573,21 @@ __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
 }
 
 // -------------------------------------- W8A16 for few rows of A (decode)
-// M <= 16: the 128-row tile would multiply mostly padding and stage 128 A
+// M <= 64: the 128-row tile would multiply mostly padding and stage 128 A
 // rows per K tile, so a decode-shaped product streams B instead.  A
 // workgroup of 8 waves owns 32 columns (two 16-column tiles) and the whole
 // K: wave w sums K range w of 8, and the waves' partial tiles are added in
-// wave order through LDS (no workspace, no second launch, the same result
-// every run).  Each wave multiplies with v_mfma_f32_16x16x32 (the A rows on
-// the A port, B columns widened from int8 on the B port).  Per 64-element
-// K step, lane (g = lane/16, i = lane%16) loads 16 contiguous int8 of column
-// n0 + 16t + i at k + 16g (64-byte runs per column) and the 32 bytes of A
-// row i at the same k: its first 8 k feed one MFMA, the next 8 a second one
-// (the two MFMAs' k sets interleave, which leaves each dot product
-// unchanged).  Steps are loaded SKINNY_STEPS at a time, before their MFMAs.
-constexpr int SKINNY_STEPS = 8;   // 64-element K steps loaded together
+// wave order through LDS (no workspace, no second launch, no workgroup
+// waits on another, the same result every run).  A holds R groups of 16 rows
+// (R = 1, 2, 4: M <= 16, 32, 64); each widened B operand feeds all R groups.
+// Each wave multiplies with v_mfma_f32_16x16x32 (the A rows on the A port,
+// B columns widened from int8 on the B port).  Per 64-element K step, lane
+// (g = lane/16, i = lane%16) loads 16 contiguous int8 of column n0 + 16t + i
+// at k + 16g (64-byte runs per column) and the 32 bytes of A row 16r + i at
+// the same k: its first 8 k feed one MFMA, the next 8 a second one (the two
+// MFMAs' k sets interleave, which leaves each dot product unchanged).  Steps
+// are loaded SKINNY_STEPS / R at a time, before their MFMAs.
+constexpr int SKINNY_STEPS = 8;   // 64-element K steps loaded together (R = 1)
 constexpr int SKINNY_WAVES = 8;   // K ranges (waves) per workgroup
 constexpr int SKINNY_TILES = 2;   // 16-column tiles per workgroup
 
@@ -708,10 +640,11 @@ __device__ __forceinline__ void widen_i8_body(const GemmArgs& p) {
   dst[1] = hi;
 }
 
-template <bool F16>
+template <bool F16, int R>
 __device__ __forceinline__ void gemm_w8a16_skinny_body(const GemmArgs& p) {
   constexpr int T = SKINNY_TILES;
-  __shared__ f32x4 part[SKINNY_WAVES][T][64];
+  constexpr int STEPS = SKINNY_STEPS / R;
+  __shared__ f32x4 part[SKINNY_WAVES][R][T][64];
   if (blockDim.x != SKINNY_WAVES * 64) return;  // launch shape must match the kernel
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -723,58 +656,74 @@ __device__ __forceinline__ void gemm_w8a16_skinny_body(const GemmArgs& p) {
   const int ke = min(p.K, kb + kw);
   // rows past M repeat row M-1 and columns past N repeat column N-1: their
   // outputs are never stored
-  const char* arow = (const char*)p.a + (long long)min(i, p.M - 1) * p.a_s0 * 2;
+  const char* arow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) arow[r] = (const char*)p.a + (long long)min(16 * r + i, p.M - 1) * p.a_s0 * 2;
   const char* bcol[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) bcol[t] = (const char*)p.b + (long long)min(n0 + 16 * t + i, p.N - 1) * p.b_s0;
-  f32x4 acc[T];
+  f32x4 acc[R][T];
 #pragma unroll
-  for (int t = 0; t < T; ++t) acc[t] = (f32x4){};
-  for (int k0 = kb; k0 < ke; k0 += SKINNY_STEPS * 64) {
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[r][t] = (f32x4){};
+  for (int k0 = kb; k0 < ke; k0 += STEPS * 64) {
     // a lane whose 16 k lie past the range contributes zeros (K % 16 == 0)
-    u32x4 a0[SKINNY_STEPS], a1[SKINNY_STEPS], bw[SKINNY_STEPS][T];
+    u32x4 a0[STEPS][R], a1[STEPS][R], bw[STEPS][T];
 #pragma unroll
-    for (int st = 0; st < SKINNY_STEPS; ++st) {
+    for (int st = 0; st < STEPS; ++st) {
       const int kk = k0 + st * 64 + 16 * g;
       if (kk < ke) {
-        a0[st] = *(const u32x4*)(arow + 2 * (long long)kk);
-        a1[st] = *(const u32x4*)(arow + 2 * (long long)kk + 16);
 #pragma unroll
         for (int t = 0; t < T; ++t) bw[st][t] = __builtin_nontemporal_load((const u32x4*)(bcol[t] + kk));
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          a0[st][r] = *(const u32x4*)(arow[r] + 2 * (long long)kk);
+          a1[st][r] = *(const u32x4*)(arow[r] + 2 * (long long)kk + 16);
+        }
       } else {
-        a0[st] = a1[st] = (u32x4){};
 #pragma unroll
         for (int t = 0; t < T; ++t) bw[st][t] = (u32x4){};
+#pragma unroll
+        for (int r = 0; r < R; ++r) a0[st][r] = a1[st][r] = (u32x4){};
       }
     }
 #pragma unroll
-    for (int st = 0; st < SKINNY_STEPS; ++st)
+    for (int st = 0; st < STEPS; ++st)
 #pragma unroll
       for (int t = 0; t < T; ++t) {
         u32x4 lo, hi;
         widen_i8x16<F16>(bw[st][t], lo, hi);
-        acc[t] = mfma16x16x32<F16>(a0[st], lo, acc[t]);
-        acc[t] = mfma16x16x32<F16>(a1[st], hi, acc[t]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          acc[r][t] = mfma16x16x32<F16>(a0[st][r], lo, acc[r][t]);
+          acc[r][t] = mfma16x16x32<F16>(a1[st][r], hi, acc[r][t]);
+        }
       }
   }
-  // lane (g, i) holds rows 4g .. 4g+3 of column n0 + 16t + i; wave 0 adds
-  // the waves' tiles in wave order, scales and stores
+  // lane (g, i) holds rows 16r + 4g .. +3 of column n0 + 16t + i; wave 0
+  // adds the waves' tiles in wave order, scales and stores
 #pragma unroll
-  for (int t = 0; t < T; ++t) part[wave][t][lane] = acc[t];
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < T; ++t) part[wave][r][t][lane] = acc[r][t];
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    f32x4 sum = part[0][t][lane];
-#pragma unroll
-    for (int w = 1; w < SKINNY_WAVES; ++w) sum += part[w][t][lane];
     const int n = n0 + 16 * t + i;
     if (n >= p.N) continue;
     const float sc = load_as_f32(p.bscale, n, p.bscale_dtype);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = 4 * g + j;
-      if (m < p.M) store_from_f32(p.c, (long long)m * p.c_s0 + n, p.c_dtype, sum[j] * sc);
+    for (int r = 0; r < R; ++r) {
+      f32x4 sum = part[0][r][t][lane];
+#pragma unroll
+      for (int w = 1; w < SKINNY_WAVES; ++w) sum += part[w][r][t][lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = 16 * r + 4 * g + j;
+        if (m < p.M) store_from_f32(p.c, (long long)m * p.c_s0 + n, p.c_dtype, sum[j] * sc);
+      }
     }
   }
 }
@@ -880,12 +829,17 @@ extern "C" __global__ __launch_bounds__(256) void g950_i8_sums(const g950::I8Sum
 extern "C" __global__ __launch_bounds__(256) void g950_gemm_w8a16_bf16_128x128(const g950::GemmArgs p) {
   g950::gemm_w8a16_body<false>(p);
 }
-extern "C" __global__ __launch_bounds__(512) void g950_gemm_w8a16_skinny_bf16(const g950::GemmArgs p) {
-  g950::gemm_w8a16_skinny_body<false>(p);
-}
-extern "C" __global__ __launch_bounds__(512) void g950_gemm_w8a16_skinny_f16(const g950::GemmArgs p) {
-  g950::gemm_w8a16_skinny_body<true>(p);
-}
+// W8A16 decode: up to 16, 32 and 64 rows of A
+#define G950_W8A16_SKINNY(NAME, F16, R)                                                    \
+  extern "C" __global__ __launch_bounds__(512) void NAME(const g950::GemmArgs p) {        \
+    g950::gemm_w8a16_skinny_body<F16, R>(p);                                               \
+  }
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny_bf16, false, 1)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny_f16, true, 1)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny32_bf16, false, 2)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny32_f16, true, 2)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny64_bf16, false, 4)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny64_f16, true, 4)
 extern "C" __global__ __launch_bounds__(256) void g950_gemm_w8a16_f16_128x128(const g950::GemmArgs p) {
   g950::gemm_w8a16_body<true>(p);
 }

@@ -996,8 +996,3 @@ extern "C" __global__ __launch_bounds__(256) void g950_stream_copy(const g950::C
   }
 }
 
-// p[0 .. n) = 0 with vector stores: clears arrival counters in memory a caller
-// may capture into a graph (no memset node there).
-extern "C" __global__ __launch_bounds__(256) void g950_zero_i32(const g950::ZeroArgs a) {
-  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (long long)gridDim.x * 256) a.p[i] = 0;
-}

@@ -205,16 +205,16 @@ int g950_launch(g950_module *module, uint32_t op, const g950_view *views, uint32
                 const g950_scalar *scalars, uint32_t nscalars, void *stream);
 
 /* Bytes of the static device scratch array behind g950_launch_noalloc (one
- * per GPU, held from the module's load until the process ends).  The last
- * 64 KiB hold split-K arrival counters; the rest is workspace. */
+ * per GPU, held from the module's load until the process ends); all of it
+ * serves as workspace. */
 #define G950_NOALLOC_SCRATCH_BYTES (32u << 20)
 
 /* g950_launch that allocates nothing.  No counterpart in the reference: it is
  * for callers that cannot call hipMalloc (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  Same contracts, checks
- * and results as g950_launch; workspace and counters come from the library's
- * static scratch array instead of hipMalloc, and no hipMalloc, hipFree or
- * memset is issued (counters are cleared by a fill kernel).  A call whose
+ * and results as g950_launch; workspace comes from the library's static
+ * scratch array instead of hipMalloc, and no hipMalloc, hipFree or memset is
+ * issued (no route needs memory cleared before it runs).  A call whose
  * workspace exceeds the scratch is refused with G950_USAGE; the W8A16 route
  * that copies B first takes the fused kernel instead when the copy does not
  * fit.  All calls on one GPU share its array and it keeps the last call's

@@ -271,8 +271,12 @@ def test_dequant_matmul_contract():
     assert rc == 0 and name == "g950_gemm_w8a16_bf16_128x128", err
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(16, 4096, 4096, rt.DT_F16), [4096, 16, 4096])
     assert rc == 0 and name == "g950_gemm_w8a16_skinny_f16", err   # decode shape (M <= 16)
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(17, 4096, 4096), [4096, 17, 4096])
+    assert rc == 0 and name == "g950_gemm_w8a16_skinny32_bf16", err   # 17..32 rows
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 4096, 4096, rt.DT_F16), [4096, 64, 4096])
-    assert rc == 0 and name == "g950_gemm_w8a16_f16_128x128", err   # split-K shape
+    assert rc == 0 and name == "g950_gemm_w8a16_skinny64_f16", err   # 33..64 rows
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(65, 4096, 4096), [4096, 65, 4096])
+    assert rc == 0 and name == "g950_gemm_w8a16_bf16_128x128", err   # 65 rows: the tiled kernel
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(4096, 4096, 256), [256, 4096, 4096])
     assert rc == 0 and name == "g950_gemm_bf16_256x256", err   # B widened once, 256 tiles
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(1024, 8192, 128), [128, 1024, 8192])

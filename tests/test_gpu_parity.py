@@ -426,7 +426,8 @@ def test_gemm_bf16_config3_sampled(m, n, k):
 @pytest.mark.parametrize("m,n,k", [(32, 32, 32), (33, 33, 48), (256, 256, 128), (300, 260, 192), (16, 4096, 4096),
                                    (1, 1000, 4096), (2048, 2048, 4096), (7, 70, 208), (16, 8192, 8192),
                                    (5, 130, 1040), (64, 4096, 4096), (4096, 4096, 256), (4100, 4096, 320),
-                                   (1100, 8192, 128), (1024, 8192, 128)])
+                                   (1100, 8192, 128), (1024, 8192, 128), (17, 8192, 8192), (48, 4096, 1040),
+                                   (65, 4096, 4096)])
 def test_dequant_matmul_fused(m, n, k, dt):
     """dequantize_matmul fused into the GEMM: a [M,K] in dt, b int8 ~ U{-127..127}
     (K-contiguous), scale ~ U[0,1) / 64 in dt.  Bar 2e-2 (the bf16 GEMM bar,
@@ -444,14 +445,16 @@ def test_dequant_matmul_fused(m, n, k, dt):
     widened = k % 64 == 0 and 2 * -(-m // 256) * -(-n // 256) > 256
     want = ("g950_gemm_general" if k % 16 else
             f"g950_gemm_w8a16_skinny_{short}" if m <= 16 else
+            f"g950_gemm_w8a16_skinny32_{short}" if m <= 32 else
+            f"g950_gemm_w8a16_skinny64_{short}" if m <= 64 else
             f"g950_gemm_{short}_256x256" if widened else f"g950_gemm_w8a16_{short}_128x128")
     assert rt.module().last_kernel == want
     rows = np.arange(m) if m <= 512 else np.unique(np.r_[0, 127, 128, m - 1,
                                                         np.random.default_rng(5).integers(0, m, 24)])
     expect = ref.matmul(host(ad)[rows], ref.dequantize(b, host(sd)))
     close(host(y)[rows], expect, 2e-2, 2e-2)
-    # split-K shapes (few output tiles) leave their arrival counters at zero:
-    # a second call reproduces the first bit for bit
+    # no kernel keeps state between calls: a second call reproduces the
+    # first bit for bit
     y2 = ops.dequant_matmul(ad, bt.t(), sd, sync=True)
     assert torch.equal(y, y2)
 
