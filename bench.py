@@ -3,8 +3,8 @@
 Headline workload: masked-tail bf16 row reductions
 on x[8191, 3000] -- one step = one LayerNorm pass + one softmax pass over one
 batch; value = algorithmic HBM bytes per step / step time (GB/s).  Inputs are
-resident in HBM before the timed region; the timed region rotates 4 buffer
-sets (~590 MB > the 256 MB Infinity Cache) so that successive steps cannot be
+resident in HBM before the timed region; the timed region rotates 6 buffer
+sets (~885 MB > the 256 MB Infinity Cache) so that successive steps cannot be
 served from MALL.
 
 The same line carries
@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFS = 2516.6   # dense, 256 CU x 2.4 GHz x 4096 FLOP/clk
 INT8_PEAK_TOPS = 5033.2  # dense, 8192 OP/clk/CU
 FP32_PEAK_TFS = 157.3    # dense fp32 MFMA
-ROTATE = 4
+ROTATE = 6   # rotating buffer sets: >= 512 MiB touched per cycle, so the 256 MB MALL cannot hold them
 
 
 def log(msg):
@@ -263,7 +263,7 @@ def suite(torch, ops, cpu=True):
     dev = "cuda:0"
     out = []
 
-    # C1: fp32 RMSNorm + softmax [4096, 4096], 4 rotating sets (512 MiB)
+    # C1: fp32 RMSNorm + softmax [4096, 4096], 6 rotating sets (768 MiB)
     sets = []
     for s in range(ROTATE):
         c = inputs.config1(seed=inputs.SEEDS["c1"] + s)
@@ -297,7 +297,7 @@ def suite(torch, ops, cpu=True):
             lambda n: ref.softmax(x1[:n]), sb / 4096, "GB/s", 1e9, "rows of [4096,4096]", 256, 4096)
         del c1, x1, y1
 
-    # next-row operators at their BASELINE-sized shapes, 4 rotating sets each:
+    # next-row operators at their BASELINE-sized shapes, 6 rotating sets each:
     # row logsumexp bf16 [8191, 3000] -> fp32, int8 weight dequant [8192, 8192] -> bf16
     g = torch.Generator(device=dev)
     g.manual_seed(7)
@@ -428,7 +428,7 @@ def suite(torch, ops, cpu=True):
     torch.cuda.empty_cache()
 
     # rows whose length is not a whole number of 16-byte vectors: bf16 [8191, 3001]
-    # (C2's distribution), LayerNorm and softmax, 4 rotating sets
+    # (C2's distribution), LayerNorm and softmax, 6 rotating sets
     odd = []
     for sidx in range(ROTATE):
         c = inputs.config2(8191, 3001, seed=inputs.SEEDS["c2"] + 10 + sidx)
@@ -567,7 +567,7 @@ def pmc_probe(torch, ops):
     """Counter-collection workload (run under rocprofv3 --pmc): the streaming
     copy kernel on exactly the bytes of one x (the calibration kernel: same
     nontemporal 16-byte loads/stores as the row kernels), then 8 launches of
-    each headline kernel on 4 rotating buffer sets, as in the timed region."""
+    each headline kernel on 6 rotating buffer sets, as in the timed region."""
     from oracle import inputs
     rows, cols = 8191, 3000
     dev = "cuda:0"
@@ -596,7 +596,7 @@ def pmc_probe(torch, ops):
             calls[i % ROTATE]()
         torch.cuda.synchronize()
     del sets, ln, sm, lr
-    # C1 fp32 [4096, 4096] RMSNorm and softmax, 4 rotating sets
+    # C1 fp32 [4096, 4096] RMSNorm and softmax, 6 rotating sets
     c1 = [(torch.randn((4096, 4096), device=dev), torch.rand(4096, device=dev) + 0.5,
            torch.empty((4096, 4096), device=dev), torch.empty(4096, device=dev)) for _ in range(ROTATE)]
     rms = [ops.rms_layernorm_forward_kernel(y, 4096, x, 4096, w, 1, r, 1, 4096, 1e-6, prepare=True)
@@ -607,7 +607,7 @@ def pmc_probe(torch, ops):
             calls[i % ROTATE]()
         torch.cuda.synchronize()
     del c1, rms, smf
-    # int8 weight dequantisation [8192, 8192] -> bf16, 4 rotating sets
+    # int8 weight dequantisation [8192, 8192] -> bf16, 6 rotating sets
     dq = [(torch.randint(-127, 127, (8192, 8192), device=dev, dtype=torch.int8),
            torch.rand(8192, device=dev).to(torch.bfloat16),
            torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)) for _ in range(ROTATE)]
@@ -726,7 +726,7 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded numpy draws of the BASELINE distributions, oracle/inputs.py)",
         "config": {"workload": "C2 masked-tail bf16 LayerNorm + softmax, x[8191,3000] (1% +-60), "
-                               "fp32 statistics, 4 rotating buffer sets",
+                               "fp32 statistics, 6 rotating buffer sets",
                    "rows": 8191, "cols": 3000, "bytes_per_step": step_bytes},
         "roofline": roof, "kernels": per_kernel, "cpu_baseline": cpu, "suite": suite_rows,
     }
