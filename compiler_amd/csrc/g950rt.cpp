@@ -117,7 +117,7 @@ int check_view(const g950_view* views, uint32_t idx, const char* name, int ndim,
   if (output && !(v.flags & G950_VIEW_OUTPUT))
     return fail(G950_REJECTED, "view %s: output argument lacks the output flag", name);
   out.nd = ndim;
-  int64_t lo = 0, hi = 0;
+  __int128 lo = 0, hi = 0;  // 128-bit: caller strides times extents cannot wrap
   bool empty = false;
   for (int i = 0; i < ndim; ++i) {
     out.shape[i] = v.shape[i];
@@ -127,14 +127,14 @@ int check_view(const g950_view* views, uint32_t idx, const char* name, int ndim,
       return fail(G950_REJECTED, "view %s: byte stride %lld not a multiple of the item size",
                   name, (long long)v.strides[i]);
     out.stride[i] = v.strides[i] / out.isz;
-    if (v.strides[i] < 0) lo += v.strides[i] * (v.shape[i] - 1);
-    else hi += v.strides[i] * (v.shape[i] - 1);
+    if (v.strides[i] < 0) lo += (__int128)v.strides[i] * (v.shape[i] - 1);
+    else hi += (__int128)v.strides[i] * (v.shape[i] - 1);
   }
   // an empty view is never dereferenced and may carry null pointers
   if (!empty && (!v.data || !v.storage)) return fail(G950_REJECTED, "view %s: null device pointer", name);
   if (!empty) {
-    const intptr_t base = (intptr_t)v.data - (intptr_t)v.storage;
-    if (base + lo < 0 || (uint64_t)(base + hi + out.isz) > v.storage_size)
+    const __int128 base = (intptr_t)v.data - (intptr_t)v.storage;
+    if (base + lo < 0 || base + hi + out.isz > (__int128)v.storage_size)
       return fail(G950_REJECTED, "view %s: reach [%lld, %lld) outside its %llu-byte storage", name,
                   (long long)(base + lo), (long long)(base + hi + out.isz),
                   (unsigned long long)v.storage_size);
@@ -564,8 +564,12 @@ int op_layernorm_row(g950_module* m, const g950_view* views, uint32_t nviews, co
   if (nrow > 1 && (ys < nc || ms < 1 || rs < 1))
     return fail(G950_USAGE, "layer_norm_forward_row: output rows overlap (Y_row_stride < n_cols or a zero statistic stride)");
   if (nw < nc || nb < nc) return fail(G950_USAGE, "layer_norm_forward_row: W_ptr/B_ptr need n_cols entries");
-  if (nrow > 0 && ((nrow - 1) * xs + nc > nx || (nrow - 1) * ys + nc > ny || (nrow - 1) * ms + 1 > nm ||
-                   (nrow - 1) * rs + 1 > nr))
+  // (n_rows - 1) * stride + width <= elements, in 128-bit arithmetic (the
+  // strides are caller scalars)
+  auto fits = [&](long long stride, long long width, long long n) {
+    return (__int128)(nrow - 1) * stride + width <= (__int128)n;
+  };
+  if (nrow > 0 && !(fits(xs, nc, nx) && fits(ys, nc, ny) && fits(ms, 1, nm) && fits(rs, 1, nr)))
     return fail(G950_USAGE, "layer_norm_forward_row: n_rows rows exceed X_ptr, Y_ptr, Mean_ptr or RSTD_ptr");
   RowArgs a{};
   a.x = x.v->data; a.y = y.v->data; a.w = w.v->data; a.b = b.v->data;
@@ -1135,9 +1139,9 @@ int varlen_index(const char* name) {
 // Rows a flat buffer holds for (row stride rs, heads nh at head stride hs,
 // d contiguous elements): the largest R with (R-1)*rs + (nh-1)*hs + d <= n.
 long long rows_held(long long n, long long rs, long long nh, long long hs, long long d) {
-  const long long fixed = (nh - 1) * hs + d;
-  if (n < fixed) return 0;
-  return rs > 0 ? (n - fixed) / rs + 1 : 0x7FFFFFFF;
+  const __int128 fixed = (__int128)(nh - 1) * hs + d;
+  if ((__int128)n < fixed) return 0;
+  return rs > 0 ? (long long)((n - fixed) / rs) + 1 : 0x7FFFFFFF;
 }
 
 int op_flash_varlen(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
@@ -1183,6 +1187,12 @@ int op_flash_varlen(g950_module* m, const g950_view* views, uint32_t nviews, con
                            "v_batch_stride", "o_batch_stride", "k_page_stride", "page_table_batch_stride"};
   for (const char* n : strides)
     if (I(n) < 0) return fail(G950_USAGE, "flash_varlen: %s must be >= 0", n);
+  // highest element offset + 1 of (nb batches, nr rows, nh heads, d) at the
+  // named strides, in 128-bit arithmetic (the strides are caller scalars)
+  auto reach = [&](long long nb, const char* bst, long long nr, const char* rst, long long nh, const char* hst,
+                   long long d) {
+    return (__int128)(nb - 1) * I(bst) + (__int128)(nr - 1) * I(rst) + (__int128)(nh - 1) * I(hst) + d;
+  };
   const bool cu_q = I("is_cu_seqlens_q") != 0, cu_k = I("is_cu_seqlens_k") != 0;
   const bool seqused = I("is_seqused_k") != 0, paged = I("is_paged") != 0, local = I("is_local") != 0;
   const long long bs = I("block_size");
@@ -1205,8 +1215,8 @@ int op_flash_varlen(g950_module* m, const g950_view* views, uint32_t nviews, con
   vl.q_rows = std::min(rows_held(qe, I("q_row_stride"), H, I("q_head_stride"), D),
                        rows_held(oe, I("o_row_stride"), H, I("o_head_stride"), D));
   if (!cu_q && B > 0 && SQ > 0) {
-    if ((B - 1) * I("q_batch_stride") + (SQ - 1) * I("q_row_stride") + (H - 1) * I("q_head_stride") + D > qe ||
-        (B - 1) * I("o_batch_stride") + (SQ - 1) * I("o_row_stride") + (H - 1) * I("o_head_stride") + D > oe)
+    if (reach(B, "q_batch_stride", SQ, "q_row_stride", H, "q_head_stride", D) > qe ||
+        reach(B, "o_batch_stride", SQ, "o_row_stride", H, "o_head_stride", D) > oe)
       return fail(G950_USAGE, "flash_varlen: b x seqlen_q rows exceed q_ptr/o_ptr");
     if (B * SQ > TQ) return fail(G950_USAGE, "flash_varlen: b x seqlen_q exceeds total_q");
   }
@@ -1215,11 +1225,11 @@ int op_flash_varlen(g950_module* m, const g950_view* views, uint32_t nviews, con
     if (bs <= 0) return fail(G950_USAGE, "flash_varlen: block_size must be positive");
     if (int rc = int_view(pt, "page_table_ptr", 1)) return rc;
     const long long ps = I("k_page_stride"), krs = I("k_row_stride");
-    const long long kfix = (bs - 1) * krs + (HK - 1) * I("k_head_stride") + D;
-    const long long vfix = (bs - 1) * krs + (HK - 1) * I("v_head_stride") + D;
+    const __int128 kfix = (__int128)(bs - 1) * krs + (__int128)(HK - 1) * I("k_head_stride") + D;
+    const __int128 vfix = (__int128)(bs - 1) * krs + (__int128)(HK - 1) * I("v_head_stride") + D;
     long long pages = 0;
     if (ke >= kfix && ve >= vfix)
-      pages = ps > 0 ? std::min((ke - kfix) / ps, (ve - vfix) / ps) + 1 : 1;
+      pages = ps > 0 ? (long long)std::min((ke - kfix) / ps, (ve - vfix) / ps) + 1 : 1;
     vl.pages = pages;
     vl.pt_elems = pt.shape[0];
     vl.pt_stride = I("page_table_batch_stride");
@@ -1231,8 +1241,8 @@ int op_flash_varlen(g950_module* m, const g950_view* views, uint32_t nviews, con
     vl.k_rows = std::min(rows_held(ke, I("k_row_stride"), HK, I("k_head_stride"), D),
                          rows_held(ve, I("v_row_stride"), HK, I("v_head_stride"), D));
     if (!cu_k && B > 0 && SK > 0 &&
-        ((B - 1) * I("k_batch_stride") + (SK - 1) * I("k_row_stride") + (HK - 1) * I("k_head_stride") + D > ke ||
-         (B - 1) * I("v_batch_stride") + (SK - 1) * I("v_row_stride") + (HK - 1) * I("v_head_stride") + D > ve))
+        (reach(B, "k_batch_stride", SK, "k_row_stride", HK, "k_head_stride", D) > ke ||
+         reach(B, "v_batch_stride", SK, "v_row_stride", HK, "v_head_stride", D) > ve))
       return fail(G950_USAGE, "flash_varlen: b x seqlen_k rows exceed k_ptr/v_ptr");
   }
   vl.cu_q = cu_q ? (const int*)cuq.v->data : nullptr;

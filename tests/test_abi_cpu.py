@@ -136,6 +136,13 @@ def test_softmax_refusals():
     assert validate(rt.OP_SOFTMAX, a, [97])[0] == rt.USAGE
     # wrong arity
     assert validate(rt.OP_SOFTMAX, softmax_args(4, 97, rt.DT_F32), [97, 1])[0] == rt.USAGE
+    # a stride whose reach wraps 64 bits (4 row steps x 2^62 bytes = 2^64, which
+    # wraps to 0) is outside any storage
+    a = Args().view([5, 97], rt.DT_F32).view([5, 97], rt.DT_F32, output=True)
+    shape, strides, dtype, output, data, storage, size = a.specs[0]
+    a.specs[0] = (shape, [1 << 62, 4], dtype, output, data, storage, size)
+    rc, _, err = validate(rt.OP_SOFTMAX, a, [97])
+    assert rc == rt.REJECTED and "reach" in err, err
 
 
 @pytest.mark.parametrize("rows,cols,dtype,ydt,kernel", [
@@ -540,6 +547,10 @@ def test_layernorm_row_contract():
     bad = lnrow_scalars(3, 16)
     bad[5] = 0
     assert validate(rt.OP_LAYERNORM_ROW, lnrow_args(3, 16, rt.DT_F32), bad)[0] == rt.USAGE
+    # a row stride whose reach overflows 64 bits ((n_rows - 1) * stride wraps
+    # negative) is still refused
+    rc, _, err = validate(rt.OP_LAYERNORM_ROW, lnrow_args(3, 16, rt.DT_F32), lnrow_scalars(3, 16, xs=1 << 62))
+    assert rc == rt.USAGE and "exceed" in err, err
 
 
 def gqa_args(z, hq, hkv, n, d, dt):
