@@ -534,6 +534,46 @@ __device__ __forceinline__ void rw_body(const RowArgs& a) {
   }
 }
 
+// Parameters (gamma / beta, staged in LDS at their column index) of the
+// columns v*VEC - ph .. v*VEC - ph + VEC-1 of a row whose start lies ph
+// elements past a 16-byte boundary: the 32 bytes of LDS vectors v-1 and v,
+// funnel-shifted by (VEC - ph) elements (v_alignbyte_b32 per dword), one
+// branch per row phase (ph is wave-uniform).  Vector v-1 of v = 0 is
+// replaced by vector 0: its columns lie before the row and are masked.
+template <typename T, int VEC, int PH>
+__device__ __forceinline__ u32x4 shift_pair(const u32x4& lo, const u32x4& hi) {
+  constexpr int O = (VEC - PH) * (int)sizeof(T);  // byte offset of the first column in lo|hi
+  constexpr int Q = O / 4, SH = O % 4;
+  auto d = [&](int j) { return j < 4 ? lo[j] : hi[j - 4]; };
+  u32x4 r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if constexpr (SH == 0) r[k] = d(Q + k);
+    else r[k] = __builtin_amdgcn_alignbyte(d(Q + k + 1), d(Q + k), SH);
+  }
+  return r;
+}
+
+template <typename T, int VEC, typename S>
+__device__ __forceinline__ void shifted_params(const S* arr, int v, int ph, float* out) {
+  using IO = RawIO<T, VEC>;
+  using R = typename IO::type;
+  const u32x4 hi = __builtin_bit_cast(u32x4, ((const R*)arr)[v]);
+  const u32x4 lo = v > 0 ? __builtin_bit_cast(u32x4, ((const R*)arr)[v - 1]) : hi;
+  u32x4 r;
+  switch (ph) {
+    case 0: r = hi; break;
+    case 1: r = shift_pair<T, VEC, 1>(lo, hi); break;
+    case 2: r = shift_pair<T, VEC, 2>(lo, hi); break;
+    case 3: r = shift_pair<T, VEC, 3>(lo, hi); break;
+    case 4: r = shift_pair<T, VEC, (VEC > 4 ? 4 : 0)>(lo, hi); break;
+    case 5: r = shift_pair<T, VEC, (VEC > 5 ? 5 : 0)>(lo, hi); break;
+    case 6: r = shift_pair<T, VEC, (VEC > 6 ? 6 : 0)>(lo, hi); break;
+    default: r = shift_pair<T, VEC, (VEC > 7 ? 7 : 0)>(lo, hi); break;
+  }
+  IO::unpack(__builtin_bit_cast(R, r), out);
+}
+
 // Rows whose length is not a whole number of 16-byte vectors, or whose
 // starts are not 16-byte aligned (e.g. bf16 [8191, 3001]): 16-byte aligned
 // vector loads still, from the boundary at or below the row start, with a
@@ -542,26 +582,22 @@ __device__ __forceinline__ void rw_body(const RowArgs& a) {
 // stored one by one (y's rows must share x's 16-byte phase).  An aligned
 // 16-byte block holding a row element lies within the same page as that
 // element, so the edge reads stay inside mapped memory.  The per-column
-// parameters are staged in LDS element by element and read at the element's
-// column, whatever the row's phase.  Same workgroup shape as rw_body: WAVES
-// waves, RPW rows each, one row per wave at a time.
+// parameters are staged in LDS element by element and read as two aligned
+// vectors shifted to the row's phase (shifted_params).  Same workgroup shape
+// as rw_body: WAVES waves, RPW rows each, one row per wave at a time.
 template <int OP, typename T, int VEC, int ITEMS, int WAVES, int RPW>
 __device__ __forceinline__ void rm_body(const RowArgs& a) {
   using IO = RawIO<T, VEC>;
   using R = typename IO::type;
   using S = typename std::conditional<sizeof(T) == 4, float, uint16_t>::type;  // storage element
   constexpr int MAXC = ITEMS * 64 * VEC;
-  __shared__ S wl[row_has_w(OP) ? MAXC : 1];
-  __shared__ S bl[row_has_b(OP) ? MAXC : 1];
+  __shared__ __attribute__((aligned(16))) S wl[row_has_w(OP) ? MAXC : 1];
+  __shared__ __attribute__((aligned(16))) S bl[row_has_b(OP) ? MAXC : 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int cols = a.cols;  // host guarantees 0 < cols and ph + cols <= ITEMS * 64 * VEC
   if (cols <= 0) return;    // no row element: no vector may be read
   const int row0 = blockIdx.x * WAVES * RPW + wave;
-  auto to_f = [](S x) -> float {
-    if constexpr (sizeof(T) == 4) return x;
-    else return Elem<T>::to_f32(x);
-  };
   // 16-byte boundary at or below a row start and the start's phase (elements)
   auto base = [&](const void* p, long long row, long long stride, int& ph) -> char* {
     const uintptr_t at = (uintptr_t)p + (uintptr_t)(row * stride * (long long)sizeof(T));
@@ -592,7 +628,7 @@ __device__ __forceinline__ void rm_body(const RowArgs& a) {
     const int row = row0 + k * WAVES;
     if (row >= a.rows) break;
     if (k + 1 < RPW && row + WAVES < a.rows) load(row + WAVES, nxt, nph);
-    const int ph = cph;
+    const int ph = __builtin_amdgcn_readfirstlane(cph);  // one phase per row: wave-uniform
     auto col = [&](int i, int e) { return (lane + i * 64) * VEC + e - ph; };
     auto ok = [&](int i, int e) {
       const int c = col(i, e);
@@ -612,12 +648,8 @@ __device__ __forceinline__ void rm_body(const RowArgs& a) {
         a, row, v, lane, nullptr,
         row_edge([&](int i) { return (lane + i * 64) * VEC - ph < cols; }, ok,
                  [&](int i, float* w, float* bb) {
-#pragma unroll
-                   for (int e = 0; e < VEC; ++e) {
-                     const int c = min(max(col(i, e), 0), cols - 1);
-                     if constexpr (row_has_w(OP)) w[e] = to_f(wl[c]);
-                     if constexpr (row_has_b(OP)) bb[e] = to_f(bl[c]);
-                   }
+                   if constexpr (row_has_w(OP)) shifted_params<T, VEC>(wl, lane + i * 64, ph, w);
+                   if constexpr (row_has_b(OP)) shifted_params<T, VEC>(bl, lane + i * 64, ph, bb);
                  },
                  [&](int i, const float* o) {
                    const long long j = lane + i * 64;
