@@ -670,7 +670,8 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
 // every score is computed once.  Workgroup = 4 waves x 32 queries of one
 // (z, head); key tiles of 64 staged in LDS as fp32 (converted on load, keys
 // past Sk as zeros), 129-float rows so the per-key column reads hit distinct
-// banks.  Per wave and tile:
+// banks; fp32 tiles are prefetched into registers one tile ahead.  Per wave
+// and tile:
 //   * S^T = K.Q^T: the K tile (LDS) on the A port, Q (registers, lane half
 //     h holding d = 2s + h of its query) on the B port; each lane then holds
 //     16 scores of ONE query per 32-key block (keys 8(v/4) + 4h + v%4), so
@@ -715,17 +716,52 @@ __device__ __forceinline__ void attn_f32_body(const AttnGenArgs& g) {
 #pragma unroll
   for (int b = 0; b < D / 32; ++b) o[b] = (f32x16){};
   float m = -__builtin_huge_valf(), l = 0.0f;
+  // fp32 inputs: the next tile's K and V rows are loaded into registers as
+  // 16-byte vectors while the current tile is multiplied, then written to
+  // LDS behind the next barrier; vector i of a thread is key (tid + 256 i) /
+  // (D / 4), columns 4 * ((tid + 256 i) % (D / 4)) .. +3
+  constexpr int NV = AF_BK * D / 4 / 256;
+  const bool f32 = g.dtype == DT_F32;
+  const float* kf = (const float*)p.k + koff;
+  const float* vf = (const float*)p.v + voff;
+  f32x4 kst[NV], vst[NV];
+  auto stage_load = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int idx = tid + 256 * i, key = idx / (D / 4), c = 4 * (idx % (D / 4));
+      const int j = t * AF_BK + key;
+      kst[i] = vst[i] = (f32x4){};
+      if (j < p.Sk) {
+        kst[i] = *(const f32x4*)(kf + (long long)j * p.k_ss + c);
+        vst[i] = *(const f32x4*)(vf + (long long)j * p.v_ss + c);
+      }
+    }
+  };
+  if (f32 && ntiles > 0) stage_load(0);
   for (int t = 0; t < ntiles; ++t) {
     const int kv0 = t * AF_BK;
     __syncthreads();  // every wave is done with the previous tile
-    for (int idx = tid; idx < AF_BK * D; idx += 256) {
-      const int key = idx / D, d = idx - key * D;
-      const int j = kv0 + key;
-      const bool in = j < p.Sk;
-      Ks[key][d] = in ? load_as_f32(p.k, koff + (long long)j * p.k_ss + d, g.dtype) : 0.0f;
-      Vs[key][d] = in ? load_as_f32(p.v, voff + (long long)j * p.v_ss + d, g.dtype) : 0.0f;
+    if (f32) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int idx = tid + 256 * i, key = idx / (D / 4), c = 4 * (idx % (D / 4));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          Ks[key][c + e] = kst[i][e];
+          Vs[key][c + e] = vst[i][e];
+        }
+      }
+    } else {
+      for (int idx = tid; idx < AF_BK * D; idx += 256) {
+        const int key = idx / D, d = idx - key * D;
+        const int j = kv0 + key;
+        const bool in = j < p.Sk;
+        Ks[key][d] = in ? load_as_f32(p.k, koff + (long long)j * p.k_ss + d, g.dtype) : 0.0f;
+        Vs[key][d] = in ? load_as_f32(p.v, voff + (long long)j * p.v_ss + d, g.dtype) : 0.0f;
+      }
     }
     __syncthreads();
+    if (f32 && t + 1 < ntiles) stage_load(t + 1);
     // the whole wave past Sq, or (causal) every query of the wave before the tile
     if (qw >= p.Sq || (p.causal && kv0 > qw + 31)) continue;
     f32x16 sc[2];
