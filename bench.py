@@ -691,6 +691,8 @@ def main():
                     help="run only the counter-collection workload (for rocprofv3 --pmc)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="run only the GEMM + attention counter workload (for rocprofv3 --pmc)")
+    ap.add_argument("--hw-probe", action="store_true",
+                    help="run only the gfx950 micro-probes (compiler_amd/probes.py) and print them as JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the multi-GPU "
@@ -706,6 +708,10 @@ def main():
         return
     if args.mfma_probe:
         mfma_probe(torch, ops)
+        return
+    if args.hw_probe:
+        from compiler_amd import probes
+        print(json.dumps(probes.run(torch), indent=1))
         return
     log("bench: headline (config 2) ...")
     value, ms_step, wall, roof, per_kernel, step_bytes = headline(torch, ops, args)

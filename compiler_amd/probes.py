@@ -1,0 +1,94 @@
+"""gfx950 micro-probes: the hardware rates the kernel designs are built on.
+
+Measurement only (``python bench.py --hw-probe``): loads
+``lib/g950_probes.hsaco`` (``compiler_amd/csrc/g950_probes.hip``) with the HIP
+module API and reports, per probe, the mean over waves of the best-of-four
+``s_memtime`` cycle count, at 1, 4 and 8 waves per CU (one workgroup per CU,
+256 workgroups).  ``s_memtime`` counts shader-clock cycles; the ``clock``
+entry checks that against the 100 MHz real-time counter.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+from .build import PROBES
+
+RATE = {
+    "lds_b128": ("g950p_lds_b128", "64 ds_read_b128 (1 KiB each)", 64 * 1024),
+    "lds_tr_b16": ("g950p_lds_tr_b16", "64 ds_read_b64_tr_b16 (512 B each)", 64 * 512),
+    "exp": ("g950p_exp", "256 v_exp_f32, 8 chains", 0),
+    "fma": ("g950p_fma", "256 v_fma_f32, 8 chains", 0),
+    "mfma": ("g950p_mfma", "64 v_mfma_f32_32x32x16_bf16, 4 accumulators", 0),
+    "mfma_exp2": ("g950p_mfma_exp2", "64 MFMA, each + 2 v_exp_f32", 0),
+    "mfma_fma4": ("g950p_mfma_fma4", "64 MFMA, each + 4 v_fma_f32", 0),
+    "mfma_fma8": ("g950p_mfma_fma8", "64 MFMA, each + 8 v_fma_f32", 0),
+}
+ISSUE = {
+    "issue_lds_dma": ("g950p_issue_lds_dma", "8 global_load_lds_dwordx4 per wave"),
+    "issue_global": ("g950p_issue_global", "8 global_load_dwordx4 per wave"),
+}
+BLOCKS = 256
+
+
+class _Hip:
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.mod = ctypes.c_void_p()
+        path = Path(PROBES)
+        if not path.exists():
+            raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+        rc = self.lib.hipModuleLoad(ctypes.byref(self.mod), str(path).encode())
+        if rc:
+            raise RuntimeError(f"hipModuleLoad({path}) failed: {rc}")
+
+    def launch(self, name, threads, args, stream):
+        f = ctypes.c_void_p()
+        rc = self.lib.hipModuleGetFunction(ctypes.byref(f), self.mod, name.encode())
+        if rc:
+            raise RuntimeError(f"hipModuleGetFunction({name}) failed: {rc}")
+        vals = [ctypes.c_void_p(a) for a in args]
+        ptrs = (ctypes.c_void_p * len(vals))(*[ctypes.addressof(v) for v in vals])
+        rc = self.lib.hipModuleLaunchKernel(f, BLOCKS, 1, 1, threads, 1, 1, 0, stream, ptrs, None)
+        if rc:
+            raise RuntimeError(f"hipModuleLaunchKernel({name}) failed: {rc}")
+
+
+def run(torch) -> dict:
+    """All probes on cuda:0; returns {probe: {waves_per_cu: result}}."""
+    hip = _Hip()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = torch.zeros(BLOCKS * 16 * 2, dtype=torch.int64, device="cuda")
+    sink = torch.zeros(512 * 4, dtype=torch.int32, device="cuda")
+    res: dict = {}
+    for key, (name, what, nbytes) in RATE.items():
+        res[key] = {"what": what}
+        for waves in (1, 4, 8):
+            for _ in range(2):  # the second launch is the one kept
+                out.zero_()
+                hip.launch(name, 64 * waves, [out.data_ptr(), sink.data_ptr()], stream)
+                torch.cuda.synchronize()
+            cyc = out[: BLOCKS * 16].view(BLOCKS, 16)[:, :waves].double()
+            row = {"cycles": round(cyc.mean().item(), 1)}
+            if nbytes:
+                # bytes the workgroup's waves read / cycles of its slowest wave
+                row["bytes_per_clk_per_cu"] = round(nbytes * waves / cyc.max(dim=1).values.mean().item(), 1)
+            res[key][waves] = row
+    src = torch.zeros(BLOCKS * 16 * 8 * 1024 // 4, dtype=torch.float32, device="cuda").normal_()
+    for key, (name, what) in ISSUE.items():
+        res[key] = {"what": what}
+        for waves in (4, 8):
+            for _ in range(3):
+                out.zero_()
+                hip.launch(name, 64 * waves, [src.data_ptr(), out.data_ptr(), sink.data_ptr()], stream)
+                torch.cuda.synchronize()
+            o = out.view(BLOCKS, 16, 2)[:, :waves].double()
+            res[key][waves] = {"issue_cycles": round(o[..., 0].mean().item(), 1),
+                               "to_data_cycles": round(o[..., 1].mean().item(), 1)}
+    for _ in range(2):
+        out.zero_()
+        hip.launch("g950p_clock", 64, [out.data_ptr()], stream)
+        torch.cuda.synchronize()
+    c = out[: BLOCKS * 2].view(BLOCKS, 2).double()
+    res["clock"] = {"memtime_mhz": round(100.0 * c[:, 0].mean().item() / c[:, 1].mean().item(), 1)}
+    return res
