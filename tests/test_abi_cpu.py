@@ -28,6 +28,15 @@ def test_library_exports_every_declared_function():
         assert hasattr(lib, name), name
 
 
+def test_probe_code_object_holds_every_probe_kernel():
+    # bench.py --hw-probe launches these by name from the probe code object
+    from compiler_amd import probes
+    data = Path(probes.PROBES).read_bytes()
+    names = [n for n, *_ in probes.RATE.values()] + [n for n, _ in probes.ISSUE.values()] + ["g950p_clock"]
+    for name in names:
+        assert (name + ".kd").encode() in data, name
+
+
 def test_record_layouts_match_reference_abi():
     # a100c/runtime/a100rt.h:186-199 pins these sizes and offsets
     assert ctypes.sizeof(rt.View) == 56
