@@ -601,6 +601,17 @@ bool gemm_fast_ok(const View& a, const View& b, int K, int esz) {
 
 bool gemm_ktail(int K, int esz) { return (K * esz) % 128 != 0; }
 
+// The whole-slab MFMA kernels address a lane's DMA rows by 32-bit byte
+// offsets from the operand base (gemm.hip, gemm_mfma_body): the farthest row
+// either operand can reach plus a slab's last 16-byte chunk must lie below
+// 4 GiB, or the _kt kernels (64-bit addresses) serve the call.
+bool gemm_off32(const GemmArgs& g, int esz) {
+  auto fits = [esz](long long rows, long long s0) {
+    return (__int128)(rows - 1) * s0 * esz + 128 <= (__int128)0xFFFFFFFFll;
+  };
+  return fits(g.M, g.a_s0) && fits(g.N, g.b_s0);
+}
+
 // Row-major B[K,N] (N-contiguous, the reference matmul's layout,
 // ops/suite/perf/matmul.py:33) with A K-contiguous: B is copied once into a
 // K-contiguous Bt in the workspace (g950_transpose_b16) for the MFMA kernels.
@@ -646,14 +657,19 @@ int op_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g95
   const int esz = a.isz;
   const bool out16 = y.stride[1] == 1 && aligned16(y.addr());
   char mfma_name[48];
-  snprintf(mfma_name, sizeof mfma_name, "g950_gemm_%s_256x256%s", rr_dtype(a.v->dtype),
-           gemm_ktail((int)K, esz) ? "_kt" : "");
+  // (call once g.a_s0 / g.b_s0 hold the operand row strides)
+  auto mfma_kernel = [&]() -> const char* {
+    snprintf(mfma_name, sizeof mfma_name, "g950_gemm_%s_256x256%s", rr_dtype(a.v->dtype),
+             gemm_ktail((int)K, esz) || !gemm_off32(g, esz) ? "_kt" : "");
+    return mfma_name;
+  };
   if (same16 && gemm_fast_ok(a, b, (int)K, esz) && out16) {
     g.a_s0 = a.stride[0];
     g.b_s0 = b.stride[1];  // Bt row (n) stride
     const int tiles = gemm_tiles(g);
     if (tiles < 0) return fail(G950_USAGE, "matmul: too many tiles");
-    return launch(m, mfma_name, (unsigned)tiles, (unsigned)kernel_threads(m, mfma_name, 512), g, stream);
+    const char* name = mfma_kernel();
+    return launch(m, name, (unsigned)tiles, (unsigned)kernel_threads(m, name, 512), g, stream);
   }
   void* bt = nullptr;
   const size_t bt_bytes = (size_t)N * (size_t)K * esz;
@@ -673,7 +689,8 @@ int op_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g95
     g.b_s0 = K;
     const int tiles = gemm_tiles(g);
     if (tiles < 0) return fail(G950_USAGE, "matmul: too many tiles");
-    return launch(m, mfma_name, (unsigned)tiles, (unsigned)kernel_threads(m, mfma_name, 512), g, stream);
+    const char* name = mfma_kernel();
+    return launch(m, name, (unsigned)tiles, (unsigned)kernel_threads(m, name, 512), g, stream);
   }
   g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
   g.b_s0 = b.stride[0]; g.b_s1 = b.stride[1];
@@ -729,15 +746,16 @@ int op_matmul_i8(g950_module* m, const g950_view* views, uint32_t nviews, const 
   if (M == 0 || N == 0) return launch(m, "g950_gemm_general_i8", 0, 256, g, stream);
   const bool out_ok = dequant ? (y.stride[1] == 1 && aligned16(y.addr())) : aligned16(y.addr());
   // an unsigned operand's flipped bytes would read the zero tail as -128:
-  // the signedness variants need whole 128-byte K slabs
-  if (gemm_fast_ok(a, b, (int)K, 1) && out_ok && (umask == 0 || !gemm_ktail((int)K, 1))) {
-    g.a_s0 = a.stride[0];
-    g.b_s0 = b.stride[1];
+  // the signedness variants need whole 128-byte K slabs and 32-bit row
+  // offsets (they have no _kt form)
+  g.a_s0 = a.stride[0];
+  g.b_s0 = b.stride[1];
+  const bool ktail = gemm_ktail((int)K, 1) || !gemm_off32(g, 1);
+  if (gemm_fast_ok(a, b, (int)K, 1) && out_ok && (umask == 0 || !ktail)) {
     const int tiles = gemm_tiles(g);
     if (tiles < 0) return fail(G950_USAGE, "matmul_i8: too many tiles");
     static const char* const names[4] = {"g950_gemm_i8_256x256", "g950_gemm_u8s8_256x256",
                                          "g950_gemm_s8u8_256x256", "g950_gemm_u8u8_256x256"};
-    const bool ktail = gemm_ktail((int)K, 1);
     if (umask) {
       // the MFMA multiplies u - 128 for an unsigned operand: first the sums
       // over k its correction needs (A's rows if B is unsigned, B's columns
@@ -908,7 +926,9 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
     const int tiles = gemm_tiles(g);
     if (tiles < 0) return fail(G950_USAGE, "dequant_matmul: too many tiles");
     {
-      const char* name = bf16 ? "g950_gemm_bf16_256x256" : "g950_gemm_f16_256x256";
+      const bool off32 = gemm_off32(g, 2);
+      const char* name = bf16 ? (off32 ? "g950_gemm_bf16_256x256" : "g950_gemm_bf16_256x256_kt")
+                              : (off32 ? "g950_gemm_f16_256x256" : "g950_gemm_f16_256x256_kt");
       return launch(m, name, (unsigned)tiles, (unsigned)kernel_threads(m, name, 512), g, stream);
     }
   }

@@ -18,7 +18,9 @@
 //     of 64 KiB (A rows then B rows, 128-byte rows), filled by direct
 //     global->LDS 16-byte DMA (global_load_lds_dwordx4) of whole 128-byte
 //     lines (measured on MI355X: 64-byte row pieces cost the load path 1.5x
-//     per byte)
+//     per byte); the DMA takes a scalar base plus a fixed 32-bit lane offset
+//     and the fragment reads fixed per-lane LDS offsets plus immediates, so
+//     the main loop holds MFMAs, LDS reads, DMAs and scalar work only
 //   * the eight 16-byte chunks of a 128-byte LDS row are XOR-swizzled with
 //     (row >> 1) & 7, so the 32 rows an MFMA operand read touches spread over
 //     all 64 banks
@@ -38,6 +40,8 @@
 // inputs (fp32 FMA) or int8 (int32 exact); 64x64 tiles.  It serves the
 // reference's row-major-B fixtures and shapes the MFMA kernel refuses.
 #include "g950_common.h"
+
+#include <utility>
 
 namespace g950 {
 
@@ -235,6 +239,24 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   // w*GROUPS .. w*GROUPS+GROUPS-1, issued in two halves.
   const int dr = lane >> 3;
   const int dslot = lane & 7;
+  // Whole-slab kernels: a lane's DMA rows are fixed for the whole kernel, so
+  // its byte offsets from the operand base are computed once (32-bit: the
+  // host routes operands whose rows reach past 4 GiB to the _kt kernels) and
+  // each slab's source is a wave-uniform base plus that offset -- the
+  // scalar-base form of the load, no vector address arithmetic per DMA.  The
+  // empty asm re-defines the offset inside the loop so instruction selection
+  // sees the (scalar + 32-bit lane offset) shape there instead of a 64-bit
+  // address hoisted out of it.  _kt kernels keep 64-bit addresses.
+  uint32_t doff[GROUPS];
+#pragma unroll
+  for (int t = 0; t < GROUPS; ++t) {
+    const int rg = wave * GROUPS + t;
+    const bool is_a = rg < BM / 8;
+    const int row = (is_a ? rg : rg - BM / 8) * 8 + dr;
+    const int grow = min(row, is_a ? a_lim : b_lim);
+    const int chunk = dslot ^ ((row >> 1) & 7);
+    doff[t] = (uint32_t)((long long)grow * (is_a ? lda_b : ldb_b) + chunk * 16);
+  }
   auto issue = [&](int stage, int slab, int t0, int t1) {
     char* st = lds + stage * STAGE;
     const long long kb = (long long)slab * SLAB;
@@ -242,13 +264,18 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
     for (int t = t0; t < t1; ++t) {
       const int rg = wave * GROUPS + t;
       const bool is_a = rg < BM / 8;
-      const int row = (is_a ? rg : rg - BM / 8) * 8 + dr;
-      const int grow = min(row, is_a ? a_lim : b_lim);
-      const int chunk = dslot ^ ((row >> 1) & 7);
-      const char* src = (is_a ? abase : bbase) + (long long)grow * (is_a ? lda_b : ldb_b) + kb +
-                        chunk * 16;
-      if constexpr (KTAIL)
+      const char* src;
+      if constexpr (KTAIL) {
+        const int row = (is_a ? rg : rg - BM / 8) * 8 + dr;
+        const int grow = min(row, is_a ? a_lim : b_lim);
+        const int chunk = dslot ^ ((row >> 1) & 7);
+        src = (is_a ? abase : bbase) + (long long)grow * (is_a ? lda_b : ldb_b) + kb + chunk * 16;
         if (kb + chunk * 16 >= kbytes) src = (const char*)g950_zero_line;
+      } else {
+        const char* ub = (is_a ? abase : bbase) + kb;
+        asm volatile("" : "+v"(doff[t]));
+        src = ub + (uint64_t)doff[t];
+      }
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                        (__attribute__((address_space(3))) void*)(st + rg * 1024),
                                        16, 0, 0);
@@ -260,19 +287,25 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   const int g = lane >> 5;
   const int r = lane & 31;
   u32x4 af[2][FM], bfr[2][FN];
-  auto frags = [&](const char* st, int ks, int buf) {
-    const char* sb = st + BM * SLAB;
-    const int chunk = ks * 2 + g;
+  // Per-lane LDS offsets of k-step ks's fragments in stage s, computed once:
+  // the swizzle (row >> 1) & 7 depends on r alone (fragment rows start at
+  // multiples of 32), so fragment mi (ni) is that offset plus an immediate
+  // mi (ni) * 32 rows, and the loop does no address arithmetic.
+  int aoff[2][4], boff[2][4];
 #pragma unroll
-    for (int mi = 0; mi < FM; ++mi) {
-      const int row = wm * (BM / WM) + mi * 32 + r;
-      af[buf][mi] = *(const u32x4*)(st + row * SLAB + ((chunk ^ ((row >> 1) & 7)) << 4));
-    }
+  for (int s_ = 0; s_ < 2; ++s_)
 #pragma unroll
-    for (int ni = 0; ni < FN; ++ni) {
-      const int row = wn * (BN / WN) + ni * 32 + r;
-      bfr[buf][ni] = *(const u32x4*)(sb + row * SLAB + ((chunk ^ ((row >> 1) & 7)) << 4));
+    for (int ks = 0; ks < 4; ++ks) {
+      const int sw = ((((ks * 2 + g) ^ ((r >> 1) & 7))) << 4) + r * SLAB;
+      aoff[s_][ks] = s_ * STAGE + wm * (BM / WM) * SLAB + sw;
+      boff[s_][ks] = s_ * STAGE + BM * SLAB + wn * (BN / WN) * SLAB + sw;
     }
+  auto frags = [&](auto sc, int ks, int buf) {
+    constexpr int S = decltype(sc)::value;
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi) af[buf][mi] = *(const u32x4*)(lds + aoff[S][ks] + mi * 32 * SLAB);
+#pragma unroll
+    for (int ni = 0; ni < FN; ++ni) bfr[buf][ni] = *(const u32x4*)(lds + boff[S][ks] + ni * 32 * SLAB);
   };
   auto mfmas = [&](int buf) {
     if constexpr (UMASK & 1) {
@@ -316,29 +349,36 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   // kt + 1 have landed; k-step 3 then reads slab kt + 1's first fragments.
   // Past the end of K the DMA re-reads the last slab into a stage nobody
   // reads again, so the loop body has no branch.
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
   issue(0, 0, 0, GROUPS);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  frags(lds, 0, 0);
+  frags(S0{}, 0, 0);
   issue(1, min(1, last), 0, H);
   __builtin_amdgcn_s_waitcnt(0xc07f);
-  int cur = 0;
-  for (int kt = 0; kt < kslabs; ++kt) {
-    const char* st = lds + cur * STAGE;
-    const int nxt = cur ^ 1;
-    issue(nxt, min(kt + 1, last), H, GROUPS);
-    frags(st, 1, 1);
+  auto slab_iter = [&](auto cc, int kt) {
+    constexpr int CUR = decltype(cc)::value, NXT = CUR ^ 1;
+    issue(NXT, min(kt + 1, last), H, GROUPS);
+    frags(cc, 1, 1);
     kstep(0, H);
-    frags(st, 2, 0);
+    frags(cc, 2, 0);
     kstep(1, 0);
-    frags(st, 3, 1);
+    frags(cc, 3, 1);
     kstep(0, 0);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    issue(cur, min(kt + 2, last), 0, H);
-    frags(lds + nxt * STAGE, 0, 0);  // (after the last slab: a stale stage, never used)
+    issue(CUR, min(kt + 2, last), 0, H);
+    frags(std::integral_constant<int, NXT>{}, 0, 0);  // (after the last slab: a stale stage, never used)
     kstep(1, H);
-    cur = nxt;
+  };
+  // two slabs per trip, so each stage's fragment offsets are compile-time
+  // picks; an odd last slab runs from stage 0
+  int kt = 0;
+  for (; kt + 1 < kslabs; kt += 2) {
+    slab_iter(S0{}, kt);
+    slab_iter(S1{}, kt + 1);
   }
+  if (kt < kslabs) slab_iter(S0{}, kt);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   gemm_epilogue<MODE, FM, FN, UMASK>(p, accf, acci, m0 + wm * (BM / WM), n0 + wn * (BN / WN), r, g);

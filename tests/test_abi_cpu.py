@@ -394,6 +394,30 @@ def test_matmul_selection(m, n, k, colb, kernel):
     assert name == kernel
 
 
+def test_matmul_rows_past_4gib_take_64bit_kernels():
+    # the whole-slab kernels address DMA rows by 32-bit offsets from the
+    # operand base; a row stride that puts the last row at 4 GiB or beyond
+    # selects the _kt kernels (64-bit addresses), or the general kernel for
+    # unsigned int8 operands (no _kt form)
+    near = Args().view([2, 64], rt.DT_BF16, strides=[(1 << 31) - 128, 1]) \
+        .view([64, 64], rt.DT_BF16, strides=[1, 64]).view([2, 64], rt.DT_BF16, output=True)
+    rc, name, err = validate(rt.OP_MATMUL, near, [64, 2, 64])
+    assert rc == 0 and name == "g950_gemm_bf16_256x256", err
+    far = Args().view([2, 64], rt.DT_BF16, strides=[1 << 31, 1]) \
+        .view([64, 64], rt.DT_BF16, strides=[1, 64]).view([2, 64], rt.DT_BF16, output=True)
+    rc, name, err = validate(rt.OP_MATMUL, far, [64, 2, 64])
+    assert rc == 0 and name == "g950_gemm_bf16_256x256_kt", err
+    farb = Args().view([2, 64], rt.DT_BF16).view([64, 2], rt.DT_BF16, strides=[1, 1 << 31]) \
+        .view([2, 2], rt.DT_BF16, output=True)
+    rc, name, err = validate(rt.OP_MATMUL, farb, [64, 2, 2])
+    assert rc == 0 and name == "g950_gemm_bf16_256x256_kt", err
+    for adt, want in ((rt.DT_INT8, "g950_gemm_i8_256x256_kt"), (rt.DT_UINT8, "g950_gemm_general_i8")):
+        c = (Args().view([2, 128], adt, strides=[1 << 32, 1]).view([128, 64], rt.DT_INT8, strides=[1, 128])
+             .view([2, 64], rt.DT_INT32, output=True))
+        rc, name, err = validate(rt.OP_MATMUL_I8, c, [128, 2, 64])
+        assert rc == 0 and name == want, err
+
+
 def test_matmul_fp32_and_int8_tails():
     # fp32 operands (the corpus base dtype) take the fp32 MFMA kernel in both B
     # layouts; mixed operand dtypes and unaligned rows the general kernel
