@@ -27,8 +27,9 @@
 //   * per slab: four k-steps; each k-step's MFMAs run with the next k-step's
 //     fragment reads (second register set) spread between them, and the
 //     slab's DMA is spread over k-step 3 of the previous slab and k-step 0
-//     (sched_group_barrier), so no wave stalls issuing a burst of loads while
-//     its MFMAs wait behind it; one workgroup barrier per slab, before k-step 3
+//     (sched_group_barrier), issued by one wave of each SIMD only, so the
+//     other wave's MFMAs fill the matrix core while the DMA wave waits on the
+//     load path; one workgroup barrier per slab, before k-step 3
 //   * XCD-aware block order: consecutive tiles go to the same XCD (the
 //     hardware deals workgroups round-robin over 8 XCDs), grouped 4 tile-rows
 //     deep for L2 reuse (4 beat 2, 8, 16 and 32 at 8192^3)
@@ -197,9 +198,10 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   constexpr int FM = BM / WM / 32;
   constexpr int FN = BN / WN / 32;
   constexpr int STAGE = (BM + BN) * SLAB;     // 64 KiB
-  constexpr int GROUPS = (BM + BN) / 8 / NW;  // 8-row DMA groups per wave per slab
+  constexpr int DW = NW / 2;                  // DMA waves: the first half, one per SIMD
+  constexpr int GROUPS = (BM + BN) / 8 / DW;  // 8-row DMA groups per DMA wave per slab
   constexpr int H = GROUPS / 2;
-  static_assert(GROUPS * 8 * NW == BM + BN && GROUPS % 2 == 0, "DMA split over waves and halves");
+  static_assert(GROUPS * 8 * DW == BM + BN && GROUPS % 2 == 0, "DMA split over waves and halves");
   __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -235,8 +237,13 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
 
   // DMA: one wave instruction moves 8 rows x 128 bytes (lane: row lane / 8,
   // 16-byte slot lane % 8, which holds the swizzled chunk).  Row groups
-  // 0..BM/8-1 are A rows, the rest B rows; wave w owns groups
-  // w*GROUPS .. w*GROUPS+GROUPS-1, issued in two halves.
+  // 0..BM/8-1 are A rows, the rest B rows; DMA wave w (w < DW) owns groups
+  // w*GROUPS .. w*GROUPS+GROUPS-1, issued in two halves.  Waves are dealt to
+  // the four SIMDs round-robin, so each SIMD pairs one DMA wave with one
+  // wave that only multiplies: while the DMA wave waits on the load path
+  // (every wave issuing at once left both waves of a SIMD stalled together),
+  // the other keeps the matrix core busy (measured on MI355X at 8192^3:
+  // 1361 -> 1415 TFLOP/s).
   const int dr = lane >> 3;
   const int dslot = lane & 7;
   // Whole-slab kernels: a lane's DMA rows are fixed for the whole kernel, so
@@ -345,40 +352,49 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   // iteration kt - 1, its second half in k-step 0 of iteration kt, both past
   // the barrier after which nobody reads slab kt - 1 again.  The barrier
   // before k-step 3 comes after every read of slab kt (the k-step 3
-  // fragments are read during k-step 2) and after this wave's DMAs of slab
-  // kt + 1 have landed; k-step 3 then reads slab kt + 1's first fragments.
+  // fragments are read during k-step 2) and after each DMA wave's loads of
+  // slab kt + 1 have landed (its vmcnt(0) just before the barrier); k-step 3
+  // then reads slab kt + 1's first fragments.
   // Past the end of K the DMA re-reads the last slab into a stage nobody
   // reads again, so the loop body has no branch.
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
-  issue(0, 0, 0, GROUPS);
+  const bool dwave = wave < DW;
+  if (dwave) issue(0, 0, 0, GROUPS);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   frags(S0{}, 0, 0);
-  issue(1, min(1, last), 0, H);
+  if (dwave) issue(1, min(1, last), 0, H);
   __builtin_amdgcn_s_waitcnt(0xc07f);
-  auto slab_iter = [&](auto cc, int kt) {
-    constexpr int CUR = decltype(cc)::value, NXT = CUR ^ 1;
-    issue(NXT, min(kt + 1, last), H, GROUPS);
-    frags(cc, 1, 1);
-    kstep(0, H);
-    frags(cc, 2, 0);
-    kstep(1, 0);
-    frags(cc, 3, 1);
-    kstep(0, 0);
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    issue(CUR, min(kt + 2, last), 0, H);
-    frags(std::integral_constant<int, NXT>{}, 0, 0);  // (after the last slab: a stale stage, never used)
-    kstep(1, H);
+  // the main loop in two compiled forms, with and without the DMA: same
+  // barriers, so the two wave roles stay in step slab by slab; two slabs per
+  // trip, so each stage's fragment offsets are compile-time picks (an odd
+  // last slab runs from stage 0)
+  auto run = [&](auto dc) {
+    constexpr bool DMA = decltype(dc)::value;
+    auto slab_iter = [&](auto cc, int kt) {
+      constexpr int CUR = decltype(cc)::value, NXT = CUR ^ 1;
+      if constexpr (DMA) issue(NXT, min(kt + 1, last), H, GROUPS);
+      frags(cc, 1, 1);
+      kstep(0, DMA ? H : 0);
+      frags(cc, 2, 0);
+      kstep(1, 0);
+      frags(cc, 3, 1);
+      kstep(0, 0);
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (DMA) issue(CUR, min(kt + 2, last), 0, H);
+      frags(std::integral_constant<int, NXT>{}, 0, 0);  // (after the last slab: a stale stage, never used)
+      kstep(1, DMA ? H : 0);
+    };
+    int kt = 0;
+    for (; kt + 1 < kslabs; kt += 2) {
+      slab_iter(S0{}, kt);
+      slab_iter(S1{}, kt + 1);
+    }
+    if (kt < kslabs) slab_iter(S0{}, kt);
   };
-  // two slabs per trip, so each stage's fragment offsets are compile-time
-  // picks; an odd last slab runs from stage 0
-  int kt = 0;
-  for (; kt + 1 < kslabs; kt += 2) {
-    slab_iter(S0{}, kt);
-    slab_iter(S1{}, kt + 1);
-  }
-  if (kt < kslabs) slab_iter(S0{}, kt);
+  if (dwave) run(std::true_type{});
+  else run(std::false_type{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   gemm_epilogue<MODE, FM, FN, UMASK>(p, accf, acci, m0 + wm * (BM / WM), n0 + wn * (BN / WN), r, g);
