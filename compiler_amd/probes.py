@@ -23,6 +23,9 @@ RATE = {
     "mfma_exp2": ("g950p_mfma_exp2", "64 MFMA, each + 2 v_exp_f32", 0),
     "mfma_fma4": ("g950p_mfma_fma4", "64 MFMA, each + 4 v_fma_f32", 0),
     "mfma_fma8": ("g950p_mfma_fma8", "64 MFMA, each + 8 v_fma_f32", 0),
+    "mfma_lds": ("g950p_mfma_lds", "64 MFMA, each + 1 ds_read_b128 (4 in flight)", 0),
+    "mfma_mix": ("g950p_mfma_mix", "64 MFMA, each + one softmax step (fma, exp, add, 1/2 cvt_pk, 9/16 max3)", 0),
+    "mfma_mix_lds": ("g950p_mfma_mix_lds", "64 MFMA, each + the softmax step + 1 ds_read_b128", 0),
 }
 ISSUE = {
     "issue_lds_dma": ("g950p_issue_lds_dma", "8 global_load_lds_dwordx4 per wave"),
