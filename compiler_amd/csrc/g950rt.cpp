@@ -201,7 +201,13 @@ hipFunction_t function(g950_module* m, const std::string& name) {
   auto it = m->fns.find(name);
   if (it != m->fns.end()) return it->second;
   hipFunction_t f = nullptr;
-  if (hipModuleGetFunction(&f, m->mod, name.c_str()) != hipSuccess) return nullptr;
+  if (hipModuleGetFunction(&f, m->mod, name.c_str()) != hipSuccess) {
+    // a kernel the code object does not hold is an answer, not an error:
+    // clear the thread's last-error state so the caller's next check (a
+    // framework's launch check, say) does not report it
+    (void)hipGetLastError();
+    return nullptr;
+  }
   m->fns.emplace(name, f);
   return f;
 }

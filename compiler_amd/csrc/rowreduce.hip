@@ -186,13 +186,29 @@ template <> struct RawIO<f16_t, 8> : RawIO16<f16_t> {};
 template <> struct RawIO<bf16_t, 1> : RawIO16s<bf16_t> {};
 template <> struct RawIO<f16_t, 1> : RawIO16s<f16_t> {};
 
-// e^x.  fp32 rows keep libm expf (about 1 ulp); 16-bit rows,
-// whose results are rounded to 8 or 11 mantissa bits, use v_exp_f32 on
-// x*log2(e) (relative error ~1e-6 for |x| < 20, far inside one bf16/fp16 ulp).
-template <typename T>
-__device__ __forceinline__ float row_exp(float x) {
-  if constexpr (sizeof(T) == 4) return expf(x);
-  else return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+// e^(x - m) with v_exp_f32.  FMA form (|m| < 2^24): exp2(fma(x, log2(e),
+// -mL)) with mL = m * log2(e) rounded, one rounding before the exponential.
+// The rounding of mL (at most half an ulp of mL, <= 1 below 2^24 * log2(e))
+// shifts every exponent of a row by the same amount, which the softmax
+// normalisation cancels (and which moves a logsumexp by |m| * 2^-24); the
+// fma's own rounding gives a relative error of |x - m| * 2^-24 (6e-7 at
+// x - m = -10) on top of v_exp_f32's ~1 ulp -- inside the fp32 bar of 1e-5
+// relative.  Larger or infinite m: exp2((x - m) * log2(e)), the same error
+// bound with two roundings (the FMA form's shift would leave the exponent
+// range).  Masked lanes (x = -inf, m finite) give 0; an infinite m gives
+// NaN where x is infinite too, as x - m does.
+constexpr float kLog2e = 1.4426950408889634f;
+template <bool FMA>
+__device__ __forceinline__ float row_exp(float x, float m, float mL) {
+  if constexpr (FMA) return __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -mL));
+  else return __builtin_amdgcn_exp2f((x - m) * kLog2e);
+}
+// calls f(std::true_type) when |m| < 2^24 (the FMA form of row_exp
+// applies), f(std::false_type) otherwise: one wave-uniform branch
+template <class F>
+__device__ __forceinline__ void with_exp_form(float m, F&& f) {
+  if (__builtin_fabsf(m) < 16777216.0f) f(std::true_type{});
+  else f(std::false_type{});
 }
 
 // v rounded to T's precision (the value a store of T would keep)
@@ -257,29 +273,42 @@ __device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)
     nan = block_reduce<OpMax, BLOCK>(nan, scratch);
     float s = 0.0f;
     if (__builtin_fabsf(m) != __builtin_huge_valf()) {
+      const float mL = m * kLog2e;
+      with_exp_form(m, [&](auto fc) {
+        constexpr bool F = decltype(fc)::value;
 #pragma unroll
-      for (int i = 0; i < ITEMS; ++i)
+        for (int i = 0; i < ITEMS; ++i)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) s += row_exp<T>(v[i][e] - m);  // tail: exp(-inf) = 0
+          for (int e = 0; e < VEC; ++e) s += row_exp<F>(v[i][e], m, mL);  // tail: exp(-inf) = 0
+      });
     }
     s = block_reduce<OpSum, BLOCK>(s, scratch);
     if (tid == 0)
       store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, lse_finish(m, s, nan != 0.0f));
   } else if constexpr (OP == ROW_SOFTMAX) {
-    float m = -__builtin_huge_valf();
+    // four independent max and sum chains per lane (a dependent VALU
+    // operation waits ~11 cycles on gfx950)
+    float m4[4] = {-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf(),
+                   -__builtin_huge_valf()};
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) m = fmaxf(m, v[i][e]);
+      for (int e = 0; e < VEC; ++e) m4[(i * VEC + e) & 3] = fmaxf(m4[(i * VEC + e) & 3], v[i][e]);
+    float m = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
     m = block_reduce<OpMax, BLOCK>(m, scratch);
-    float s = 0.0f;
+    const float mL = m * kLog2e;
+    float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    with_exp_form(m, [&](auto fc) {
+      constexpr bool F = decltype(fc)::value;
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i)
+      for (int i = 0; i < ITEMS; ++i)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        v[i][e] = row_exp<T>(v[i][e] - m);  // masked lanes: exp(-inf) = 0
-        s += v[i][e];
-      }
+        for (int e = 0; e < VEC; ++e) {
+          v[i][e] = row_exp<F>(v[i][e], m, mL);  // masked lanes: exp(-inf) = 0
+          s4[(i * VEC + e) & 3] += v[i][e];
+        }
+    });
+    float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
     s = block_reduce<OpSum, BLOCK>(s, scratch);
     const float inv = 1.0f / s;
 #pragma unroll
@@ -292,11 +321,12 @@ __device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)
       }
     }
   } else if constexpr (OP == ROW_RMSNORM) {
-    float ss = 0.0f;
+    float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four independent chains
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) ss = fmaf(v[i][e], v[i][e], ss);
+      for (int e = 0; e < VEC; ++e) s4[(i * VEC + e) & 3] = fmaf(v[i][e], v[i][e], s4[(i * VEC + e) & 3]);
+    float ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
     ss = block_reduce<OpSum, BLOCK>(ss, scratch);
     const float inv = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
     if (tid == 0) store_from_f32(a.stat0, (long long)row * a.stat0_stride, a.stat_dtype, inv);
@@ -312,14 +342,15 @@ __device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)
     }
   } else if constexpr (OP == ROW_LNROW) {
     // both sums in one pass (the reference's E[x^2] - mean^2 form)
-    float s = 0.0f, q = 0.0f;
+    float s2[2] = {0.0f, 0.0f}, q2[2] = {0.0f, 0.0f};  // two chains each
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
-        s += v[i][e];
-        q = fmaf(v[i][e], v[i][e], q);
+        s2[e & 1] += v[i][e];
+        q2[e & 1] = fmaf(v[i][e], v[i][e], q2[e & 1]);
       }
+    float s = s2[0] + s2[1], q = q2[0] + q2[1];
     s = block_reduce<OpSum, BLOCK>(s, scratch);
     q = block_reduce<OpSum, BLOCK>(q, scratch);
     const float inv_n = 1.0f / (float)a.cols;
@@ -340,14 +371,15 @@ __device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)
       }
     }
   } else {  // LayerNorm, centered two-pass from registers
-    float s = 0.0f;
+    float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four independent chains
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) s += v[i][e];
+      for (int e = 0; e < VEC; ++e) s4[(i * VEC + e) & 3] += v[i][e];
+    float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
     s = block_reduce<OpSum, BLOCK>(s, scratch);
     const float mean = s / (float)a.cols;
-    float q = 0.0f;
+    float q4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
       if (eg.live(i)) {
@@ -355,11 +387,12 @@ __device__ __forceinline__ void row_finish(const RowArgs& a, int row, float (&v)
         for (int e = 0; e < VEC; ++e) {
           if (eg.ok(i, e)) {
             v[i][e] -= mean;
-            q = fmaf(v[i][e], v[i][e], q);
+            q4[(i * VEC + e) & 3] = fmaf(v[i][e], v[i][e], q4[(i * VEC + e) & 3]);
           }
         }
       }
     }
+    float q = (q4[0] + q4[1]) + (q4[2] + q4[3]);
     q = block_reduce<OpSum, BLOCK>(q, scratch);
     const float rstd = 1.0f / sqrtf(q / (float)a.cols + a.eps);
     if (tid == 0) {
@@ -740,7 +773,7 @@ __device__ __forceinline__ void rs_part_body(const RowArgs& a) {
 #pragma unroll
       for (int i = 0; i < RS_ITEMS; ++i)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) z += row_exp<T>(v[i][e] - m);
+        for (int e = 0; e < VEC; ++e) z += row_exp<false>(v[i][e], m, 0.0f);
     }
     z = block_reduce<OpSum, RS_BLOCK>(z, scratch);
     p[0] = m; p[1] = z; p[2] = nan;
@@ -886,7 +919,7 @@ __device__ __forceinline__ void rs_final_body(const RowArgs& a) {
       float o[VEC];
       if constexpr (OP == ROW_SOFTMAX) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) o[e] = row_exp<T>(v[i][e] - sub) * mul;
+        for (int e = 0; e < VEC; ++e) o[e] = row_exp<false>(v[i][e], sub, 0.0f) * mul;
       } else if constexpr (OP == ROW_RMSNORM) {
         float w[VEC];
         load_param<T, VEC>(a.w, (long long)j * VEC, w);

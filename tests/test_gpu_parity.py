@@ -228,6 +228,35 @@ def test_logsumexp_special_rows(cols):
     close(y[fin], e[fin], 3e-5, 3e-6)
 
 
+@pytest.mark.parametrize("dt", ["float32", "bfloat16"])
+@pytest.mark.parametrize("cols", [97, 3000, 4096])
+def test_softmax_special_rows(dt, cols):
+    """Rows with huge maxima (|max| >= 2^24: the exponent takes its
+    two-rounding form), a row just below that bound (the fma form, whose
+    rounded max*log2(e) shifts the whole row's exponents alike), an +inf
+    entry (NaN row), an all -inf row (NaN, 0/0), a partly -inf row, and a
+    huge row with three tied maxima beside ordinary values (1/3 at the
+    maxima, 0 elsewhere)."""
+    rng = np.random.default_rng(cols + 1)
+    x = rng.standard_normal((8, cols)).astype(np.float32)
+    x[0, :] = 3.0e38
+    x[1, :] = -3.0e38
+    x[2, cols // 2] = np.inf
+    x[3, :] = -np.inf
+    x[4, : cols // 3] = -np.inf
+    x[5, [0, cols // 2, cols - 1]] = 2.5e38
+    x[6, :] = 1.5e38 + 0.0 * x[6, :]
+    x[7, :] = 1.6e7 + 4.0 * x[7, :]
+    if dt == "bfloat16":
+        x = ref.bf16_round(x)
+    y = host(ops.softmax(dev(x, dt), sync=True)).astype(np.float64)
+    e = ref.softmax(x)
+    assert np.array_equal(np.isnan(y), np.isnan(e))
+    assert np.isnan(y[[2, 3]]).all()
+    fin = ~np.isnan(e)
+    close(y[fin], e[fin], *((1e-5, 1e-6) if dt == "float32" else (1e-2, 1e-2)))
+
+
 def _dq_expect(b, s, dt):
     p = ref.dequantize(b, s)
     if dt == "bfloat16":
