@@ -86,79 +86,157 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
                                               const i32x16 (&acci)[FM][FN], int wm0, int wn0,
                                               int r, int g) {
   const bool vec_ok = ((p.c_s0 & 3) == 0);
+  // per-row factors
+  bool live[FM];
+  float rs[FM];
+  uint32_t rcorr[FM];
 #pragma unroll
   for (int mi = 0; mi < FM; ++mi) {
     const int m = wm0 + mi * 32 + r;
-    if (m >= p.M) continue;
-    float rs = 1.0f;
-    if constexpr (MODE == GEMM_I8) rs = p.sa ? p.sa[m] : 1.0f;
-    uint32_t rcorr = 0;
-    if constexpr (MODE == GEMM_I8 && (UMASK & 2)) rcorr = 128u * (uint32_t)p.rsum[m];
-    if constexpr (MODE == GEMM_I8 && UMASK == 3) rcorr -= 16384u * (uint32_t)p.K;
+    live[mi] = m < p.M;
+    rs[mi] = 1.0f;
+    rcorr[mi] = 0;
+    if constexpr (MODE == GEMM_I8) {
+      if (live[mi] && p.sa) rs[mi] = p.sa[m];
+      if constexpr (UMASK & 2) rcorr[mi] = live[mi] ? 128u * (uint32_t)p.rsum[m] : 0u;
+      if constexpr (UMASK == 3) rcorr[mi] -= 16384u * (uint32_t)p.K;
+    }
+  }
+  // one group: C[m][n..n+3] of fragment (mi, ni), column factors colf
+  // (sb for int8, cscale for the 16-bit / fp32 GEMMs) and colc (128 * csum)
+  auto group = [&](int mi, int ni, int q, int n, bool full, const float (&colf)[4], const uint32_t (&colc)[4]) {
+    const int m = wm0 + mi * 32 + r;
+    float v[4];
+    if constexpr (MODE == GEMM_I8) {
+      int iv[4];
 #pragma unroll
-    for (int ni = 0; ni < FN; ++ni) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = wn0 + ni * 32 + q * 8 + g * 4;
-        float v[4];
-        if constexpr (MODE == GEMM_I8) {
-          int iv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            uint32_t c = rcorr;
-            if constexpr (UMASK & 1) c += (n + e < p.N) ? 128u * (uint32_t)p.csum[n + e] : 0u;
-            iv[e] = (int)((uint32_t)acci[mi][ni][q * 4 + e] + c);
-          }
-          if (p.acc_out) {
-            int* dst = p.acc_out + (long long)m * p.acc_s0 + n;
-            if (((p.acc_s0 & 3) == 0) && n + 3 < p.N) {
-              *(i32x4*)dst = (i32x4){iv[0], iv[1], iv[2], iv[3]};
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (n + e < p.N) dst[e] = iv[e];
-            }
-          }
-          if (!p.sa) continue;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float sbv = (n + e < p.N) ? p.sb[n + e] : 0.0f;
-            v[e] = ((float)iv[e] * rs) * sbv;
-          }
+      for (int e = 0; e < 4; ++e) iv[e] = (int)((uint32_t)acci[mi][ni][q * 4 + e] + rcorr[mi] + colc[e]);
+      if (p.acc_out) {
+        int* dst = p.acc_out + (long long)m * p.acc_s0 + n;
+        if (((p.acc_s0 & 3) == 0) && full) {
+          *(i32x4*)dst = (i32x4){iv[0], iv[1], iv[2], iv[3]};
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = accf[mi][ni][q * 4 + e];
-          if (p.cscale) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              v[e] *= (n + e < p.N) ? load_as_f32(p.cscale, n + e, p.cscale_dtype) : 0.0f;
-          }
-        }
-        char* crow = (char*)p.c + (long long)m * p.c_s0 * (p.c_dtype == DT_F32 ? 4 : 2);
-        if (p.c_dtype == DT_F32) {
-          float* dst = (float*)crow + n;
-          if (vec_ok && n + 3 < p.N) {
-            *(f32x4*)dst = (f32x4){v[0], v[1], v[2], v[3]};
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (n + e < p.N) dst[e] = v[e];
-          }
-        } else {
-          uint16_t h[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = (p.c_dtype == DT_BF16) ? f32_to_bf16(v[e]) : f32_to_f16(v[e]);
-          uint16_t* dst = (uint16_t*)crow + n;
-          if (vec_ok && n + 3 < p.N) {
-            *(u32x2*)dst = (u32x2){(uint32_t)h[0] | ((uint32_t)h[1] << 16),
-                                   (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (n + e < p.N) dst[e] = h[e];
-          }
+          for (int e = 0; e < 4; ++e)
+            if (n + e < p.N) dst[e] = iv[e];
         }
       }
+      if (!p.sa) return;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = ((float)iv[e] * rs[mi]) * colf[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = accf[mi][ni][q * 4 + e];
+      if (p.cscale) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] *= colf[e];
+      }
+    }
+    char* crow = (char*)p.c + (long long)m * p.c_s0 * (p.c_dtype == DT_F32 ? 4 : 2);
+    if (p.c_dtype == DT_F32) {
+      float* dst = (float*)crow + n;
+      if (vec_ok && full) {
+        *(f32x4*)dst = (f32x4){v[0], v[1], v[2], v[3]};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < p.N) dst[e] = v[e];
+      }
+    } else {
+      uint16_t h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = (p.c_dtype == DT_BF16) ? f32_to_bf16(v[e]) : f32_to_f16(v[e]);
+      uint16_t* dst = (uint16_t*)crow + n;
+      if (vec_ok && full) {
+        *(u32x2*)dst = (u32x2){(uint32_t)h[0] | ((uint32_t)h[1] << 16),
+                               (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < p.N) dst[e] = h[e];
+      }
+    }
+  };
+  const bool colwise = MODE == GEMM_I8 || p.cscale;
+  if (!colwise) {
+    // no column factors: row by row, the stores of a row back to back
+    const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    const uint32_t zero[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi) {
+      if (!live[mi]) continue;
+#pragma unroll
+      for (int ni = 0; ni < FN; ++ni)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = wn0 + ni * 32 + q * 8 + g * 4;
+          group(mi, ni, q, n, n + 3 < p.N, one, zero);
+        }
+    }
+    return;
+  }
+  // column factors: loaded once per group of four columns and shared by the
+  // fragment rows, as one vector load where the group lies inside N and the
+  // vector is aligned -- a scalar load per element cost a load-path slot
+  // each (128 per lane per tile for the int8 dequant scale)
+  const bool sb_vec = MODE == GEMM_I8 && p.sb && ((uintptr_t)p.sb & 15) == 0;
+  const bool cs_vec = MODE != GEMM_I8 && p.cscale &&
+                      ((uintptr_t)p.cscale & (p.cscale_dtype == DT_F32 ? 15 : 7)) == 0;
+  const bool csum_vec = (UMASK & 1) && ((uintptr_t)p.csum & 15) == 0;
+#pragma unroll
+  for (int ni = 0; ni < FN; ++ni) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = wn0 + ni * 32 + q * 8 + g * 4;
+      if (n >= p.N) continue;
+      const bool full = n + 3 < p.N;
+      float colf[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+      uint32_t colc[4] = {0u, 0u, 0u, 0u};
+      if constexpr (MODE == GEMM_I8) {
+        if (p.sa) {
+          if (sb_vec && full) {
+            const f32x4 t = *(const f32x4*)(p.sb + n);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) colf[e] = t[e];
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) colf[e] = (n + e < p.N) ? p.sb[n + e] : 0.0f;
+          }
+        }
+        if constexpr (UMASK & 1) {
+          if (csum_vec && full) {
+            const i32x4 t = *(const i32x4*)(p.csum + n);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) colc[e] = 128u * (uint32_t)t[e];
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) colc[e] = (n + e < p.N) ? 128u * (uint32_t)p.csum[n + e] : 0u;
+          }
+        }
+      } else {
+        if (cs_vec && full) {
+          if (p.cscale_dtype == DT_F32) {
+            const f32x4 t = *(const f32x4*)((const float*)p.cscale + n);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) colf[e] = t[e];
+          } else {
+            const u32x2 t = *(const u32x2*)((const uint16_t*)p.cscale + n);
+            const bool bf = p.cscale_dtype == DT_BF16;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint16_t hb = (uint16_t)(t[e >> 1] >> (16 * (e & 1)));
+              colf[e] = bf ? bf16_to_f32(hb) : f16_to_f32(hb);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            colf[e] = (n + e < p.N) ? load_as_f32(p.cscale, n + e, p.cscale_dtype) : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int mi = 0; mi < FM; ++mi)
+        if (live[mi]) group(mi, ni, q, n, full, colf, colc);
     }
   }
 }
