@@ -53,6 +53,11 @@ enum GemmMode : int { GEMM_BF16 = 0, GEMM_F16 = 1, GEMM_I8 = 2, GEMM_F32 = 3 };
 // one value per lane) takes the chunk's four values in four MFMAs
 constexpr int mfma_per_chunk(int mode) { return mode == GEMM_F32 ? 4 : 1; }
 
+// 1: whole-slab 16-bit / int8 GEMMs with M, N >= 256 run on 16x16 output
+// fragments (gemm_mfma16_body); 0: every shape on the 32x32 form
+#ifndef G950_GEMM16
+#define G950_GEMM16 1
+#endif
 constexpr int BM = 256, BN = 256;  // workgroup tile
 constexpr int SLAB = 128;          // bytes of K per row per LDS stage (two stages)
 
@@ -81,10 +86,16 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& 
 // output row / column of the wave's tile.  UMASK (int8 only): bit 0 A
 // unsigned, bit 1 B unsigned -- the accumulator of the offset operands gets
 // its exact correction (modulo 2^32, GemmArgs::rsum / csum).
-template <int MODE, int FM, int FN, int UMASK = 0>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&accf)[FM][FN],
-                                              const i32x16 (&acci)[FM][FN], int wm0, int wn0,
-                                              int r, int g) {
+template <int MODE, int FM, int FN, int UMASK = 0, int RF = 32, class FA = f32x16, class IA = i32x16>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const FA (&accf)[FM][FN],
+                                              const IA (&acci)[FM][FN], int wm0, int wn0,
+                                              int lane, int m_lo = 0, int n_lo = 0) {
+  // only rows >= m_lo and columns >= n_lo are stored (a tile computed over a
+  // window shifted back from the matrix edge owns only its own part)
+  // RF x RF output fragments: lane holds C[m][n..n+3] for m = row lane % RF of
+  // each fragment and n = 4 * (lane / RF) + (64 / RF) * 4 * q, q < QN
+  constexpr int QN = RF * RF / 256;
+  const int r = lane % RF, g = lane / RF;
   const bool vec_ok = ((p.c_s0 & 3) == 0);
   // per-row factors
   bool live[FM];
@@ -92,8 +103,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
   uint32_t rcorr[FM];
 #pragma unroll
   for (int mi = 0; mi < FM; ++mi) {
-    const int m = wm0 + mi * 32 + r;
-    live[mi] = m < p.M;
+    const int m = wm0 + mi * RF + r;
+    live[mi] = m < p.M && m >= m_lo;
     rs[mi] = 1.0f;
     rcorr[mi] = 0;
     if constexpr (MODE == GEMM_I8) {
@@ -105,7 +116,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
   // one group: C[m][n..n+3] of fragment (mi, ni), column factors colf
   // (sb for int8, cscale for the 16-bit / fp32 GEMMs) and colc (128 * csum)
   auto group = [&](int mi, int ni, int q, int n, bool full, const float (&colf)[4], const uint32_t (&colc)[4]) {
-    const int m = wm0 + mi * 32 + r;
+    const int m = wm0 + mi * RF + r;
     float v[4];
     if constexpr (MODE == GEMM_I8) {
       int iv[4];
@@ -118,7 +129,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (n + e < p.N) dst[e] = iv[e];
+            if (n + e < p.N && n + e >= n_lo) dst[e] = iv[e];
         }
       }
       if (!p.sa) return;
@@ -140,7 +151,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (n + e < p.N) dst[e] = v[e];
+          if (n + e < p.N && n + e >= n_lo) dst[e] = v[e];
       }
     } else {
       uint16_t h[4];
@@ -153,7 +164,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (n + e < p.N) dst[e] = h[e];
+          if (n + e < p.N && n + e >= n_lo) dst[e] = h[e];
       }
     }
   };
@@ -168,9 +179,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
 #pragma unroll
       for (int ni = 0; ni < FN; ++ni)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int n = wn0 + ni * 32 + q * 8 + g * 4;
-          group(mi, ni, q, n, n + 3 < p.N, one, zero);
+        for (int q = 0; q < QN; ++q) {
+          const int n = wn0 + ni * RF + q * (256 / RF) + g * 4;
+          if (n + 3 < n_lo) continue;
+          group(mi, ni, q, n, n + 3 < p.N && n >= n_lo && (n & 3) == 0, one, zero);
         }
     }
     return;
@@ -186,10 +198,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const f32x16 (&
 #pragma unroll
   for (int ni = 0; ni < FN; ++ni) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = wn0 + ni * 32 + q * 8 + g * 4;
-      if (n >= p.N) continue;
-      const bool full = n + 3 < p.N;
+    for (int q = 0; q < QN; ++q) {
+      const int n = wn0 + ni * RF + q * (256 / RF) + g * 4;
+      if (n >= p.N || n + 3 < n_lo) continue;
+      const bool full = n + 3 < p.N && n >= n_lo && (n & 3) == 0;
       float colf[4] = {1.0f, 1.0f, 1.0f, 1.0f};
       uint32_t colc[4] = {0u, 0u, 0u, 0u};
       if constexpr (MODE == GEMM_I8) {
@@ -266,6 +278,187 @@ __device__ __forceinline__ void mfma_step(const u32x4& bfrag, const u32x4& afrag
   }
 }
 
+// 16x16-fragment form of the 256x256 kernel, for M and N of at least one
+// tile: a tile at the bottom / right edge computes the 256 x 256 window
+// ending at the matrix edge (every DMA row lies inside the operands, so a
+// lane's DMA source is a fixed 32-bit offset plus a wave-uniform base, no
+// per-row clamp) and stores only its own rows and columns.
+template <int MODE, int WM, int WN, int UMASK>
+__device__ __forceinline__ void gemm_mfma16_body(const GemmArgs& p, char* lds) {
+  constexpr int NW = WM * WN;
+  constexpr int STAGE = (BM + BN) * SLAB;     // 64 KiB
+  constexpr int DW = NW / 2;                  // DMA waves: the first half, one per SIMD
+  constexpr int GROUPS = (BM + BN) / 8 / DW;  // 8-row DMA groups per DMA wave per slab
+  constexpr int H = GROUPS / 2;
+  static_assert(GROUPS * 8 * DW == BM + BN && GROUPS % 2 == 0 && (BM / 8) % GROUPS == 0,
+                "each DMA wave's groups lie in one operand");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m_own = tm * BM, n_own = tn * BN;
+  const int m0 = min(m_own, p.M - BM);  // the window the tile computes
+  const int n0 = min(n_own, p.N - BN);
+  constexpr int ES = (MODE == GEMM_I8) ? 1 : 2;  // element bytes
+  const long long lda_b = p.a_s0 * ES;
+  const long long ldb_b = p.b_s0 * ES;
+  const char* abase = (const char*)p.a + (long long)m0 * lda_b;
+  const char* bbase = (const char*)p.b + (long long)n0 * ldb_b;
+  const int kslabs = p.K * ES / SLAB;
+  const int last = kslabs - 1;
+  // DMA: wave w < DW owns row groups w*GROUPS .. +GROUPS-1 (A rows for the
+  // first BM/8 groups, B rows after), 8 rows x 128 bytes per instruction
+  // (lane: row lane / 8, 16-byte slot lane % 8 holding chunk slot ^ ((row >>
+  // 1) & 7)).  Group t's rows are the first group's plus 8t, and the
+  // swizzle repeats every second group, so a lane needs two offsets.
+  const bool dma_a = wave * GROUPS < BM / 8;
+  const long long ld = dma_a ? lda_b : ldb_b;
+  const char* obase = dma_a ? abase : bbase;
+  uint32_t doff[2];
+  {
+    const int row0 = ((dma_a ? wave * GROUPS : wave * GROUPS - BM / 8) * 8) + (lane >> 3);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = row0 + 8 * j;
+      doff[j] = (uint32_t)((long long)row * ld + (((lane & 7) ^ ((row >> 1) & 7)) * 16));
+    }
+  }
+  auto issue = [&](int stage, int slab, int t0, int t1) {
+    char* st = lds + stage * STAGE;
+#pragma unroll
+    for (int t = t0; t < t1; ++t) {
+      const char* ub = obase + (long long)slab * SLAB + (long long)(t & ~1) * 8 * ld;
+      asm volatile("" : "+v"(doff[t & 1]));
+      const char* src = ub + (uint64_t)doff[t & 1];
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(st + (wave * GROUPS + t) * 1024),
+                                       16, 0, 0);
+    }
+  };
+  // ---- 16x16 output fragments (v_mfma_f32_16x16x32_{bf16,f16} /
+  // v_mfma_i32_16x16x64_i8: 16 bytes of K per lane, the 64-byte k-step
+  // split over the four 16-lane groups).  Under the power limit these
+  // sustain more FLOP/s than the 32x32x16 form with the same operand
+  // traffic (half the accumulator register traffic per FLOP).  Wave tile
+  // 64 x 128 = 4 x 8 fragments; per slab two k-steps of 64 bytes.  Lane
+  // (g4, l16) reads row l16 of each 16-row fragment, chunk 4 ks + g4; the
+  // swizzle (row >> 1) & 7 depends on l16 alone, so fragment i is the
+  // lane's offset plus an immediate i * 16 rows (conflict-free: each
+  // 16-lane group covers the 64 banks once).
+  constexpr int FM16 = BM / WM / 16, FN16 = BN / WN / 16;
+  f32x4 acf[FM16][FN16];
+  i32x4 aci[FM16][FN16];
+#pragma unroll
+  for (int i = 0; i < FM16; ++i)
+#pragma unroll
+    for (int j = 0; j < FN16; ++j) {
+      if constexpr (MODE == GEMM_I8) aci[i][j] = (i32x4){};
+      else acf[i][j] = (f32x4){};
+    }
+  const int l16 = lane & 15, g4 = lane >> 4;
+  int aoff[2][2], boff[2][2];
+#pragma unroll
+  for (int s_ = 0; s_ < 2; ++s_)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int sw = (((ks * 4 + g4) ^ ((l16 >> 1) & 7)) << 4) + l16 * SLAB;
+      aoff[s_][ks] = s_ * STAGE + wm * (BM / WM) * SLAB + sw;
+      boff[s_][ks] = s_ * STAGE + BM * SLAB + wn * (BN / WN) * SLAB + sw;
+    }
+  u32x4 a16[2][FM16], b16[FN16];
+  auto afrag = [&](auto sc, int ks, int buf) {
+    constexpr int S = decltype(sc)::value;
+#pragma unroll
+    for (int mi = 0; mi < FM16; ++mi) a16[buf][mi] = *(const u32x4*)(lds + aoff[S][ks] + mi * 16 * SLAB);
+  };
+  auto bfrag = [&](auto sc, int ks, int ni) {
+    constexpr int S = decltype(sc)::value;
+    b16[ni] = *(const u32x4*)(lds + boff[S][ks] + ni * 16 * SLAB);
+  };
+  auto mma = [&](const u32x4& bv, const u32x4& av, f32x4& cf, i32x4& ci) {
+    if constexpr (MODE == GEMM_BF16)
+      cf = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, bv), __builtin_bit_cast(bf16x8, av),
+                                                   cf, 0, 0, 0);
+    else if constexpr (MODE == GEMM_F16)
+      cf = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, bv), __builtin_bit_cast(f16x8, av), cf,
+                                                  0, 0, 0);
+    else
+      ci = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, bv), __builtin_bit_cast(i32x4, av), ci,
+                                                 0, 0, 0);
+  };
+  // One k-step: the MFMAs of (a16[buf], b16) with the next k-step's
+  // fragments read behind them -- stage NS, k-step nks: A into the other
+  // buffer (first four slots), each B fragment into its own registers once
+  // its last MFMA has issued -- and ndma DMA instructions spread over the
+  // slots; an explicit lgkmcnt(0) closes the k-step (the compiler cannot
+  // count LDS reads issued behind a DMA).
+  constexpr int NMF16 = FM16 * FN16;
+  auto kstep = [&](auto bc, auto nsc, int nks, int ndma) {
+    constexpr int buf = decltype(bc)::value;
+    afrag(nsc, nks, buf ^ 1);
+    if constexpr (UMASK & 1) {
+#pragma unroll
+      for (int mi = 0; mi < FM16; ++mi) a16[buf][mi] ^= 0x80808080u;
+    }
+#pragma unroll
+    for (int ni = 0; ni < FN16; ++ni) {
+      if constexpr (UMASK & 2) b16[ni] ^= 0x80808080u;
+#pragma unroll
+      for (int mi = 0; mi < FM16; ++mi) mma(b16[ni], a16[buf][mi], acf[mi][ni], aci[mi][ni]);
+      bfrag(nsc, nks, ni);
+    }
+#pragma unroll
+    for (int i = 0; i < NMF16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i < FM16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i % FM16 == FM16 - 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (ndma && i % (NMF16 / ndma) == 1 && i / (NMF16 / ndma) < ndma)
+        __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  };
+  // Two-stage protocol as below, with two k-steps per slab: the barrier
+  // sits between them, after every read of slab kt (k-step 1's fragments
+  // are read during k-step 0) and after the slab kt + 1 DMA landed.
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  const bool dwave = wave < DW;
+  if (dwave) issue(0, 0, 0, GROUPS);
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  afrag(S0{}, 0, 0);
+#pragma unroll
+  for (int ni = 0; ni < FN16; ++ni) bfrag(S0{}, 0, ni);
+  if (dwave) issue(1, min(1, last), 0, H);
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  auto run = [&](auto dc) {
+    constexpr bool DMA = decltype(dc)::value;
+    auto slab_iter = [&](auto cc, int kt) {
+      constexpr int CUR = decltype(cc)::value, NXT = CUR ^ 1;
+      if constexpr (DMA) issue(NXT, min(kt + 1, last), H, GROUPS);
+      kstep(S0{}, cc, 1, DMA ? H : 0);
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (DMA) issue(CUR, min(kt + 2, last), 0, H);
+      kstep(S1{}, std::integral_constant<int, NXT>{}, 0, DMA ? H : 0);  // (after the last slab: a stale stage, never used)
+    };
+    int kt = 0;
+    for (; kt + 1 < kslabs; kt += 2) {
+      slab_iter(S0{}, kt);
+      slab_iter(S1{}, kt + 1);
+    }
+    if (kt < kslabs) slab_iter(S0{}, kt);
+  };
+  if (dwave) run(std::true_type{});
+  else run(std::false_type{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  gemm_epilogue<MODE, FM16, FN16, UMASK, 16>(p, acf, aci, m0 + wm * (BM / WM), n0 + wn * (BN / WN), lane, m_own,
+                                              n_own);
+}
+
 // WM x WN waves; wave tile (BM/WM) x (BN/WN) = FM x FN fragments of 32x32.
 // UMASK (int8): bit 0 A unsigned, bit 1 B unsigned.  An unsigned operand's
 // bytes are flipped (XOR 0x80: u - 128, a signed int8) as its fragments enter
@@ -281,6 +474,14 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   constexpr int H = GROUPS / 2;
   static_assert(GROUPS * 8 * DW == BM + BN && GROUPS % 2 == 0, "DMA split over waves and halves");
   __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  if constexpr (G950_GEMM16 && MODE != GEMM_F32 && !KTAIL) {
+    // whole-slab 16-bit / int8 GEMMs of at least one tile each way take the
+    // 16x16-fragment form (uniform per launch)
+    if (p.M >= BM && p.N >= BN) {
+      gemm_mfma16_body<MODE, WM, WN, UMASK>(p, lds);
+      return;
+    }
+  }
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -475,7 +676,7 @@ __device__ __forceinline__ void gemm_mfma_body(const GemmArgs& p) {
   else run(std::false_type{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  gemm_epilogue<MODE, FM, FN, UMASK>(p, accf, acci, m0 + wm * (BM / WM), n0 + wn * (BN / WN), r, g);
+  gemm_epilogue<MODE, FM, FN, UMASK>(p, accf, acci, m0 + wm * (BM / WM), n0 + wn * (BN / WN), lane);
 }
 
 // Bt[n][k] = B[k][n] for 16-bit elements: B [K, N] row-major with row stride
@@ -703,7 +904,7 @@ __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi) acc[mi][ni][q * 4 + e] *= sc;
       }
-  gemm_epilogue<F16 ? GEMM_F16 : GEMM_BF16, 2, 2>(p, acc, unused, wm0, wn0, r, g);
+  gemm_epilogue<F16 ? GEMM_F16 : GEMM_BF16, 2, 2>(p, acc, unused, wm0, wn0, lane);
 }
 
 // -------------------------------------- W8A16 for few rows of A (decode)

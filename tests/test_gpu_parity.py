@@ -646,6 +646,50 @@ def test_int8_gemm_exact_and_dequant(m, n, k):
     close(host(y[torch.from_numpy(rows).to(DEV)]), deq, 2e-2, 2e-2)
 
 
+@pytest.mark.parametrize("m,n,k", [(257, 257, 128), (300, 263, 256), (511, 1001, 640), (256, 259, 128)])
+def test_gemm_16x16_edge_windows(m, n, k):
+    """M, N >= 256 with whole K slabs take the 16x16-fragment kernel, whose
+    edge tiles compute the 256x256 window ending at the matrix edge and store
+    only their own rows and columns; N not a multiple of 4 moves those
+    windows off 4-column alignment (element stores).  Every output element:
+    int8 bit-exact for all four signedness pairs (int32 and the dequant
+    epilogue), bf16 / f16 to their bars, and the output's guard rows and
+    columns untouched."""
+    rng = np.random.default_rng(m * 7 + n)
+    pad = 8 - n % 8  # output rows 16-byte aligned, >= 1 guard column after each row
+    for adt, bdt in ((np.int8, np.int8), (np.uint8, np.int8), (np.int8, np.uint8), (np.uint8, np.uint8)):
+        lo_a, hi_a = (-128, 128) if adt is np.int8 else (0, 256)
+        lo_b, hi_b = (-128, 128) if bdt is np.int8 else (0, 256)
+        a = rng.integers(lo_a, hi_a, (m, k)).astype(adt)
+        bt = rng.integers(lo_b, hi_b, (n, k)).astype(bdt)
+        full = torch.full((m + 2, n + pad), -5, dtype=torch.int32, device=DEV)
+        acc = full[1:m + 1, :n]
+        ops.matmul_i8_kernel(torch.from_numpy(a).to(DEV), torch.from_numpy(bt).to(DEV).t(), acc, m, n, k,
+                             sync=True)
+        assert rt.module().last_kernel.endswith("_256x256")
+        # |a.b| <= 255^2 * 640 < 2^31: the int32 result is the exact product
+        assert np.array_equal(acc.cpu().numpy().astype(np.int64), a.astype(np.int64) @ bt.T.astype(np.int64))
+        fh = full.cpu().numpy()
+        assert (fh[0] == -5).all() and (fh[-1] == -5).all() and (fh[:, n:] == -5).all()
+    c = inputs.config5(m, n, k)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    ops.matmul_i8_dequant_kernel(torch.from_numpy(c["a"]).to(DEV), torch.from_numpy(c["bt"]).to(DEV).t(),
+                                 torch.from_numpy(c["sa"]).to(DEV), torch.from_numpy(c["sb"]).to(DEV), y, m, n, k,
+                                 sync=True)
+    assert rt.module().last_kernel == "g950_gemm_i8_256x256"
+    close(host(y), ref.dequant(ref.matmul_i8(c["a"], c["bt"].T), c["sa"], c["sb"]), 2e-2, 2e-2)
+    for dt in ("bfloat16", "float16"):
+        c3 = inputs.config3(m, n, k)
+        full = torch.full((m + 2, n + pad), 7.0, dtype=TD[dt], device=DEV)
+        y = full[1:m + 1, :n]
+        ops.matmul_kernel(dev(c3["a"], dt), dev(c3["bt"], dt).t(), y, m, n, k, sync=True)
+        assert rt.module().last_kernel.endswith("_256x256")
+        ad, bd = host(dev(c3["a"], dt)), host(dev(c3["bt"], dt))
+        close(host(y), ref.matmul(ad, bd.T), *((2e-2, 2e-2) if dt == "bfloat16" else (1e-2, 1e-2)))
+        fh = host(full)
+        assert (fh[0] == 7).all() and (fh[-1] == 7).all() and (fh[:, n:] == 7).all()
+
+
 def test_int8_general_path_exact():
     rng = np.random.default_rng(12)
     a = rng.integers(-128, 128, (37, 100), dtype=np.int8)   # K not a slab multiple
