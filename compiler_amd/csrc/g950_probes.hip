@@ -242,3 +242,57 @@ extern "C" __global__ __launch_bounds__(512) void g950p_issue_global(const char*
   g950p::issue_body<g950p::ISSUE_GLOBAL>(src, out, sink);
 }
 extern "C" __global__ __launch_bounds__(64) void g950p_clock(unsigned long long* out) { g950p::clock_body(out); }
+
+// Sustained MFMA throughput by output shape, under the chip's power limit
+// (timed by the host over back-to-back launches): 8 waves per workgroup,
+// every MFMA taking a different pair of the wave's eight operand registers
+// (random bf16 from the caller, so the datapath toggles as in a GEMM), the
+// same FLOPs per iteration for both shapes -- 32 v_mfma_f32_32x32x16_bf16
+// into 4 accumulators, or 64 v_mfma_f32_16x16x32_bf16 into 8.  Each thread
+// stores the sum of its accumulators so none of the work is dead.
+typedef float p_f32x4 __attribute__((ext_vector_type(4)));
+template <bool S16>
+__device__ __forceinline__ void mfma_rate_body(const p_u32x4* in, float* out, int iters) {
+  const int t = threadIdx.x + blockIdx.x * 512;
+  p_u32x4 a[8], b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = in[(t * 16 + i) & 65535];
+    b[i] = in[(t * 16 + 8 + i) & 65535];
+  }
+  float s = 0.0f;
+  if constexpr (S16) {
+    p_f32x4 acc[8] = {};
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(p_bf16x8, a[(i + j) & 7]),
+                                                           __builtin_bit_cast(p_bf16x8, b[(i + 3 * j) & 7]), acc[j],
+                                                           0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      for (int e = 0; e < 4; ++e) s += acc[j][e];
+  } else {
+    p_f32x16 acc[4] = {};
+    for (int it = 0; it < iters; ++it)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(p_bf16x8, a[(i + j) & 7]),
+                                                           __builtin_bit_cast(p_bf16x8, b[(i + 3 * j) & 7]), acc[j],
+                                                           0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      for (int e = 0; e < 16; ++e) s += acc[j][e];
+  }
+  out[t] = s;
+}
+extern "C" __global__ __launch_bounds__(512) void g950p_mfma_rate32(const p_u32x4* in, float* out, int iters) {
+  mfma_rate_body<false>(in, out, iters);
+}
+extern "C" __global__ __launch_bounds__(512) void g950p_mfma_rate16(const p_u32x4* in, float* out, int iters) {
+  mfma_rate_body<true>(in, out, iters);
+}

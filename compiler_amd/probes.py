@@ -50,7 +50,7 @@ class _Hip:
         rc = self.lib.hipModuleGetFunction(ctypes.byref(f), self.mod, name.encode())
         if rc:
             raise RuntimeError(f"hipModuleGetFunction({name}) failed: {rc}")
-        vals = [ctypes.c_void_p(a) for a in args]
+        vals = [a if isinstance(a, ctypes._SimpleCData) else ctypes.c_void_p(a) for a in args]
         ptrs = (ctypes.c_void_p * len(vals))(*[ctypes.addressof(v) for v in vals])
         rc = self.lib.hipModuleLaunchKernel(f, BLOCKS, 1, 1, threads, 1, 1, 0, stream, ptrs, None)
         if rc:
@@ -94,4 +94,40 @@ def run(torch) -> dict:
         torch.cuda.synchronize()
     c = out[: BLOCKS * 2].view(BLOCKS, 2).double()
     res["clock"] = {"memtime_mhz": round(100.0 * c[:, 0].mean().item() / c[:, 1].mean().item(), 1)}
+    res["mfma_shape"] = mfma_shape_rates(torch, hip, stream)
     return res
+
+
+def mfma_shape_rates(torch, hip, stream, seconds=1.0) -> dict:
+    """Sustained bf16 MFMA TFLOP/s of the 32x32x16 and 16x16x32 forms
+    (g950p_mfma_rate32 / _rate16: 8 waves per CU, random operands rotating
+    through eight registers), each timed with HIP events over about
+    ``seconds`` of back-to-back launches so the power limit sets the clock;
+    each shape is measured twice, interleaved."""
+    import time
+    words = torch.randint(0, 2 ** 31 - 1, (65536 * 4,), dtype=torch.int32, device="cuda")
+    words = (words & 0x807F807F) | 0x3F003F00  # random signs and mantissas, exponents near 1
+    sink = torch.empty(BLOCKS * 512, dtype=torch.float32, device="cuda")
+    iters = 2000
+    out = {}
+    for name, key in (("g950p_mfma_rate32", "32x32x16"), ("g950p_mfma_rate16", "16x16x32")) * 2:
+        args = [words.data_ptr(), sink.data_ptr(), ctypes.c_int(iters)]
+        for _ in range(3):
+            hip.launch(name, 512, args, stream)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        n = 0
+        while time.perf_counter() - t0 < seconds:
+            hip.launch(name, 512, args, stream)
+            n += 1
+            if n % 8 == 0:
+                torch.cuda.synchronize()
+        e1.record()
+        e1.synchronize()
+        flop = n * BLOCKS * 8 * iters * 32 * 32768  # per wave per iteration: 32 x 32768 = 64 x 16384
+        out.setdefault(key, []).append(round(flop / (e0.elapsed_time(e1) * 1e-3) / 1e12, 1))
+    return {"what": "bf16 MFMA, random operands, 8 waves/CU, ~1 s of back-to-back launches each",
+            "tflops": out}

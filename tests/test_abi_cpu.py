@@ -32,7 +32,8 @@ def test_probe_code_object_holds_every_probe_kernel():
     # bench.py --hw-probe launches these by name from the probe code object
     from compiler_amd import probes
     data = Path(probes.PROBES).read_bytes()
-    names = [n for n, *_ in probes.RATE.values()] + [n for n, _ in probes.ISSUE.values()] + ["g950p_clock"]
+    names = [n for n, *_ in probes.RATE.values()] + [n for n, _ in probes.ISSUE.values()] + \
+        ["g950p_clock", "g950p_mfma_rate32", "g950p_mfma_rate16"]
     for name in names:
         assert (name + ".kd").encode() in data, name
 
