@@ -920,8 +920,9 @@ __device__ __forceinline__ void gemm_w8a16_body(const GemmArgs& p) {
 // (g = lane/16, i = lane%16) loads 16 contiguous int8 of column n0 + 16t + i
 // at k + 16g (64-byte runs per column) and the 32 bytes of A row 16r + i at
 // the same k: its first 8 k feed one MFMA, the next 8 a second one (the two
-// MFMAs' k sets interleave, which leaves each dot product unchanged).  Steps
-// are loaded SKINNY_STEPS / R at a time, before their MFMAs.
+// MFMAs' k sets interleave, which leaves each dot product unchanged).
+// SKINNY_STEPS / R steps are in flight per wave, each reloaded with the next
+// batch's step once its MFMAs have issued.
 constexpr int SKINNY_STEPS = 8;   // 64-element K steps loaded together (R = 1)
 constexpr int SKINNY_WAVES = 8;   // K ranges (waves) per workgroup
 constexpr int SKINNY_TILES = 2;   // 16-column tiles per workgroup
@@ -1002,20 +1003,58 @@ __device__ __forceinline__ void gemm_w8a16_skinny_body(const GemmArgs& p) {
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[r][t] = (f32x4){};
-  for (int k0 = kb; k0 < ke; k0 += STEPS * 64) {
-    // a lane whose 16 k lie past the range contributes zeros (K % 16 == 0)
-    u32x4 a0[STEPS][R], a1[STEPS][R], bw[STEPS][T];
+  // STEPS 64-element K steps in flight per wave.  Over whole batches, step st
+  // of the next batch is loaded into step st's registers as soon as their
+  // MFMAs have issued, so the loads stream without a gap between batches (no
+  // per-lane branch around them, so each MFMA waits only for its own
+  // step's loads).  A last partial batch loads per lane: a lane whose 16 k
+  // lie past the range contributes zeros (K % 16 == 0).
+  u32x4 a0[STEPS][R], a1[STEPS][R], bw[STEPS][T];
+  auto load = [&](int st, int k0) {
+    const int kk = k0 + st * 64 + 16 * g;
+#pragma unroll
+    for (int t = 0; t < T; ++t) bw[st][t] = __builtin_nontemporal_load((const u32x4*)(bcol[t] + kk));
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      a0[st][r] = *(const u32x4*)(arow[r] + 2 * (long long)kk);
+      a1[st][r] = *(const u32x4*)(arow[r] + 2 * (long long)kk + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the steps' loads in step order
+  };
+  auto mma = [&](int st) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      u32x4 lo, hi;
+      widen_i8x16<F16>(bw[st][t], lo, hi);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        acc[r][t] = mfma16x16x32<F16>(a0[st][r], lo, acc[r][t]);
+        acc[r][t] = mfma16x16x32<F16>(a1[st][r], hi, acc[r][t]);
+      }
+    }
+  };
+  constexpr int BK = STEPS * 64;
+  int k0 = kb;
+  const int kwhole = kb + (ke > kb ? (ke - kb) / BK * BK : 0);  // end of the whole batches
+  if (k0 < kwhole) {
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) load(st, k0);
+    for (; k0 + BK < kwhole; k0 += BK) {
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) {
+        mma(st);
+        load(st, k0 + BK);
+      }
+    }
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) mma(st);
+    k0 += BK;
+  }
+  if (k0 < ke) {
 #pragma unroll
     for (int st = 0; st < STEPS; ++st) {
-      const int kk = k0 + st * 64 + 16 * g;
-      if (kk < ke) {
-#pragma unroll
-        for (int t = 0; t < T; ++t) bw[st][t] = __builtin_nontemporal_load((const u32x4*)(bcol[t] + kk));
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          a0[st][r] = *(const u32x4*)(arow[r] + 2 * (long long)kk);
-          a1[st][r] = *(const u32x4*)(arow[r] + 2 * (long long)kk + 16);
-        }
+      if (k0 + st * 64 + 16 * g < ke) {
+        load(st, k0);
       } else {
 #pragma unroll
         for (int t = 0; t < T; ++t) bw[st][t] = (u32x4){};
@@ -1024,17 +1063,7 @@ __device__ __forceinline__ void gemm_w8a16_skinny_body(const GemmArgs& p) {
       }
     }
 #pragma unroll
-    for (int st = 0; st < STEPS; ++st)
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        u32x4 lo, hi;
-        widen_i8x16<F16>(bw[st][t], lo, hi);
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          acc[r][t] = mfma16x16x32<F16>(a0[st][r], lo, acc[r][t]);
-          acc[r][t] = mfma16x16x32<F16>(a1[st][r], hi, acc[r][t]);
-        }
-      }
+    for (int st = 0; st < STEPS; ++st) mma(st);
   }
   // lane (g, i) holds rows 16r + 4g .. +3 of column n0 + 16t + i; wave 0
   // adds the waves' tiles in wave order, scales and stores
