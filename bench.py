@@ -457,9 +457,10 @@ def suite(torch, ops, cpu=True):
                 "frac": round(gbs / HBM_PEAK_GBS, 4)})
     del xs, ys, sp_calls
 
-    # dequantize_matmul fused into the GEMM (W8A16): 8192^3 and a decode shape
-    # (16 rows; split-K), bf16 activations, int8 K-contiguous weights
-    for m_, n_, k_ in ((8192, 8192, 8192), (16, 8192, 8192)):
+    # dequantize_matmul fused into the GEMM (W8A16): 8192^3 and two decode
+    # shapes (16 rows and one row: the B-streaming kernels), bf16 activations,
+    # int8 K-contiguous weights
+    for m_, n_, k_ in ((8192, 8192, 8192), (16, 8192, 8192), (1, 8192, 8192)):
         a_ = torch.randn((m_, k_), device=dev, generator=g).to(torch.bfloat16)
         bt_ = torch.randint(-127, 127, (n_, k_), device=dev, generator=g, dtype=torch.int8)
         s_ = torch.rand(n_, device=dev, generator=g).to(torch.bfloat16)

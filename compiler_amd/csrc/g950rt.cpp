@@ -891,13 +891,21 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
   if (fast && M <= 64) {
     // decode shapes: the few-row kernels stream B, 32 columns and all of K
     // per workgroup (8 waves, one K range each, summed in LDS), for up to 16,
-    // 32 or 64 rows of A
+    // 32 or 64 rows of A.  With at most 16 rows, 16 columns per workgroup
+    // (twice the workgroups, each reading all of A) where the 32-column grid
+    // leaves CUs idle or exceeds them by more than a quarter, and for one row
+    // of A.  Measured on MI355X (rotating inputs): 16x4096x4096 12.3 -> 9.1 us,
+    // 16x4096x11008 27.1 -> 19.8, 16x11008x4096 22.2 -> 21.1, 1x8192x8192
+    // 20.9 -> 15.1; 16x8192x8192 ties and 16x8192x8000 loses (21.7 -> 24.8).
     g.a_s0 = a.stride[0];
     g.b_s0 = b.stride[1];
-    const long long blocks = (N + 31) / 32;
+    const long long cus = m ? m->cus : 256;
+    const long long blocks32 = (N + 31) / 32;
+    const bool c16 = M <= 16 && (M == 1 || blocks32 < cus || 4 * blocks32 > 5 * cus);
+    const long long blocks = c16 ? (N + 15) / 16 : blocks32;
     if (blocks > 0x7FFFFFFF) return fail(G950_USAGE, "dequant_matmul: too many tiles");
     char name[48];
-    snprintf(name, sizeof name, "g950_gemm_w8a16_skinny%s_%s", M <= 16 ? "" : M <= 32 ? "32" : "64",
+    snprintf(name, sizeof name, "g950_gemm_w8a16_skinny%s_%s", c16 ? "_c16" : M <= 16 ? "" : M <= 32 ? "32" : "64",
              a.v->dtype == G950_DTYPE_BFLOAT16 ? "bf16" : "f16");
     return launch(m, name, (unsigned)blocks, 512u, g, stream);
   }

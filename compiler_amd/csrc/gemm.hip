@@ -976,9 +976,9 @@ __device__ __forceinline__ void widen_i8_body(const GemmArgs& p) {
   dst[1] = hi;
 }
 
-template <bool F16, int R>
+// T: 16-column tiles per workgroup (SKINNY_TILES, or 1 for the 16-column form)
+template <bool F16, int R, int T = SKINNY_TILES>
 __device__ __forceinline__ void gemm_w8a16_skinny_body(const GemmArgs& p) {
-  constexpr int T = SKINNY_TILES;
   constexpr int STEPS = SKINNY_STEPS / R;
   __shared__ f32x4 part[SKINNY_WAVES][R][T][64];
   if (blockDim.x != SKINNY_WAVES * 64) return;  // launch shape must match the kernel
@@ -1194,16 +1194,20 @@ extern "C" __global__ __launch_bounds__(256) void g950_gemm_w8a16_bf16_128x128(c
   g950::gemm_w8a16_body<false>(p);
 }
 // W8A16 decode: up to 16, 32 and 64 rows of A
-#define G950_W8A16_SKINNY(NAME, F16, R)                                                    \
+#define G950_W8A16_SKINNY(NAME, F16, R, T)                                                 \
   extern "C" __global__ __launch_bounds__(512) void NAME(const g950::GemmArgs p) {        \
-    g950::gemm_w8a16_skinny_body<F16, R>(p);                                               \
+    g950::gemm_w8a16_skinny_body<F16, R, T>(p);                                            \
   }
-G950_W8A16_SKINNY(g950_gemm_w8a16_skinny_bf16, false, 1)
-G950_W8A16_SKINNY(g950_gemm_w8a16_skinny_f16, true, 1)
-G950_W8A16_SKINNY(g950_gemm_w8a16_skinny32_bf16, false, 2)
-G950_W8A16_SKINNY(g950_gemm_w8a16_skinny32_f16, true, 2)
-G950_W8A16_SKINNY(g950_gemm_w8a16_skinny64_bf16, false, 4)
-G950_W8A16_SKINNY(g950_gemm_w8a16_skinny64_f16, true, 4)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny_bf16, false, 1, 2)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny_f16, true, 1, 2)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny32_bf16, false, 2, 2)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny32_f16, true, 2, 2)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny64_bf16, false, 4, 2)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny64_f16, true, 4, 2)
+// 16 columns per workgroup: twice the workgroups, for grids the 32-column
+// form leaves short of the CUs and for a one-row A (whose loads cost little)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny_c16_bf16, false, 1, 1)
+G950_W8A16_SKINNY(g950_gemm_w8a16_skinny_c16_f16, true, 1, 1)
 extern "C" __global__ __launch_bounds__(256) void g950_gemm_w8a16_f16_128x128(const g950::GemmArgs p) {
   g950::gemm_w8a16_body<true>(p);
 }

@@ -286,8 +286,13 @@ def test_dequant_matmul_contract():
                 .view([n], sdt or adt).view([m, n], adt, output=True))
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(256, 512, 1024), [1024, 256, 512])
     assert rc == 0 and name == "g950_gemm_w8a16_bf16_128x128", err
-    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(16, 4096, 4096, rt.DT_F16), [4096, 16, 4096])
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(16, 8192, 8192, rt.DT_F16), [8192, 16, 8192])
     assert rc == 0 and name == "g950_gemm_w8a16_skinny_f16", err   # decode shape (M <= 16)
+    # 16 columns per workgroup: a 32-column grid short of the CUs (128 < 256),
+    # more than a quarter past them (344 > 320), or one row of A
+    for m, n in ((16, 4096), (16, 11008), (1, 8192)):
+        rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(m, n, 4096), [4096, m, n])
+        assert rc == 0 and name == "g950_gemm_w8a16_skinny_c16_bf16", (m, n, err)
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(17, 4096, 4096), [4096, 17, 4096])
     assert rc == 0 and name == "g950_gemm_w8a16_skinny32_bf16", err   # 17..32 rows
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 4096, 4096, rt.DT_F16), [4096, 64, 4096])

@@ -454,7 +454,8 @@ def test_gemm_bf16_config3_sampled(m, n, k):
 @pytest.mark.parametrize("dt", ["bfloat16", "float16"])
 @pytest.mark.parametrize("m,n,k", [(32, 32, 32), (33, 33, 48), (256, 256, 128), (300, 260, 192), (16, 4096, 4096),
                                    (1, 1000, 4096), (2048, 2048, 4096), (7, 70, 208), (16, 8192, 8192),
-                                   (5, 130, 1040), (64, 4096, 4096), (4096, 4096, 256), (4100, 4096, 320),
+                                   (5, 130, 1040), (1, 8192, 8192), (16, 11008, 4096), (16, 8192, 8000),
+                                   (64, 4096, 4096), (4096, 4096, 256), (4100, 4096, 320),
                                    (1100, 8192, 128), (1024, 8192, 128), (17, 8192, 8192), (48, 4096, 1040),
                                    (65, 4096, 4096)])
 def test_dequant_matmul_fused(m, n, k, dt):
@@ -472,7 +473,10 @@ def test_dequant_matmul_fused(m, n, k, dt):
     short = "bf16" if dt == "bfloat16" else "f16"
     # more 256x256 tiles than half the CUs: B is widened once and the bf16/f16 GEMM runs
     widened = k % 64 == 0 and 2 * -(-m // 256) * -(-n // 256) > 256
+    blocks32 = -(-n // 32)
+    c16 = m == 1 or blocks32 < 256 or 4 * blocks32 > 5 * 256  # 16 columns per workgroup (256 CUs)
     want = ("g950_gemm_general" if k % 16 else
+            f"g950_gemm_w8a16_skinny_c16_{short}" if m <= 16 and c16 else
             f"g950_gemm_w8a16_skinny_{short}" if m <= 16 else
             f"g950_gemm_w8a16_skinny32_{short}" if m <= 32 else
             f"g950_gemm_w8a16_skinny64_{short}" if m <= 64 else
