@@ -4,6 +4,8 @@
   compiler_amd/lib/libg950rt.so   the C-ABI module loader/launcher (include/g950rt.h)
   compiler_amd/lib/g950_exec      the bundle-driven command-line runner
   compiler_amd/lib/g950_probes.hsaco  hardware micro-probes (measurement only)
+  compiler_amd/lib/g950_att_stamps.hsaco  attention kernels with phase stamps
+                                  (measurement only)
 
 Both are written next to the package so they travel with the source tree; the
 Python runtime loads exactly these two files.
@@ -23,6 +25,7 @@ HSACO = LIB / "g950.hsaco"
 RTLIB = LIB / "libg950rt.so"
 EXEC = LIB / "g950_exec"
 PROBES = LIB / "g950_probes.hsaco"
+STAMPS = LIB / "g950_att_stamps.hsaco"
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -78,11 +81,21 @@ def build_probes() -> Path:
     return PROBES
 
 
+def build_stamps() -> Path:
+    """The attention kernels with phase stamps (measurement only; probes.py)."""
+    LIB.mkdir(exist_ok=True)
+    tmp = STAMPS.with_suffix(".hsaco.tmp")
+    _run([HIPCC, *DEVICE_FLAGS, "--genco", f"-I{CSRC}", "-o", str(tmp), str(CSRC / "g950_att_stamps.hip")])
+    os.replace(tmp, STAMPS)
+    return STAMPS
+
+
 def build_all() -> None:
     build_code_object()
     build_runtime()
     build_exec()
     build_probes()
+    build_stamps()
 
 
 if __name__ == "__main__":

@@ -12,7 +12,7 @@ from __future__ import annotations
 import ctypes
 from pathlib import Path
 
-from .build import PROBES
+from .build import PROBES, STAMPS
 
 RATE = {
     "lds_b128": ("g950p_lds_b128", "64 ds_read_b128 (1 KiB each)", 64 * 1024),
@@ -95,7 +95,71 @@ def run(torch) -> dict:
     c = out[: BLOCKS * 2].view(BLOCKS, 2).double()
     res["clock"] = {"memtime_mhz": round(100.0 * c[:, 0].mean().item() / c[:, 1].mean().item(), 1)}
     res["mfma_shape"] = mfma_shape_rates(torch, hip, stream)
+    res["attention_phases"] = attention_phases(torch)
     return res
+
+
+STAMP_WG = 1000  # G950_ATT_STAMP_WG of g950_att_stamps.hip
+
+
+def attention_phases(torch, t_lo=8, t_hi=40) -> dict:
+    """Where an iteration of the bf16 attention main loop goes: one launch of
+    the stamped code object (lib/g950_att_stamps.hsaco) at the non-causal
+    [4, 32 / 8 KV heads, 4096, 128] shape, after the product kernel warmed
+    the clock; workgroup STAMP_WG writes its s_memtime stamps (loop top,
+    after the barrier, after the DMA issue, after the first-half softmax,
+    after the MFMA phase, after the lead waves' softmax) over its output.
+    Mean shader cycles per iteration over tiles t_lo..t_hi-1, for the lead
+    waves 0-3 (DMA, MFMA phase, softmax) and waves 4-7 (softmax, MFMA phase)."""
+    import math
+    import time
+
+    from . import operators as ops
+    from . import runtime as rt
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    B, H, HK, S, D = 4, 32, 8, 4096, 128
+    q = torch.randn((B, H, S, D), device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn((B, HK, S, D), device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn((B, HK, S, D), device=dev, generator=g).to(torch.bfloat16)
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), device=dev)
+    args = (q, k, v, o, B, H, S, 1.0 / math.sqrt(D), *q.stride(), *k.stride(), *v.stride(), *o.stride())
+    call = ops.attn_fwd_causal_kernel(*args, CAUSAL=False, lse_ptr=lse, prepare=True)
+    t_end = time.perf_counter() + 0.5
+    while time.perf_counter() < t_end:  # clock ramp on the product kernel
+        call()
+        torch.cuda.synchronize()
+    devi = torch.cuda.current_device()
+    prod = rt.module()
+    stamped = rt.Module(str(STAMPS))
+    try:
+        rt._modules[devi] = stamped
+        ops.attn_fwd_causal_kernel(*args, CAUSAL=False, lse_ptr=lse, prepare=True)()
+        torch.cuda.synchronize()
+    finally:
+        rt._modules[devi] = prod
+        stamped.close()
+    # the workgroup -> (q-block, batch, head) map of the kernel: longest
+    # q-blocks first, the G query heads of one KV head 8 ids apart
+    nqb, per_qb, G = S // 256, B * H, H // HK
+    qb = nqb - 1 - STAMP_WG // per_qb
+    i = STAMP_WG % per_qb
+    xcd, j = i & 7, i >> 3
+    zk = xcd + 8 * (j // G)
+    z, h = zk // HK, (zk % HK) * G + j % G
+    raw = o[z, h, qb * 256:qb * 256 + 256].contiguous().view(torch.int64).cpu()
+    st = raw.view(8, -1)[:, :64 * 6].view(8, 64, 6).double()
+    out = {"shape": "non-causal bf16 [4, 32/8, 4096, 128]", "tiles": [t_lo, t_hi], "workgroup": STAMP_WG}
+    for grp, ws, cols in (("lead", range(0, 4), (("barrier", 0, 1), ("dma_issue", 1, 2), ("mfma_phase", 3, 4),
+                                                  ("softmax", 4, 5))),
+                          ("other", range(4, 8), (("barrier", 0, 1), ("softmax", 2, 3), ("mfma_phase", 3, 4)))):
+        sel = st[list(ws), t_lo:t_hi]
+        row = {name: round((sel[..., b] - sel[..., a]).mean().item(), 1) for name, a, b in cols}
+        row["period"] = round((st[list(ws), t_lo + 1:t_hi + 1, 0] - sel[..., 0]).mean().item(), 1)
+        out[grp] = row
+    return out
 
 
 def mfma_shape_rates(torch, hip, stream, seconds=1.0) -> dict:

@@ -36,6 +36,9 @@ def test_probe_code_object_holds_every_probe_kernel():
         ["g950p_clock", "g950p_mfma_rate32", "g950p_mfma_rate16"]
     for name in names:
         assert (name + ".kd").encode() in data, name
+    # the phase-stamp probe swaps in the stamped attention kernels by name
+    stamped = Path(probes.STAMPS).read_bytes()
+    assert b"g950_attn_fwd_bf16_d128.kd" in stamped
 
 
 def test_record_layouts_match_reference_abi():
