@@ -663,7 +663,15 @@ __device__ __forceinline__ void rm_body(const RowArgs& a) {
     if (k + 1 < RPW && row + WAVES < a.rows) load(row + WAVES, nxt, nph);
     const int ph = __builtin_amdgcn_readfirstlane(cph);  // one phase per row: wave-uniform
     auto col = [&](int i, int e) { return (lane + i * 64) * VEC + e - ph; };
+    // LayerNorm: item i whole for every lane of the wave (wave-uniform, no
+    // element before or after the row) skips the element masks, here and in
+    // the centered pass ([8191, 3001] bf16: 25.5 -> 23.9 us, same bits; the
+    // softmax measured 1.5% slower with it, so it keeps the masks)
+    auto whole = [&](int i) {
+      return OP == ROW_LAYERNORM && (i > 0 || ph == 0) && (i * 64 + 64) * VEC - ph <= cols;
+    };
     auto ok = [&](int i, int e) {
+      if (whole(i)) return true;
       const int c = col(i, e);
       return c >= 0 && c < cols;
     };
@@ -671,9 +679,15 @@ __device__ __forceinline__ void rm_body(const RowArgs& a) {
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
       float t[VEC];
-      if ((lane + i * 64) * VEC - ph < cols) IO::unpack(cur[i], t);
+      if (whole(i)) {
+        IO::unpack(cur[i], t);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) v[i][e] = ok(i, e) ? t[e] : ident;
+        for (int e = 0; e < VEC; ++e) v[i][e] = t[e];
+      } else {
+        if ((lane + i * 64) * VEC - ph < cols) IO::unpack(cur[i], t);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[i][e] = ok(i, e) ? t[e] : ident;
+      }
     }
     int yph;
     char* ylo = base(a.y, row, a.y_row, yph);  // yph == ph (host-checked)
