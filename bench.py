@@ -114,10 +114,13 @@ def headline(torch, ops, args):
         ln(i)
         sm(i)
 
-    # per-kernel launch times (events around many launches of one kernel)
-    ln_ms = event_time(torch, ln, 200, 10, warm_s=0.3)
+    # per-kernel launch times: events around many back-to-back launches of one
+    # kernel (its average launch duration), and the reference's per-launch median
+    ln_t = timed(torch, ln, 200, 10, warm_s=0.3)
+    ln_ms = ln_t["mean_ms"]
     ln_kernel = ln_calls[0].kernel
-    sm_ms = event_time(torch, sm, 200, 10)
+    sm_t = timed(torch, sm, 200, 10)
+    sm_ms = sm_t["mean_ms"]
     sm_kernel = sm_calls[0].kernel
 
     # the timed steps: barrier-free single process, synchronize on both sides
@@ -142,10 +145,14 @@ def headline(torch, ops, args):
             "algorithmic_bytes": dom[2], "avg_launch_us": round(dom[3] * 1e3, 2)}
     per_kernel = {
         "layernorm": {"kernel": ln_kernel, "us": round(ln_ms * 1e3, 2),
-                      "GB/s": round(ln_bytes / (ln_ms * 1e-3) / 1e9, 1), "bytes": ln_bytes},
+                      "GB/s": round(ln_bytes / (ln_ms * 1e-3) / 1e9, 1), "bytes": ln_bytes,
+                      "median_us": round(ln_t["median_ms"] * 1e3, 2), "n_samples": ln_t["n"]},
         "softmax": {"kernel": sm_kernel, "us": round(sm_ms * 1e3, 2),
-                    "GB/s": round(sm_bytes / (sm_ms * 1e-3) / 1e9, 1), "bytes": sm_bytes},
+                    "GB/s": round(sm_bytes / (sm_ms * 1e-3) / 1e9, 1), "bytes": sm_bytes,
+                    "median_us": round(sm_t["median_ms"] * 1e3, 2), "n_samples": sm_t["n"]},
     }
+    roof["median_us"] = per_kernel[dom[0]]["median_us"]
+    roof["frac_median"] = round(dom[2] / (roof["median_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     del sets
     return value, ms_step, wall, roof, per_kernel, ln_bytes + sm_bytes
 
@@ -250,10 +257,66 @@ def _cpu_model():
     return "unknown"
 
 
-def suite(torch, ops, cpu=True):
+def event_samples(torch, launch, min_samples=50, min_time_s=0.2, max_samples=1000, floor=10):
+    """The reference benchmark's statistic (ops/harness/benchmark/run.py:141-186,
+    benchmark/README.md:64-67): one HIP-event pair around each launch on the
+    launch stream, each launch waited for before the next (the harness
+    Device's launch returns once the kernel has finished), sampled until
+    EITHER >= 50 samples or >= 0.2 s of kernel time, never fewer than 10, at
+    most 1000.  Returns the samples in ms; the reference reports their median."""
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    times = []
+    i = 0
+    while True:
+        start.record(stream)
+        launch(i)
+        end.record(stream)
+        end.synchronize()
+        times.append(start.elapsed_time(end))
+        i += 1
+        n = len(times)
+        if n >= max(min_samples, floor) or (n >= floor and sum(times) >= min_time_s * 1e3) or n >= max_samples:
+            return times
+
+
+def timed(torch, launch, iters, warmup, warm_s=0.0):
+    """Both statistics of one prepared launch: the batched mean (events around
+    ``iters`` back-to-back launches after a ``warm_s`` warm-up: the kernel's
+    average launch duration plus the inter-dispatch gap) and the reference's
+    per-launch median (``event_samples``)."""
+    mean_ms = event_time(torch, launch, iters, warmup, warm_s=warm_s)
+    s = sorted(event_samples(torch, launch))
+    pick = lambda f: s[min(len(s) - 1, round(f * (len(s) - 1)))]  # noqa: E731
+    return {"mean_ms": mean_ms, "median_ms": float(np.median(s)), "p10_ms": pick(0.1), "p90_ms": pick(0.9),
+            "n": len(s)}
+
+
+def make_row(name, kernel, work, unit, scale, peak, bound, t):
+    """One suite row: value and roofline fraction from the batched mean (the
+    average launch duration, as rocprofv3 sees the kernel back to back), the
+    reference statistic (median of per-launch samples) beside it."""
+    v = work / (t["mean_ms"] * 1e-3) / scale
+    vm = work / (t["median_ms"] * 1e-3) / scale
+    return {"config": name, "kernel": kernel, "us": round(t["mean_ms"] * 1e3, 2), "value": round(v, 1),
+            "unit": unit, "bound": bound, "frac": round(v / peak, 4),
+            "median_us": round(t["median_ms"] * 1e3, 2), "n_samples": t["n"],
+            "p10_us": round(t["p10_ms"] * 1e3, 2), "p90_us": round(t["p90_ms"] * 1e3, 2),
+            "value_median": round(vm, 1), "frac_median": round(vm / peak, 4)}
+
+
+# suite sections (bench.py --only KEY[,KEY...] runs just these, without the
+# headline or the CPU legs: one rocprofv3 trace per config)
+SECTIONS = ("c1", "lse", "dequantize", "c3a", "c3b", "c3a_rowb", "gemm_f32", "c4", "attn_f32", "odd", "split",
+            "w8a16", "w8a16_16", "w8a16_1", "w8a16_rowb", "varlen", "c5")
+
+
+def suite(torch, ops, cpu=True, only=None):
     """Every other BASELINE config, timed per kernel with HIP events; with
     ``cpu`` each BASELINE config row also carries its CPU baselines (both
-    legs) on a bounded sample of the same inputs."""
+    legs) on a bounded sample of the same inputs.  ``only``: the section keys
+    to run (SECTIONS), all when None."""
     from oracle import build as obuild
     from oracle import inputs
     from oracle import reference as ref
@@ -263,75 +326,75 @@ def suite(torch, ops, cpu=True):
     dev = "cuda:0"
     out = []
 
+    def want(key):
+        return only is None or key in only
+
     # C1: fp32 RMSNorm + softmax [4096, 4096], 6 rotating sets (768 MiB)
-    sets = []
-    for s in range(ROTATE):
-        c = inputs.config1(seed=inputs.SEEDS["c1"] + s)
-        sets.append({"x": torch.from_numpy(c["x"]).to(dev), "w": torch.from_numpy(c["w"]).to(dev),
-                     "y": torch.empty((4096, 4096), device=dev), "r": torch.empty(4096, device=dev)})
-    rb = 2 * 4096 * 4096 * 4 + 2 * 4096 * 4
-    sb = 2 * 4096 * 4096 * 4
-
-    rms_calls = [ops.rms_layernorm_forward_kernel(d["y"], 4096, d["x"], 4096, d["w"], 1, d["r"], 1,
-                                                  4096, 1e-6, prepare=True) for d in sets]
-    smx_calls = [ops.softmax_kernel(d["x"], d["y"], 4096, prepare=True) for d in sets]
-
-    for name, calls, nbytes in (("C1a rmsnorm fp32 [4096,4096]", rms_calls, rb),
-                                ("C1b softmax fp32 [4096,4096]", smx_calls, sb)):
-        ms = event_time(torch, lambda i: calls[i % ROTATE](), 200, 10, warm_s=0.3)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out.append({"config": name, "kernel": calls[0].kernel, "us": round(ms * 1e3, 2),
-                    "value": round(gbs, 1), "unit": "GB/s", "bound": "hbm",
-                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
-    del sets
-    torch.cuda.empty_cache()
-    if cpu:
-        c1 = inputs.config1()
-        x1, w1 = c1["x"], c1["w"]
-        y1, r1 = np.empty_like(x1), np.empty(4096, np.float32)
-        out[-2]["cpu_baseline"] = cpu_legs(
-            lambda n: lib.g950o_rmsnorm_f32(P(x1), P(w1), P(y1), P(r1), n, 4096, 1e-6),
-            lambda n: ref.rms_layernorm(x1[:n], w1, 1e-6), rb / 4096, "GB/s", 1e9, "rows of [4096,4096]", 256, 4096)
-        out[-1]["cpu_baseline"] = cpu_legs(
-            lambda n: lib.g950o_softmax_f32(P(x1), P(y1), n, 4096),
-            lambda n: ref.softmax(x1[:n]), sb / 4096, "GB/s", 1e9, "rows of [4096,4096]", 256, 4096)
-        del c1, x1, y1
+    if want("c1"):
+        sets = []
+        for s in range(ROTATE):
+            c = inputs.config1(seed=inputs.SEEDS["c1"] + s)
+            sets.append({"x": torch.from_numpy(c["x"]).to(dev), "w": torch.from_numpy(c["w"]).to(dev),
+                         "y": torch.empty((4096, 4096), device=dev), "r": torch.empty(4096, device=dev)})
+        rb = 2 * 4096 * 4096 * 4 + 2 * 4096 * 4
+        sb = 2 * 4096 * 4096 * 4
+        rms_calls = [ops.rms_layernorm_forward_kernel(d["y"], 4096, d["x"], 4096, d["w"], 1, d["r"], 1,
+                                                      4096, 1e-6, prepare=True) for d in sets]
+        smx_calls = [ops.softmax_kernel(d["x"], d["y"], 4096, prepare=True) for d in sets]
+        for name, calls, nbytes in (("C1a rmsnorm fp32 [4096,4096]", rms_calls, rb),
+                                    ("C1b softmax fp32 [4096,4096]", smx_calls, sb)):
+            t = timed(torch, lambda i: calls[i % ROTATE](), 200, 10, warm_s=0.3)
+            out.append(make_row(name, calls[0].kernel, nbytes, "GB/s", 1e9, HBM_PEAK_GBS, "hbm", t))
+        del sets, rms_calls, smx_calls
+        torch.cuda.empty_cache()
+        if cpu:
+            c1 = inputs.config1()
+            x1, w1 = c1["x"], c1["w"]
+            y1, r1 = np.empty_like(x1), np.empty(4096, np.float32)
+            out[-2]["cpu_baseline"] = cpu_legs(
+                lambda n: lib.g950o_rmsnorm_f32(P(x1), P(w1), P(y1), P(r1), n, 4096, 1e-6),
+                lambda n: ref.rms_layernorm(x1[:n], w1, 1e-6), rb / 4096, "GB/s", 1e9, "rows of [4096,4096]", 256,
+                4096)
+            out[-1]["cpu_baseline"] = cpu_legs(
+                lambda n: lib.g950o_softmax_f32(P(x1), P(y1), n, 4096),
+                lambda n: ref.softmax(x1[:n]), sb / 4096, "GB/s", 1e9, "rows of [4096,4096]", 256, 4096)
+            del c1, x1, y1
 
     # next-row operators at their BASELINE-sized shapes, 6 rotating sets each:
     # row logsumexp bf16 [8191, 3000] -> fp32, int8 weight dequant [8192, 8192] -> bf16
     g = torch.Generator(device=dev)
     g.manual_seed(7)
-    lse_sets = [(torch.randn((8191, 3000), device=dev, generator=g).mul_(3.0).to(torch.bfloat16),
-                 torch.empty(8191, device=dev)) for _ in range(ROTATE)]
-    lse_calls = [ops.logsumexp_kernel(x, y, 3000, prepare=True) for x, y in lse_sets]
-    dq_sets = [(torch.randint(-127, 127, (8192, 8192), device=dev, generator=g, dtype=torch.int8),
-                torch.rand(8192, device=dev, generator=g).to(torch.bfloat16),
-                torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)) for _ in range(ROTATE)]
-    dq_calls = [ops.dequantize_kernel(b, sc, y, 8192, 8192, 8192, 1, 8192, 1, prepare=True)
-                for b, sc, y in dq_sets]
-    for name, calls, nbytes, iters in (
-            ("F logsumexp bf16 [8191,3000] -> fp32", lse_calls, 8191 * 3000 * 2 + 8191 * 4, 200),
-            ("F dequantize int8 [8192,8192] -> bf16", dq_calls, 8192 * 8192 * 3 + 8192 * 2, 50)):
-        ms = event_time(torch, lambda i: calls[i % ROTATE](), iters, 10, warm_s=0.3)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out.append({"config": name, "kernel": calls[0].kernel, "us": round(ms * 1e3, 2),
-                    "value": round(gbs, 1), "unit": "GB/s", "bound": "hbm",
-                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
-    del lse_sets, dq_sets, lse_calls, dq_calls
+    if want("lse"):
+        lse_sets = [(torch.randn((8191, 3000), device=dev, generator=g).mul_(3.0).to(torch.bfloat16),
+                     torch.empty(8191, device=dev)) for _ in range(ROTATE)]
+        calls = [ops.logsumexp_kernel(x, y, 3000, prepare=True) for x, y in lse_sets]
+        t = timed(torch, lambda i: calls[i % ROTATE](), 200, 10, warm_s=0.3)
+        out.append(make_row("F logsumexp bf16 [8191,3000] -> fp32", calls[0].kernel, 8191 * 3000 * 2 + 8191 * 4,
+                            "GB/s", 1e9, HBM_PEAK_GBS, "hbm", t))
+        del lse_sets, calls
+    if want("dequantize"):
+        dq_sets = [(torch.randint(-127, 127, (8192, 8192), device=dev, generator=g, dtype=torch.int8),
+                    torch.rand(8192, device=dev, generator=g).to(torch.bfloat16),
+                    torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)) for _ in range(ROTATE)]
+        calls = [ops.dequantize_kernel(b, sc, y, 8192, 8192, 8192, 1, 8192, 1, prepare=True) for b, sc, y in dq_sets]
+        t = timed(torch, lambda i: calls[i % ROTATE](), 50, 10, warm_s=0.3)
+        out.append(make_row("F dequantize int8 [8192,8192] -> bf16", calls[0].kernel, 8192 * 8192 * 3 + 8192 * 2,
+                            "GB/s", 1e9, HBM_PEAK_GBS, "hbm", t))
+        del dq_sets, calls
     torch.cuda.empty_cache()
 
     # C3: bf16 GEMM, A row-major, B column-major
-    for m, n, k in ((8192, 8192, 8192), (4097, 11008, 4096)):
+    for key, (m, n, k) in (("c3a", (8192, 8192, 8192)), ("c3b", (4097, 11008, 4096))):
+        if not want(key):
+            continue
         c = inputs.config3(m, n, k)
         a = torch.from_numpy(c["a"]).to(dev).to(torch.bfloat16)
         bt = torch.from_numpy(c["bt"]).to(dev).to(torch.bfloat16)
         y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         call = ops.matmul_kernel(a, bt.t(), y, m, n, k, prepare=True)
-        ms = event_time(torch, lambda i: call(), 20, 3, warm_s=0.5)
-        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        out.append({"config": f"C3 gemm bf16 {m}x{n}x{k}", "kernel": call.kernel,
-                    "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
-                    "frac": round(tf / BF16_PEAK_TFS, 4)})
+        t = timed(torch, lambda i: call(), 20, 3, warm_s=0.5)
+        out.append(make_row(f"C3 gemm bf16 {m}x{n}x{k}", call.kernel, 2.0 * m * n * k, "TFLOP/s", 1e12,
+                            BF16_PEAK_TFS, "mfma", t))
         del a, bt, y
         torch.cuda.empty_cache()
         if cpu:
@@ -349,142 +412,177 @@ def suite(torch, ops, cpu=True):
             del ab, btb, b32, cbuf, b64, a64
         del c
 
-    # the reference matmul's own layout: row-major B [K, N] (ops/suite/perf/matmul.py:33);
-    # one K-contiguous copy of B, then the MFMA GEMM (both launches timed)
-    c = inputs.config3(8192, 8192, 8192)
-    a = torch.from_numpy(c["a"]).to(dev).to(torch.bfloat16)
-    b = torch.from_numpy(np.ascontiguousarray(c["bt"].T)).to(dev).to(torch.bfloat16)
-    del c
-    y = torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)
-    call = ops.matmul_kernel(a, b, y, 8192, 8192, 8192, prepare=True)
-    ms = event_time(torch, lambda i: call(), 20, 3, warm_s=0.5)
-    tf = 2.0 * 8192 ** 3 / (ms * 1e-3) / 1e12
-    out.append({"config": "F gemm bf16 8192^3, row-major B (reference layout)",
-                "kernel": "g950_transpose_b16 + " + call.kernel, "us": round(ms * 1e3, 1), "value": round(tf, 1),
-                "unit": "TFLOP/s", "bound": "mfma", "frac": round(tf / BF16_PEAK_TFS, 4)})
-    del a, b, y
-    torch.cuda.empty_cache()
+    # the reference matmul's own layout: row-major B [K, N] (ops/suite/perf/matmul.py:33),
+    # read as it lies by the MFMA kernel (transposing LDS reads)
+    if want("c3a_rowb"):
+        c = inputs.config3(8192, 8192, 8192)
+        a = torch.from_numpy(c["a"]).to(dev).to(torch.bfloat16)
+        b = torch.from_numpy(np.ascontiguousarray(c["bt"].T)).to(dev).to(torch.bfloat16)
+        del c
+        y = torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)
+        call = ops.matmul_kernel(a, b, y, 8192, 8192, 8192, prepare=True)
+        t = timed(torch, lambda i: call(), 20, 3, warm_s=0.5)
+        out.append(make_row("F gemm bf16 8192^3, row-major B (reference layout)", call.kernel, 2.0 * 8192 ** 3,
+                            "TFLOP/s", 1e12, BF16_PEAK_TFS, "mfma", t))
+        del a, b, y
+        torch.cuda.empty_cache()
 
     # fp32 operands (the matmul corpus's base dtype) on the fp32 MFMA kernel
-    g32 = torch.Generator(device=dev)
-    g32.manual_seed(5)
-    a = torch.randn((4096, 4096), device=dev, generator=g32)
-    b = torch.randn((4096, 4096), device=dev, generator=g32)
-    y = torch.empty((4096, 4096), device=dev)
-    call = ops.matmul_kernel(a, b, y, 4096, 4096, 4096, prepare=True)
-    ms = event_time(torch, lambda i: call(), 10, 2, warm_s=0.3)
-    tf = 2.0 * 4096 ** 3 / (ms * 1e-3) / 1e12
-    out.append({"config": "F gemm fp32 4096^3, row-major B", "kernel": "g950_transpose_b32 + " + call.kernel,
-                "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
-                "frac": round(tf / FP32_PEAK_TFS, 4)})
-    del a, b, y
-    torch.cuda.empty_cache()
+    if want("gemm_f32"):
+        g32 = torch.Generator(device=dev)
+        g32.manual_seed(5)
+        a = torch.randn((4096, 4096), device=dev, generator=g32)
+        b = torch.randn((4096, 4096), device=dev, generator=g32)
+        y = torch.empty((4096, 4096), device=dev)
+        call = ops.matmul_kernel(a, b, y, 4096, 4096, 4096, prepare=True)
+        t = timed(torch, lambda i: call(), 10, 2, warm_s=0.3)
+        out.append(make_row("F gemm fp32 4096^3, row-major B", "g950_transpose_b32 + " + call.kernel,
+                            2.0 * 4096 ** 3, "TFLOP/s", 1e12, FP32_PEAK_TFS, "mfma", t))
+        del a, b, y
+        torch.cuda.empty_cache()
 
     # C4: causal GQA attention bf16 (4, 32/8, 4096, 128) with LSE
-    c = inputs.config4()
-    bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
-    q, k, v = bf(c["q"]), bf(c["k"]), bf(c["v"])
-    o = torch.empty_like(q)
-    lse = torch.empty((4, 32, 4096), dtype=torch.float32, device=dev)
-    call = ops.attn_fwd_causal_kernel(q, k, v, o, 4, 32, 4096, 1 / math.sqrt(128), *q.stride(), *k.stride(),
-                                      *v.stride(), *o.stride(), CAUSAL=True, lse_ptr=lse, prepare=True)
-    ms = event_time(torch, lambda i: call(), 10, 2, warm_s=0.5)
-    flops = 4.0 * 4 * 32 * 128 * 4096 * 4096 / 2
-    tf = flops / (ms * 1e-3) / 1e12
-    out.append({"config": "C4 causal GQA attention bf16 (4,32/8,4096,128)", "kernel": call.kernel,
-                "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
-                "frac": round(tf / BF16_PEAK_TFS, 4)})
-    del q, k, v, o, lse
-    torch.cuda.empty_cache()
-    if cpu:
-        # whole (batch 0, head) slices: 4096 causal query rows each
-        qb, kb, vb = (bf16_bits(c[n][0]) for n in ("q", "k", "v"))
-        ob = np.empty((32, 4096, 128), np.uint16)
-        lb = np.empty((32, 4096), np.float32)
-        head_flops = 4.0 * 128 * 4096 * 4096 / 2
-        out[-1]["cpu_baseline"] = cpu_legs(
-            lambda hn: lib.g950o_attention_bf16(P(qb), P(kb), P(vb), P(ob), P(lb), 32, 8, 4096, 128, 0, hn, 0, 4096,
-                                                1 / math.sqrt(128), 1),
-            lambda hn: ref.attention(c["q"][:1, :hn], c["k"][:1, :(hn + 3) // 4], c["v"][:1, :(hn + 3) // 4],
-                                     1 / math.sqrt(128), causal=True, group=4),
-            head_flops, "TFLOP/s", 1e12, "(batch 0, query head) slices of 4096 causal rows", 1, 32)
-        del qb, kb, vb, ob, lb
-    del c
+    if want("c4"):
+        c = inputs.config4()
+        bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
+        q, k, v = bf(c["q"]), bf(c["k"]), bf(c["v"])
+        o = torch.empty_like(q)
+        lse = torch.empty((4, 32, 4096), dtype=torch.float32, device=dev)
+        call = ops.attn_fwd_causal_kernel(q, k, v, o, 4, 32, 4096, 1 / math.sqrt(128), *q.stride(), *k.stride(),
+                                          *v.stride(), *o.stride(), CAUSAL=True, lse_ptr=lse, prepare=True)
+        t = timed(torch, lambda i: call(), 10, 2, warm_s=0.5)
+        out.append(make_row("C4 causal GQA attention bf16 (4,32/8,4096,128)", call.kernel,
+                            4.0 * 4 * 32 * 128 * 4096 * 4096 / 2, "TFLOP/s", 1e12, BF16_PEAK_TFS, "mfma", t))
+        del q, k, v, o, lse
+        torch.cuda.empty_cache()
+        if cpu:
+            # whole (batch 0, head) slices: 4096 causal query rows each
+            qb, kb, vb = (bf16_bits(c[n][0]) for n in ("q", "k", "v"))
+            ob = np.empty((32, 4096, 128), np.uint16)
+            lb = np.empty((32, 4096), np.float32)
+            head_flops = 4.0 * 128 * 4096 * 4096 / 2
+            out[-1]["cpu_baseline"] = cpu_legs(
+                lambda hn: lib.g950o_attention_bf16(P(qb), P(kb), P(vb), P(ob), P(lb), 32, 8, 4096, 128, 0, hn, 0,
+                                                    4096, 1 / math.sqrt(128), 1),
+                lambda hn: ref.attention(c["q"][:1, :hn], c["k"][:1, :(hn + 3) // 4], c["v"][:1, :(hn + 3) // 4],
+                                         1 / math.sqrt(128), causal=True, group=4),
+                head_flops, "TFLOP/s", 1e12, "(batch 0, query head) slices of 4096 causal rows", 1, 32)
+            del qb, kb, vb, ob, lb
+        del c
 
     # the same causal GQA attention in fp32 (the fp32 MFMA kernel)
-    c = inputs.config4()
-    q, k, v = (torch.from_numpy(c[n]).to(dev) for n in ("q", "k", "v"))
-    del c
-    o = torch.empty_like(q)
-    lse = torch.empty((4, 32, 4096), dtype=torch.float32, device=dev)
-    call = ops.attn_fwd_causal_kernel(q, k, v, o, 4, 32, 4096, 1 / math.sqrt(128), *q.stride(), *k.stride(),
-                                      *v.stride(), *o.stride(), CAUSAL=True, lse_ptr=lse, prepare=True)
-    ms = event_time(torch, lambda i: call(), 3, 1, warm_s=0.3)
-    tf = 4.0 * 4 * 32 * 128 * 4096 * 4096 / 2 / (ms * 1e-3) / 1e12
-    out.append({"config": "F causal GQA attention fp32 (4,32/8,4096,128)", "kernel": call.kernel,
-                "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
-                "frac": round(tf / FP32_PEAK_TFS, 4)})
-    del q, k, v, o, lse
-    torch.cuda.empty_cache()
+    if want("attn_f32"):
+        c = inputs.config4()
+        q, k, v = (torch.from_numpy(c[n]).to(dev) for n in ("q", "k", "v"))
+        del c
+        o = torch.empty_like(q)
+        lse = torch.empty((4, 32, 4096), dtype=torch.float32, device=dev)
+        call = ops.attn_fwd_causal_kernel(q, k, v, o, 4, 32, 4096, 1 / math.sqrt(128), *q.stride(), *k.stride(),
+                                          *v.stride(), *o.stride(), CAUSAL=True, lse_ptr=lse, prepare=True)
+        t = timed(torch, lambda i: call(), 3, 1, warm_s=0.3)
+        out.append(make_row("F causal GQA attention fp32 (4,32/8,4096,128)", call.kernel,
+                            4.0 * 4 * 32 * 128 * 4096 * 4096 / 2, "TFLOP/s", 1e12, FP32_PEAK_TFS, "mfma", t))
+        del q, k, v, o, lse
+        torch.cuda.empty_cache()
 
     # rows whose length is not a whole number of 16-byte vectors: bf16 [8191, 3001]
     # (C2's distribution), LayerNorm and softmax, 6 rotating sets
-    odd = []
-    for sidx in range(ROTATE):
-        c = inputs.config2(8191, 3001, seed=inputs.SEEDS["c2"] + 10 + sidx)
-        bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
-        odd.append((bf(c["x"]), bf(c["gamma"]), bf(c["beta"]), torch.empty((8191, 3001), dtype=torch.bfloat16, device=dev),
-                    torch.empty(8191, device=dev), torch.empty(8191, device=dev)))
-    lno = [ops.layernorm_kernel(x, y, g_, b_, mm, rr, 3001, 3001, 1e-5, prepare=True) for x, g_, b_, y, mm, rr in odd]
-    smo = [ops.softmax_kernel(x, y, 3001, prepare=True) for x, g_, b_, y, mm, rr in odd]
-    for name, calls, nbytes in (("F layernorm bf16 [8191,3001] (odd rows)", lno, 2 * 8191 * 3001 * 2 + 2 * 3001 * 2 + 2 * 8191 * 4),
-                                ("F softmax bf16 [8191,3001] (odd rows)", smo, 2 * 8191 * 3001 * 2)):
-        ms = event_time(torch, lambda i: calls[i % ROTATE](), 100, 10, warm_s=0.3)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out.append({"config": name, "kernel": calls[0].kernel, "us": round(ms * 1e3, 2), "value": round(gbs, 1),
-                    "unit": "GB/s", "bound": "hbm", "frac": round(gbs / HBM_PEAK_GBS, 4)})
-    del odd, lno, smo
-    torch.cuda.empty_cache()
+    if want("odd"):
+        odd = []
+        for sidx in range(ROTATE):
+            c = inputs.config2(8191, 3001, seed=inputs.SEEDS["c2"] + 10 + sidx)
+            bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)  # noqa: E731
+            odd.append((bf(c["x"]), bf(c["gamma"]), bf(c["beta"]),
+                        torch.empty((8191, 3001), dtype=torch.bfloat16, device=dev),
+                        torch.empty(8191, device=dev), torch.empty(8191, device=dev)))
+        lno = [ops.layernorm_kernel(x, y, g_, b_, mm, rr, 3001, 3001, 1e-5, prepare=True)
+               for x, g_, b_, y, mm, rr in odd]
+        smo = [ops.softmax_kernel(x, y, 3001, prepare=True) for x, g_, b_, y, mm, rr in odd]
+        for name, calls, nbytes in (("F layernorm bf16 [8191,3001] (odd rows)", lno,
+                                     2 * 8191 * 3001 * 2 + 2 * 3001 * 2 + 2 * 8191 * 4),
+                                    ("F softmax bf16 [8191,3001] (odd rows)", smo, 2 * 8191 * 3001 * 2)):
+            t = timed(torch, lambda i: calls[i % ROTATE](), 100, 10, warm_s=0.3)
+            out.append(make_row(name, calls[0].kernel, nbytes, "GB/s", 1e9, HBM_PEAK_GBS, "hbm", t))
+        del odd, lno, smo
+        torch.cuda.empty_cache()
 
     # few long rows (split-row two-phase path): softmax bf16 [4, 2^22]
-    xs = [torch.randn((4, 1 << 22), device=dev, generator=g).to(torch.bfloat16) for _ in range(ROTATE)]
-    ys = [torch.empty_like(x) for x in xs]
-    sp_calls = [ops.softmax_kernel(x, y, 1 << 22, prepare=True) for x, y in zip(xs, ys)]
-    ms = event_time(torch, lambda i: sp_calls[i % ROTATE](), 100, 10, warm_s=0.3)
-    gbs = 2 * 4 * (1 << 22) * 2 / (ms * 1e-3) / 1e9
-    out.append({"config": "F split-row softmax bf16 [4,4194304]", "kernel": sp_calls[0].kernel,
-                "us": round(ms * 1e3, 2), "value": round(gbs, 1), "unit": "GB/s", "bound": "hbm",
-                "frac": round(gbs / HBM_PEAK_GBS, 4)})
-    del xs, ys, sp_calls
+    if want("split"):
+        xs = [torch.randn((4, 1 << 22), device=dev, generator=g).to(torch.bfloat16) for _ in range(ROTATE)]
+        ys = [torch.empty_like(x) for x in xs]
+        calls = [ops.softmax_kernel(x, y, 1 << 22, prepare=True) for x, y in zip(xs, ys)]
+        t = timed(torch, lambda i: calls[i % ROTATE](), 100, 10, warm_s=0.3)
+        out.append(make_row("F split-row softmax bf16 [4,4194304]", calls[0].kernel, 2 * 4 * (1 << 22) * 2, "GB/s",
+                            1e9, HBM_PEAK_GBS, "hbm", t))
+        del xs, ys, calls
 
     # dequantize_matmul fused into the GEMM (W8A16): 8192^3 and two decode
     # shapes (16 rows and one row: the B-streaming kernels), bf16 activations,
-    # int8 K-contiguous weights
-    for m_, n_, k_ in ((8192, 8192, 8192), (16, 8192, 8192), (1, 8192, 8192)):
+    # int8 K-contiguous weights; and 8192^3 with the reference's own row-major
+    # int8 weights [K, N] (dequantize_matmul.py:62-65)
+    for key, (m_, n_, k_), rowq in (("w8a16", (8192, 8192, 8192), False), ("w8a16_16", (16, 8192, 8192), False),
+                                    ("w8a16_1", (1, 8192, 8192), False), ("w8a16_rowb", (8192, 8192, 8192), True)):
+        if not want(key):
+            continue
         a_ = torch.randn((m_, k_), device=dev, generator=g).to(torch.bfloat16)
         bt_ = torch.randint(-127, 127, (n_, k_), device=dev, generator=g, dtype=torch.int8)
         s_ = torch.rand(n_, device=dev, generator=g).to(torch.bfloat16)
         y_ = torch.empty((m_, n_), device=dev, dtype=torch.bfloat16)
-        call = ops.dequant_matmul_kernel(a_, bt_.t(), s_, y_, m_, n_, k_, prepare=True)
-        ms = event_time(torch, lambda i: call(), 10 if m_ > 1000 else 50, 3, warm_s=0.3)
+        b_ = bt_.t().contiguous() if rowq else bt_.t()
+        call = ops.dequant_matmul_kernel(a_, b_, s_, y_, m_, n_, k_, prepare=True)
+        t = timed(torch, lambda i: call(), 10 if m_ > 1000 else 50, 3, warm_s=0.3)
         if m_ > 1000:
-            tf = 2.0 * m_ * n_ * k_ / (ms * 1e-3) / 1e12
             # large M: one exact int8 -> bf16 copy of B, then the bf16 GEMM (both timed)
             kern = call.kernel if "w8a16" in call.kernel else "g950_widen_i8_bf16 + " + call.kernel
-            out.append({"config": f"F dequant_matmul W8A16 bf16 {m_}x{n_}x{k_}", "kernel": kern,
-                        "us": round(ms * 1e3, 1), "value": round(tf, 1), "unit": "TFLOP/s", "bound": "mfma",
-                        "frac": round(tf / BF16_PEAK_TFS, 4)})
+            label = ", row-major int8 weights (reference layout)" if rowq else ""
+            out.append(make_row(f"F dequant_matmul W8A16 bf16 {m_}x{n_}x{k_}{label}", kern, 2.0 * m_ * n_ * k_,
+                                "TFLOP/s", 1e12, BF16_PEAK_TFS, "mfma", t))
         else:
-            gbs = (n_ * k_ + m_ * k_ * 2 + m_ * n_ * 2) / (ms * 1e-3) / 1e9
-            out.append({"config": f"F dequant_matmul W8A16 bf16 {m_}x{n_}x{k_} (decode)", "kernel": call.kernel,
-                        "us": round(ms * 1e3, 1), "value": round(gbs, 1), "unit": "GB/s", "bound": "hbm",
-                        "frac": round(gbs / HBM_PEAK_GBS, 4)})
-        del a_, bt_, s_, y_
+            out.append(make_row(f"F dequant_matmul W8A16 bf16 {m_}x{n_}x{k_} (decode)", call.kernel,
+                                n_ * k_ + m_ * k_ * 2 + m_ * n_ * 2, "GB/s", 1e9, HBM_PEAK_GBS, "hbm", t))
+        del a_, bt_, b_, s_, y_
     torch.cuda.empty_cache()
 
     # varlen attention (flash_varlen_fwd_kernel): 8 sequences of 4096 - 256 i
     # tokens (q = k lengths, causal), 32 query / 8 KV heads, d 128, bf16;
     # contiguous and paged (64-token pages, shuffled) K/V
+    if want("varlen"):
+        out.extend(varlen_rows(torch, ops))
+        torch.cuda.empty_cache()
+
+    # C5: int8 GEMM 4096x8192x8192 + dequant
+    if want("c5"):
+        c = inputs.config5()
+        a = torch.from_numpy(c["a"]).to(dev)
+        bt = torch.from_numpy(c["bt"]).to(dev)
+        sa = torch.from_numpy(c["sa"]).to(dev)
+        sbv = torch.from_numpy(c["sb"]).to(dev)
+        y = torch.empty((4096, 8192), dtype=torch.bfloat16, device=dev)
+        call = ops.matmul_i8_dequant_kernel(a, bt.t(), sa, sbv, y, 4096, 8192, 8192, prepare=True)
+        t = timed(torch, lambda i: call(), 20, 3, warm_s=0.5)
+        out.append(make_row("C5 int8 gemm 4096x8192x8192 + dequant", call.kernel, 2.0 * 4096 * 8192 * 8192, "TOP/s",
+                            1e12, INT8_PEAK_TOPS, "mfma", t))
+        del a, bt, sa, sbv, y
+        torch.cuda.empty_cache()
+        if cpu:
+            yc = np.empty((4096, 8192), np.uint16)
+            b64 = c["bt"].T.astype(np.float64)
+            a64 = c["a"].astype(np.float64)
+            out[-1]["cpu_baseline"] = cpu_legs(
+                lambda r: lib.g950o_gemm_i8(P(c["a"]), P(c["bt"]), P(c["sa"]), P(c["sb"]), None, P(yc), 0, r, 8192,
+                                            8192),
+                lambda r: ref.dequant(np.rint(a64[:r] @ b64), c["sa"][:r], c["sb"]),
+                2.0 * 8192 * 8192, "TOP/s", 1e12, "rows of A (4096x8192x8192, int32 exact + dequant)", 8, 4096)
+            del yc, b64, a64
+        del c
+    return out
+
+
+def varlen_rows(torch, ops):
+    """flash_varlen_fwd_kernel at the C4 scale: 8 causal sequences of
+    4096 - 256 i tokens, 32 query / 8 KV heads, d 128, bf16; contiguous and
+    paged (64-token pages, shuffled) K/V."""
+    dev = "cuda:0"
     lens = [4096 - 256 * i for i in range(8)]
     tq = sum(lens)
     cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device=dev)
@@ -503,7 +601,8 @@ def suite(torch, ops, cpu=True):
     nxt = 0
     for b, n in enumerate(lens):
         for pg in range(pages[b]):
-            ph = int(perm[nxt]); nxt += 1
+            ph = int(perm[nxt])
+            nxt += 1
             table[b, pg] = ph
             lo, hi = pg * 64, min(n, pg * 64 + 64)
             kp[ph * 64:ph * 64 + hi - lo] = kv[int(cu[b]) + lo:int(cu[b]) + hi]
@@ -525,43 +624,15 @@ def suite(torch, ops, cpu=True):
                 cu_seqlens_k_ptr=cu, seqused_k_ptr=used, philox_args=philox, alibi_slopes_ptr=zero1,
                 page_table_ptr=table)
     flops = sum(4.0 * 32 * 128 * n * (n + 1) / 2 for n in lens)
+    rows = []
     for name, extra in (("F varlen causal GQA bf16 (8 seqs 4096..2304, 32/8, d128)", {}),
                         ("F varlen paged(64) causal GQA bf16 (same)",
                          dict(k_ptr=kp, v_ptr=vp, is_paged=True, is_cu_seqlens_k=False, is_seqused_k=True,
                               page_table_batch_stride=max(pages), block_size=64, k_page_stride=64 * 8 * 128))):
         call = ops.flash_varlen_fwd_kernel(**{**ptrs, **scal, **extra}, prepare=True)
-        ms = event_time(torch, lambda i: call(), 10, 2, warm_s=0.5)
-        tf = flops / (ms * 1e-3) / 1e12
-        out.append({"config": name, "kernel": call.kernel, "us": round(ms * 1e3, 1), "value": round(tf, 1),
-                    "unit": "TFLOP/s", "bound": "mfma", "frac": round(tf / BF16_PEAK_TFS, 4)})
-    del qv, kv, vv, ov, lsev, kp, vp
-    torch.cuda.empty_cache()
-
-    # C5: int8 GEMM 4096x8192x8192 + dequant
-    c = inputs.config5()
-    a = torch.from_numpy(c["a"]).to(dev)
-    bt = torch.from_numpy(c["bt"]).to(dev)
-    sa = torch.from_numpy(c["sa"]).to(dev)
-    sbv = torch.from_numpy(c["sb"]).to(dev)
-    y = torch.empty((4096, 8192), dtype=torch.bfloat16, device=dev)
-    call = ops.matmul_i8_dequant_kernel(a, bt.t(), sa, sbv, y, 4096, 8192, 8192, prepare=True)
-    ms = event_time(torch, lambda i: call(), 20, 3, warm_s=0.5)
-    tops = 2.0 * 4096 * 8192 * 8192 / (ms * 1e-3) / 1e12
-    out.append({"config": "C5 int8 gemm 4096x8192x8192 + dequant", "kernel": call.kernel,
-                "us": round(ms * 1e3, 1), "value": round(tops, 1), "unit": "TOP/s", "bound": "mfma",
-                "frac": round(tops / INT8_PEAK_TOPS, 4)})
-    del a, bt, sa, sbv, y
-    torch.cuda.empty_cache()
-    if cpu:
-        yc = np.empty((4096, 8192), np.uint16)
-        b64 = c["bt"].T.astype(np.float64)
-        a64 = c["a"].astype(np.float64)
-        out[-1]["cpu_baseline"] = cpu_legs(
-            lambda r: lib.g950o_gemm_i8(P(c["a"]), P(c["bt"]), P(c["sa"]), P(c["sb"]), None, P(yc), 0, r, 8192, 8192),
-            lambda r: ref.dequant(np.rint(a64[:r] @ b64), c["sa"][:r], c["sb"]),
-            2.0 * 8192 * 8192, "TOP/s", 1e12, "rows of A (4096x8192x8192, int32 exact + dequant)", 8, 4096)
-        del yc, b64, a64
-    return out
+        t = timed(torch, lambda i: call(), 10, 2, warm_s=0.5)
+        rows.append(make_row(name, call.kernel, flops, "TFLOP/s", 1e12, BF16_PEAK_TFS, "mfma", t))
+    return rows
 
 
 def pmc_probe(torch, ops):
@@ -692,8 +763,9 @@ def main():
                     help="run only the counter-collection workload (for rocprofv3 --pmc)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="run only the GEMM + attention counter workload (for rocprofv3 --pmc)")
-    ap.add_argument("--hw-probe", action="store_true",
-                    help="run only the gfx950 micro-probes (compiler_amd/probes.py) and print them as JSON")
+    ap.add_argument("--only", default=None,
+                    help="comma-separated suite sections (" + ",".join(SECTIONS) + ", or 'headline'): run just "
+                         "these, without the CPU legs, and print their rows (one rocprofv3 trace per config)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {args.gpus}); the multi-GPU "
@@ -710,9 +782,21 @@ def main():
     if args.mfma_probe:
         mfma_probe(torch, ops)
         return
-    if args.hw_probe:
-        from compiler_amd import probes
-        print(json.dumps(probes.run(torch), indent=1))
+    if args.only:
+        only = set(args.only.split(","))
+        bad = only - set(SECTIONS) - {"headline"}
+        if bad:
+            sys.exit(f"bench.py: unknown --only sections {sorted(bad)} (known: headline, {', '.join(SECTIONS)})")
+        rows = {}
+        if "headline" in only:
+            value, ms_step, wall, roof, per_kernel, step_bytes = headline(torch, ops, args)
+            rows["headline"] = {"value": round(value, 1), "unit": "GB/s", "ms_per_step": round(ms_step, 5),
+                                "roofline": roof, "kernels": per_kernel}
+        rows["suite"] = suite(torch, ops, cpu=False, only=only - {"headline"})
+        for r in rows["suite"]:
+            log(f"bench:   {r['config']}: {r['value']} {r['unit']} ({r['frac'] * 100:.1f}% of peak; "
+                f"median {r['median_us']} us of {r['n_samples']})")
+        print(json.dumps({"only": sorted(only), **rows}), flush=True)
         return
     log("bench: headline (config 2) ...")
     value, ms_step, wall, roof, per_kernel, step_bytes = headline(torch, ops, args)

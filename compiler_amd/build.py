@@ -3,12 +3,9 @@
   compiler_amd/lib/g950.hsaco     every hot-path kernel (hipcc --genco, gfx950)
   compiler_amd/lib/libg950rt.so   the C-ABI module loader/launcher (include/g950rt.h)
   compiler_amd/lib/g950_exec      the bundle-driven command-line runner
-  compiler_amd/lib/g950_probes.hsaco  hardware micro-probes (measurement only)
-  compiler_amd/lib/g950_att_stamps.hsaco  attention kernels with phase stamps
-                                  (measurement only)
 
-Both are written next to the package so they travel with the source tree; the
-Python runtime loads exactly these two files.
+They are written next to the package so they travel with the source tree; the
+Python runtime loads exactly the first two.
 """
 from __future__ import annotations
 
@@ -24,8 +21,6 @@ LIB = PKG / "lib"
 HSACO = LIB / "g950.hsaco"
 RTLIB = LIB / "libg950rt.so"
 EXEC = LIB / "g950_exec"
-PROBES = LIB / "g950_probes.hsaco"
-STAMPS = LIB / "g950_att_stamps.hsaco"
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -72,30 +67,10 @@ def build_exec() -> Path:
     return EXEC
 
 
-def build_probes() -> Path:
-    """The micro-probe code object (compiler_amd/probes.py loads it)."""
-    LIB.mkdir(exist_ok=True)
-    tmp = PROBES.with_suffix(".hsaco.tmp")
-    _run([HIPCC, *DEVICE_FLAGS, "--genco", "-o", str(tmp), str(CSRC / "g950_probes.hip")])
-    os.replace(tmp, PROBES)
-    return PROBES
-
-
-def build_stamps() -> Path:
-    """The attention kernels with phase stamps (measurement only; probes.py)."""
-    LIB.mkdir(exist_ok=True)
-    tmp = STAMPS.with_suffix(".hsaco.tmp")
-    _run([HIPCC, *DEVICE_FLAGS, "--genco", f"-I{CSRC}", "-o", str(tmp), str(CSRC / "g950_att_stamps.hip")])
-    os.replace(tmp, STAMPS)
-    return STAMPS
-
-
 def build_all() -> None:
     build_code_object()
     build_runtime()
     build_exec()
-    build_probes()
-    build_stamps()
 
 
 if __name__ == "__main__":

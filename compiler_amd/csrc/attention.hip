@@ -53,17 +53,6 @@
 
 namespace g950 {
 
-
-
-// Phase-stamp hooks of the main loop: empty here; g950_att_stamps.hip (a
-// measurement-only code object) defines them to record s_memtime at the
-// phase boundaries of one workgroup and write the stamps over its output.
-#ifndef G950_ATT_STAMP
-#define G950_ATT_STAMP_DECL
-#define G950_ATT_STAMP(t, e)
-#define G950_ATT_STAMP_OUT
-#endif
-
 constexpr int ATT_BK = 64;     // keys per tile
 constexpr int ATT_KSLOTS = 2;  // K tiles in LDS: the one in use and the one in flight
 constexpr int ATT_VSLOTS = 2;  // V tiles in LDS: the one in use, the one in flight
@@ -265,7 +254,6 @@ template <int D, bool F16, int NW, bool VL>
 __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* vl) {
   using C = AttnCfg<D, NW>;
   __shared__ __attribute__((aligned(1024))) char lds[C::LDS];
-  G950_ATT_STAMP_DECL
   if (blockDim.x != C::NT) return;  // launch shape must match the instantiation
 
   const int tid = threadIdx.x;
@@ -627,17 +615,13 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   // done with K of tile t (its S^T was formed in iteration t-1) and V of
   // tile t-1, whose slots now take K of tile t+2 and V of tile t+1.
   for (int t = 0; t < ntiles; ++t) {
-    G950_ATT_STAMP(t, 0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    G950_ATT_STAMP(t, 1);
     if (t + 2 < ntiles) dma_part(true, t + 2);
     if (t + 1 < ntiles) dma_part(false, t + 1);
-    G950_ATT_STAMP(t, 2);
     const bool cur = active(t);
     const bool nxt = t + 1 < ntiles && active(t + 1);
     if (!lead && cur) softmax(t, s, pf);
-    G950_ATT_STAMP(t, 3);
     if (cur && nxt) {
       __builtin_amdgcn_s_setprio(2);
       mma_phase(t, s, pf);
@@ -646,12 +630,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
       if (cur) pv(t, pf);
       if (nxt) qk(t + 1, s);
     }
-    G950_ATT_STAMP(t, 4);
     if (lead && nxt) softmax(t + 1, s, pf);
-    G950_ATT_STAMP(t, 5);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  G950_ATT_STAMP_OUT
 
   // ---- epilogue: O = O / l ; lse = (ms + log2 l) * ln2
   const float l_sum = (l_run[0] + l_run[1]) + (l_run[2] + l_run[3]);
@@ -733,12 +714,14 @@ __device__ __forceinline__ void attn_f32_body(const AttnGenArgs& g) {
 #pragma unroll
   for (int b = 0; b < D / 32; ++b) o[b] = (f32x16){};
   float m = -__builtin_huge_valf(), l = 0.0f;
-  // fp32 inputs: the next tile's K and V rows are loaded into registers as
+  // fp32 inputs whose K/V rows are whole aligned 16-byte vectors (the host's
+  // kv_vec): the next tile's K and V rows are loaded into registers as
   // 16-byte vectors while the current tile is multiplied, then written to
   // LDS behind the next barrier; vector i of a thread is key (tid + 256 i) /
-  // (D / 4), columns 4 * ((tid + 256 i) % (D / 4)) .. +3
+  // (D / 4), columns 4 * ((tid + 256 i) % (D / 4)) .. +3.  Other inputs are
+  // staged element by element between the barriers.
   constexpr int NV = AF_BK * D / 4 / 256;
-  const bool f32 = g.dtype == DT_F32;
+  const bool f32 = g.dtype == DT_F32 && g.kv_vec;
   const float* kf = (const float*)p.k + koff;
   const float* vf = (const float*)p.v + voff;
   f32x4 kst[NV], vst[NV];

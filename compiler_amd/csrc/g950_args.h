@@ -102,6 +102,8 @@ struct AttnGenArgs {
   AttnArgs a;
   int D;
   int dtype;
+  int kv_vec;  // fp32 K/V reachable as 16-byte vectors: base 16-byte aligned,
+               // every z / head / row stride a multiple of 4 elements
 };
 
 // Variable-length attention (flash_varlen_fwd_kernel): per-batch sequences.

@@ -261,7 +261,7 @@ int main(int argc, char** argv) {
   printf(",\"repeats\":%u,\"repeats_all_equal\":%s,\"written\":%s,\"bundle_bytes\":%lld%s}\n", repeats,
          equal ? "true" : "false", write ? "true" : "false", (long long)sb.st_size, cmp.c_str());
   if (close_rc) return G950_SYNC;
-  if (!equal) return 5;
+  if (!equal) return G950_REPEAT_MISMATCH;
   if (!pass) return 7;
   return G950_OK;
 }

@@ -508,11 +508,17 @@ int op_layernorm(g950_module* m, const g950_view* views, uint32_t nviews, const 
 
 // softmax_kernel_inner (ops/suite/dev/softmax_kernel_inner.py:12-72): row
 // softmax of M rows of N contiguous elements at input_ptr + m * N, written to
-// output_ptr + m * N (flat buffers; the masked tail reads -inf).
+// output_ptr + m * N (flat buffers; the masked tail reads -inf).  With the
+// constexprs given (scalars M, N, ONE_TILE_PER_CTA, TILE_N), the one-tile
+// form with TILE_N < N normalises only the first TILE_N elements of each
+// row and leaves the rest of the output row untouched (:13-24: one
+// tl.arange(0, TILE_N) tile, masked by n < N); every other combination
+// covers the whole row (:25-72).
 int op_softmax_inner(g950_module* m, const g950_view* views, uint32_t nviews, const g950_scalar* sc,
                      uint32_t nsc, void* stream) {
-  if (nviews != 2 || nsc != 2)
-    return fail(G950_USAGE, "softmax_inner: needs views (input_ptr, output_ptr), scalars (M, N)");
+  if (nviews != 2 || (nsc != 2 && nsc != 4))
+    return fail(G950_USAGE, "softmax_inner: needs views (input_ptr, output_ptr), scalars (M, N) or "
+                "(M, N, ONE_TILE_PER_CTA, TILE_N)");
   View x, y;
   long long nx, ny, M, N;
   if (int rc = flat_view(views, 0, "input_ptr", x, false, nx)) return rc;
@@ -526,10 +532,18 @@ int op_softmax_inner(g950_module* m, const g950_view* views, uint32_t nviews, co
   if (M * N > nx || M * N > ny)
     return fail(G950_USAGE, "softmax_inner: M x N = %lld elements exceed input_ptr (%lld) or output_ptr (%lld)",
                 M * N, nx, ny);
+  long long cols = N;
+  if (nsc == 4) {
+    long long one_tile, tile_n;
+    if (int rc = scalar_int(&sc[2], "ONE_TILE_PER_CTA", one_tile)) return rc;
+    if (int rc = scalar_int(&sc[3], "TILE_N", tile_n)) return rc;
+    if (tile_n <= 0) return fail(G950_USAGE, "softmax_inner: TILE_N = %lld must be positive", tile_n);
+    if (one_tile && tile_n < N) cols = tile_n;
+  }
   RowArgs a{};
   a.x = x.v->data; a.y = y.v->data;
   a.x_row = N; a.y_row = N;
-  a.rows = (int)M; a.cols = (int)N;
+  a.rows = (int)M; a.cols = (int)cols;
   if (M == 0 || N == 0) return launch(m, "g950_rr_softmax_f32_v1_i1_b64", 0, 64u, a, stream);  // nothing stored
   return launch_rows(m, "softmax", a, x.v->dtype, x, y, nullptr, nullptr, stream);
 }
@@ -677,11 +691,35 @@ int op_matmul(g950_module* m, const g950_view* views, uint32_t nviews, const g95
     const char* name = mfma_kernel();
     return launch(m, name, (unsigned)tiles, (unsigned)kernel_threads(m, name, 512), g, stream);
   }
+  const bool rowb_ok = same16 && out16 && gemm_rowb_ok(a, b, (int)K, (int)N, esz);
+  // Row-major B read directly by the 16x16 MFMA kernel (transposing LDS
+  // reads): 16-bit operands, at least one 256 tile each way, whole 64-k
+  // slabs, A's farthest DMA row within a 32-bit offset (B's lane offsets
+  // span 16 k-rows of one slab)
+  if (rowb_ok && esz == 2 && M >= 256 && N >= 256 && K % 64 == 0 &&
+      (__int128)(M - 1) * a.stride[0] * 2 + 128 <= (__int128)0xFFFFFFFFll) {
+    g.a_s0 = a.stride[0];
+    g.b_s0 = b.stride[0];  // k-row stride of B
+    const int tiles = gemm_tiles(g);
+    if (tiles < 0) return fail(G950_USAGE, "matmul: too many tiles");
+    const char* name = a.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_gemm_bf16_256x256_rb" : "g950_gemm_f16_256x256_rb";
+    return launch(m, name, (unsigned)tiles, 512u, g, stream);
+  }
+  // Other row-major shapes (fp32, a dimension under one tile, a K tail): B
+  // is copied once into a K-contiguous Bt in the workspace, then the MFMA
+  // kernel runs on the copy.  A failed allocation is an error; under
+  // g950_launch_noalloc a copy larger than the scratch array runs the
+  // general kernel instead (the documented no-alloc fallback).
   void* bt = nullptr;
   const size_t bt_bytes = (size_t)N * (size_t)K * esz;
-  bool rowb = same16 && out16 && gemm_rowb_ok(a, b, (int)K, (int)N, esz) && bt_bytes <= ((size_t)1 << 31);
-  // without the workspace for the copy, the general kernel serves the call
-  if (rowb && m && workspace(m, stream, bt_bytes, &bt) != G950_OK) rowb = false;
+  bool rowb = rowb_ok && bt_bytes <= ((size_t)1 << 31);
+  if (rowb && m) {
+    if (t_scratch && bt_bytes > kScratchWorkspace) {
+      rowb = false;
+    } else if (int rc = workspace(m, stream, bt_bytes, &bt)) {
+      return rc;
+    }
+  }
   if (rowb) {
     GemmArgs t{};
     t.b = g.b; t.b_s0 = b.stride[0]; t.c = bt; t.N = (int)N; t.K = (int)K;
@@ -885,9 +923,67 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
     // the kernels index the scale densely: only a contiguous scale row is taken
     return fail(G950_USAGE, "dequant_matmul: b_scale_ptr must be contiguous");
   }
-  const bool fast = is_float16ish(a.v->dtype) && K % 16 == 0 && (K < 2 || (a.stride[1] == 1 && b.stride[0] == 1)) &&
-                    a.stride[0] % 8 == 0 && b.stride[1] % 16 == 0 && aligned16(a.addr()) && aligned16(b.addr()) &&
-                    y.stride[1] == 1 && aligned16(y.addr());
+  // 16-bit A with K-contiguous rows, output rows contiguous
+  const bool a16 = is_float16ish(a.v->dtype) && K % 16 == 0 && (K < 2 || a.stride[1] == 1) && a.stride[0] % 8 == 0 &&
+                   aligned16(a.addr()) && y.stride[1] == 1 && aligned16(y.addr());
+  // int8 B stored K-contiguous (Bt [N, K]) with 16-byte rows
+  bool fast = a16 && (K < 2 || b.stride[0] == 1) && b.stride[1] % 16 == 0 && aligned16(b.addr());
+  long long bts = b.stride[1];  // Bt row (n) stride of the operand the fast routes read
+  const long long cus = m ? m->cus : 256;
+  const bool bf16 = a.v->dtype == G950_DTYPE_BFLOAT16;
+  // The reference's own weight layout, int8 b row-major [K, N] (stride_bk = N,
+  // stride_bn = 1, ops/suite/perf/dequantize_matmul.py:62-65):
+  //   * at least one 256 tile each way and whole 64-k slabs: the weights are
+  //     widened as they lie into an exact bf16 / f16 [K, N] copy in the
+  //     workspace, and the row-major-B MFMA kernel runs on it with the scale
+  //     in its epilogue;
+  //   * otherwise the int8 weights are transposed once into a K-contiguous
+  //     copy in the workspace and the routes below (B-streaming decode
+  //     kernels, fused 128x128 kernel) run on it.
+  // Under g950_launch_noalloc a copy larger than the scratch array leaves
+  // the call to the general kernel (the documented no-alloc fallback).
+  const bool nrow = a16 && !fast && K > 1 && N > 1 && b.stride[1] == 1 && N % 16 == 0 && b.stride[0] % 16 == 0 &&
+                    aligned16(b.addr());
+  auto fits = [&](unsigned long long bytes) {
+    return bytes <= (1ull << 31) && !(t_scratch && bytes > kScratchWorkspace);
+  };
+  if (nrow && M >= 256 && N >= 256 && K % 64 == 0 && fits((unsigned long long)K * N * 2) &&
+      (__int128)(M - 1) * a.stride[0] * 2 + 128 <= (__int128)0xFFFFFFFFll) {
+    void* wide = nullptr;
+    if (m)
+      if (int rc = workspace(m, stream, (size_t)(K * N * 2), &wide)) return rc;
+    GemmArgs w{};
+    w.b = g.b; w.b_s0 = b.stride[0]; w.N = (int)K; w.K = (int)N;  // K rows of N weights
+    w.c = wide;
+    const long long chunks = K * (N / 16);
+    if (int rc = launch(m, bf16 ? "g950_widen_i8_bf16" : "g950_widen_i8_f16", (unsigned)((chunks + 255) / 256), 256u,
+                        w, stream))
+      return rc;
+    g.b = wide; g.b_dtype = (int)a.v->dtype;
+    g.a_s0 = a.stride[0];
+    g.b_s0 = N;  // k-row stride of the copy
+    g.bscale = nullptr;
+    g.cscale = s.v->data; g.cscale_dtype = (int)s.v->dtype;
+    const int tiles = gemm_tiles(g);
+    if (tiles < 0) return fail(G950_USAGE, "dequant_matmul: too many tiles");
+    const char* name = bf16 ? "g950_gemm_bf16_256x256_rb" : "g950_gemm_f16_256x256_rb";
+    return launch(m, name, (unsigned)tiles, 512u, g, stream);
+  }
+  bool transposed = false;
+  if (nrow && fits((unsigned long long)K * N)) {
+    void* bt = nullptr;
+    if (m)
+      if (int rc = workspace(m, stream, (size_t)(K * N), &bt)) return rc;
+    GemmArgs t{};
+    t.b = g.b; t.b_s0 = b.stride[0]; t.c = bt; t.N = (int)N; t.K = (int)K;
+    const long long tblocks = ((K + 63) / 64) * ((N + 63) / 64);
+    if (tblocks > 0x7FFFFFFF) return fail(G950_USAGE, "dequant_matmul: too many tiles");
+    if (int rc = launch(m, "g950_transpose_b8", (unsigned)tblocks, 256u, t, stream)) return rc;
+    g.b = bt;
+    bts = K;
+    fast = true;
+    transposed = true;  // the workspace now holds the copy: no second copy below
+  }
   if (fast && M <= 64) {
     // decode shapes: the few-row kernels stream B, 32 columns and all of K
     // per workgroup (8 waves, one K range each, summed in LDS), for up to 16,
@@ -898,15 +994,14 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
     // 16x4096x11008 27.1 -> 19.8, 16x11008x4096 22.2 -> 21.1, 1x8192x8192
     // 20.9 -> 15.1; 16x8192x8192 ties and 16x8192x8000 loses (21.7 -> 24.8).
     g.a_s0 = a.stride[0];
-    g.b_s0 = b.stride[1];
-    const long long cus = m ? m->cus : 256;
+    g.b_s0 = bts;
     const long long blocks32 = (N + 31) / 32;
     const bool c16 = M <= 16 && (M == 1 || blocks32 < cus || 4 * blocks32 > 5 * cus);
     const long long blocks = c16 ? (N + 15) / 16 : blocks32;
     if (blocks > 0x7FFFFFFF) return fail(G950_USAGE, "dequant_matmul: too many tiles");
     char name[48];
     snprintf(name, sizeof name, "g950_gemm_w8a16_skinny%s_%s", c16 ? "_c16" : M <= 16 ? "" : M <= 32 ? "32" : "64",
-             a.v->dtype == G950_DTYPE_BFLOAT16 ? "bf16" : "f16");
+             bf16 ? "bf16" : "f16");
     return launch(m, name, (unsigned)blocks, 512u, g, stream);
   }
   // Many output tiles: widen B once into an exact bf16 / f16 copy in the
@@ -915,17 +1010,17 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
   // which costs more than one copy (3 bytes per weight through HBM) once the
   // 256x256 tiles outnumber half the CUs.  Measured on MI355X at N = K = 8192:
   // M = 1024 (128 tiles) 186 us fused vs 148 + 36 us; M = 1536 334 vs 172 + 36.
-  const long long cus = m ? m->cus : 256;
-  const bool bf16 = a.v->dtype == G950_DTYPE_BFLOAT16;
   void* wide = nullptr;
-  bool widened = fast && K > 0 && K % 64 == 0 && 2 * ((M + 255) / 256) * ((N + 255) / 256) > cus &&
+  bool widened = fast && !transposed && K > 0 && K % 64 == 0 && 2 * ((M + 255) / 256) * ((N + 255) / 256) > cus &&
                  (unsigned long long)N * K * 2 <= (1ull << 31);
-  // without the workspace for the copy, the fused kernel below (which needs
-  // none) serves the call
-  if (widened && m && workspace(m, stream, (size_t)(N * K * 2), &wide) != G950_OK) widened = false;
+  // without room for the copy in the no-alloc scratch, the fused kernel below
+  // (which needs none) serves the call; a failed allocation is an error
+  if (widened && t_scratch && (size_t)(N * K * 2) > kScratchWorkspace) widened = false;
+  if (widened && m)
+    if (int rc = workspace(m, stream, (size_t)(N * K * 2), &wide)) return rc;
   if (widened) {
     GemmArgs w{};
-    w.b = g.b; w.b_s0 = b.stride[1]; w.N = (int)N; w.K = (int)K;
+    w.b = g.b; w.b_s0 = bts; w.N = (int)N; w.K = (int)K;
     void* ws = wide;
     w.c = ws;
     const long long chunks = N * (K / 16);
@@ -948,13 +1043,13 @@ int op_dequant_matmul(g950_module* m, const g950_view* views, uint32_t nviews, c
   }
   if (fast) {
     g.a_s0 = a.stride[0];
-    g.b_s0 = b.stride[1];  // Bt row (n) stride
+    g.b_s0 = bts;  // Bt row (n) stride
     g.tiles_m = (int)((M + 127) / 128);
     g.tiles_n = (int)((N + 127) / 128);
     const long long tiles = (long long)g.tiles_m * g.tiles_n;
     if (tiles > 0x7FFFFFFF) return fail(G950_USAGE, "dequant_matmul: too many tiles");
-    return launch(m, a.v->dtype == G950_DTYPE_BFLOAT16 ? "g950_gemm_w8a16_bf16_128x128" : "g950_gemm_w8a16_f16_128x128",
-                  (unsigned)tiles, 256u, g, stream);
+    return launch(m, bf16 ? "g950_gemm_w8a16_bf16_128x128" : "g950_gemm_w8a16_f16_128x128", (unsigned)tiles, 256u, g,
+                  stream);
   }
   g.a_s0 = a.stride[0]; g.a_s1 = a.stride[1];
   g.b_s0 = b.stride[0]; g.b_s1 = b.stride[1];
@@ -1067,6 +1162,10 @@ int launch_attention(g950_module* m, AttnArgs& a, uint32_t dt, long long D, cons
   ga.a = a;
   ga.D = (int)D;
   ga.dtype = (int)dt;
+  // the fp32 MFMA kernel's vector staging reads K/V rows as 16-byte vectors
+  // at every (z, head, row): only for aligned bases and strides of whole vectors
+  ga.kv_vec = dt == G950_DTYPE_FLOAT32 && aligned16(k.addr()) && aligned16(v.addr()) && a.k_sz % 4 == 0 &&
+              a.k_sh % 4 == 0 && a.k_ss % 4 == 0 && a.v_sz % 4 == 0 && a.v_sh % 4 == 0 && a.v_ss % 4 == 0;
   if (D == 32 || D == 64 || D == 128) {
     // fp32 (and 16-bit inputs the kernel above does not take) on the fp32
     // MFMA: 4 waves x 32 queries per workgroup, any scale
@@ -1438,6 +1537,13 @@ int g950_validate(uint32_t op, const g950_view* views, uint32_t nviews, const g9
 
 const char* g950_last_kernel(void) { return t_kernel.c_str(); }
 
+size_t g950_workspace_bytes(g950_module* m, void* stream) {
+  if (!m) return 0;
+  std::lock_guard<std::mutex> lock(m->ws_mu);
+  const auto it = m->ws.find(stream);
+  return it == m->ws.end() ? 0 : it->second.second;
+}
+
 int g950_sync(void* stream) {
   hipError_t e = hipStreamSynchronize((hipStream_t)stream);
   if (e != hipSuccess) return fail(G950_SYNC, "g950_sync: %s", hipGetErrorString(e));
@@ -1450,6 +1556,7 @@ const char* g950_strerror(int code) {
     case G950_USAGE: return "operator contract refused";
     case G950_REJECTED: return "view rejected";
     case G950_RESOURCE: return "HIP resource or launch failure";
+    case G950_REPEAT_MISMATCH: return "repeats produced different outputs";
     case G950_SYNC: return "stream synchronisation failed";
     default: return "unknown";
   }

@@ -66,6 +66,18 @@ constexpr int SLAB = 128;          // bytes of K per row per LDS stage (two stag
 // row (K % 64 != 0 kernels only)
 __device__ __attribute__((aligned(128))) const uint32_t g950_zero_line[32] = {};
 
+// One 16-byte-per-lane global->LDS DMA instruction (global_load_lds_dwordx4,
+// scalar base + 32-bit lane offset, LDS destination in M0) written as inline
+// asm: the compiler then sees no LDS write in flight and adds no vmcnt wait
+// before the transposing LDS reads (ds_read_tr16_b64), whose address it
+// cannot compare with a DMA destination.  Completion is the slab protocol's
+// explicit vmcnt(0) + barrier.  (s_nop 0: one wait state between the M0
+// write and the DMA.)
+__device__ __forceinline__ void dma16_asm(const char* sbase, uint32_t voff, uint32_t lds_dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_dst);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+
 // Map the linear workgroup id to a (tile_m, tile_n): XCD-contiguous, then
 // grouped by 4 tile-rows.
 __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -283,7 +295,21 @@ __device__ __forceinline__ void mfma_step(const u32x4& bfrag, const u32x4& afrag
 // ending at the matrix edge (every DMA row lies inside the operands, so a
 // lane's DMA source is a fixed 32-bit offset plus a wave-uniform base, no
 // per-row clamp) and stores only its own rows and columns.
-template <int MODE, int WM, int WN, int UMASK>
+//
+// BROW (16-bit only): B is the reference matmul's own row-major [K, N]
+// (N-contiguous, ops/suite/perf/matmul.py:33) and is read as it lies, with
+// no transposed copy.  A slab's 64 k-rows of the tile's 256 columns land in
+// LDS as four 64-column blocks of 64 rows x 128 bytes -- the same 8-row x
+// 128-byte DMA instruction as the K-contiguous operands, whole 128-byte
+// lines of B -- and each B fragment (16 columns x 8 k per lane) comes out of
+// two ds_read_b64_tr_b16 (gfx950's transposing read: in each 16-lane group,
+// lane 4r + j reads 4 columns of k-row r and lane i receives column i of the
+// four rows).  The 16-byte chunks of k-row k are XOR-swizzled by
+// 2 * (((k >> 1) & 1) | (((k >> 3) & 1) << 1)), so the eight k-rows a half
+// wave reads (k, k+1, k+2, k+3 and the same eight rows on) cover the 64 banks
+// once.  Stages sit as [A0][B0][B1][A1] so a B read of either stage is one
+// per-lane base plus an immediate below 64 KiB.
+template <int MODE, int WM, int WN, int UMASK, bool BROW = false>
 __device__ __forceinline__ void gemm_mfma16_body(const GemmArgs& p, char* lds) {
   constexpr int NW = WM * WN;
   constexpr int STAGE = (BM + BN) * SLAB;     // 64 KiB
@@ -292,6 +318,10 @@ __device__ __forceinline__ void gemm_mfma16_body(const GemmArgs& p, char* lds) {
   constexpr int H = GROUPS / 2;
   static_assert(GROUPS * 8 * DW == BM + BN && GROUPS % 2 == 0 && (BM / 8) % GROUPS == 0,
                 "each DMA wave's groups lie in one operand");
+  static_assert(!BROW || (MODE == GEMM_BF16 || MODE == GEMM_F16), "row-major B: 16-bit operands");
+  // LDS byte offsets of stage s's A and B slabs
+  constexpr int A_OFF[2] = {0, BROW ? STAGE + BN * SLAB : STAGE};
+  constexpr int B_OFF[2] = {BM * SLAB, BROW ? BM * SLAB + BN * SLAB : STAGE + BM * SLAB};
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -314,28 +344,49 @@ __device__ __forceinline__ void gemm_mfma16_body(const GemmArgs& p, char* lds) {
   // (lane: row lane / 8, 16-byte slot lane % 8 holding chunk slot ^ ((row >>
   // 1) & 7)).  Group t's rows are the first group's plus 8t, and the
   // swizzle repeats every second group, so a lane needs two offsets.
+  // Row-major B: group g (of the slab's 32) is column block g / 8, k-rows
+  // 8 (g % 8) .. +7; its swizzle repeats every second group too.
   const bool dma_a = wave * GROUPS < BM / 8;
+  const bool dma_brow = BROW && !dma_a;
   const long long ld = dma_a ? lda_b : ldb_b;
-  const char* obase = dma_a ? abase : bbase;
+  // per-slab step of the DMA source: 128 bytes of K, or 64 k-rows of row-major B
+  const long long slab_step = dma_brow ? 64 * ldb_b : SLAB;
+  const int g0 = dma_a ? wave * GROUPS : wave * GROUPS - BM / 8;  // first group of this wave in its operand
+  const char* obase = dma_a ? abase : dma_brow ? (const char*)p.b + (long long)n0 * 2 + (g0 >> 3) * 128 : bbase;
   uint32_t doff[2];
   {
-    const int row0 = ((dma_a ? wave * GROUPS : wave * GROUPS - BM / 8) * 8) + (lane >> 3);
+    const int r8 = lane >> 3;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int row = row0 + 8 * j;
-      doff[j] = (uint32_t)((long long)row * ld + (((lane & 7) ^ ((row >> 1) & 7)) * 16));
+      if (dma_brow) {
+        const int k = 8 * j + r8;
+        const int sw = 2 * (((k >> 1) & 1) | (((k >> 3) & 1) << 1));
+        doff[j] = (uint32_t)((long long)k * ld + (((lane & 7) ^ sw) * 16));
+      } else {
+        const int row = g0 * 8 + r8 + 8 * j;
+        doff[j] = (uint32_t)((long long)row * ld + (((lane & 7) ^ ((row >> 1) & 7)) * 16));
+      }
     }
   }
+  // LDS byte address of the stages (the asm DMA's M0)
+  const uint32_t lds32 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds;
   auto issue = [&](int stage, int slab, int t0, int t1) {
-    char* st = lds + stage * STAGE;
+    char* st = lds + (dma_a ? A_OFF[stage] : B_OFF[stage]);
 #pragma unroll
     for (int t = t0; t < t1; ++t) {
-      const char* ub = obase + (long long)slab * SLAB + (long long)(t & ~1) * 8 * ld;
-      asm volatile("" : "+v"(doff[t & 1]));
-      const char* src = ub + (uint64_t)doff[t & 1];
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(st + (wave * GROUPS + t) * 1024),
-                                       16, 0, 0);
+      // wave-uniform part of group t's source: column block and row pair
+      const long long grp = dma_brow ? (long long)(t >> 3) * 128 + (long long)((t & 7) & ~1) * 8 * ld
+                                     : (long long)(t & ~1) * 8 * ld;
+      const char* ub = obase + (long long)slab * slab_step + grp;
+      if constexpr (BROW) {
+        dma16_asm(ub, doff[t & 1], lds32 + (uint32_t)((dma_a ? A_OFF[stage] : B_OFF[stage]) + (g0 + t) * 1024));
+      } else {
+        asm volatile("" : "+v"(doff[t & 1]));
+        const char* src = ub + (uint64_t)doff[t & 1];
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                         (__attribute__((address_space(3))) void*)(st + (g0 + t) * 1024),
+                                         16, 0, 0);
+      }
     }
   };
   // ---- 16x16 output fragments (v_mfma_f32_16x16x32_{bf16,f16} /
@@ -365,9 +416,22 @@ __device__ __forceinline__ void gemm_mfma16_body(const GemmArgs& p, char* lds) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int sw = (((ks * 4 + g4) ^ ((l16 >> 1) & 7)) << 4) + l16 * SLAB;
-      aoff[s_][ks] = s_ * STAGE + wm * (BM / WM) * SLAB + sw;
-      boff[s_][ks] = s_ * STAGE + BM * SLAB + wn * (BN / WN) * SLAB + sw;
+      aoff[s_][ks] = A_OFF[s_] + wm * (BM / WM) * SLAB + sw;
+      boff[s_][ks] = B_OFF[s_] + wn * (BN / WN) * SLAB + sw;
     }
+  // Row-major B fragment ni of k-step ks: lane (g4, 4 r + j) reads k-rows
+  // 32 ks + 8 g4 + r (and + 4) at columns 4 j .. 4 j + 3 of the fragment's 16,
+  // in column block 2 wn + ni / 4, chunk pair (ni % 4) ^ swizzle: the lane's
+  // base for each ni % 4 (stage 0), everything else an immediate (stage 1 is
+  // the next 32 KiB).
+  int btr[4];
+  if constexpr (BROW) {
+    const int r = l16 >> 2, j = l16 & 3;
+    const int sw = ((r >> 1) & 1) | ((g4 & 1) << 1);
+#pragma unroll
+    for (int cp = 0; cp < 4; ++cp)
+      btr[cp] = B_OFF[0] + (2 * wn) * 64 * SLAB + (8 * g4 + r) * SLAB + 32 * (cp ^ sw) + 8 * j;
+  }
   u32x4 a16[2][FM16], b16[FN16];
   auto afrag = [&](auto sc, int ks, int buf) {
     constexpr int S = decltype(sc)::value;
@@ -376,7 +440,18 @@ __device__ __forceinline__ void gemm_mfma16_body(const GemmArgs& p, char* lds) {
   };
   auto bfrag = [&](auto sc, int ks, int ni) {
     constexpr int S = decltype(sc)::value;
-    b16[ni] = *(const u32x4*)(lds + boff[S][ks] + ni * 16 * SLAB);
+    if constexpr (BROW) {
+      typedef short s16x4 __attribute__((ext_vector_type(4)));
+      const int off = btr[ni & 3] + S * BN * SLAB + (ni >> 2) * 64 * SLAB + ks * 32 * SLAB;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(lds + off));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(lds + off + 4 * SLAB));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      b16[ni] = (u32x4){l2[0], l2[1], h2[0], h2[1]};
+    } else {
+      b16[ni] = *(const u32x4*)(lds + boff[S][ks] + ni * 16 * SLAB);
+    }
   };
   auto mma = [&](const u32x4& bv, const u32x4& av, f32x4& cf, i32x4& ci) {
     if constexpr (MODE == GEMM_BF16)
@@ -395,8 +470,12 @@ __device__ __forceinline__ void gemm_mfma16_body(const GemmArgs& p, char* lds) {
   // its last MFMA has issued -- and ndma DMA instructions spread over the
   // slots; an explicit lgkmcnt(0) closes the k-step (the compiler cannot
   // count LDS reads issued behind a DMA).
+  // (BROW: the DMA is inline asm, which the scheduling groups cannot place,
+  // so the k-step issues its ndma DMA groups itself, dt0.. of slab dslab into
+  // stage dst, one behind each B fragment's reads; the asm keeps its place
+  // among the LDS reads.)
   constexpr int NMF16 = FM16 * FN16;
-  auto kstep = [&](auto bc, auto nsc, int nks, int ndma) {
+  auto kstep = [&](auto bc, auto nsc, int nks, int ndma, int dst = 0, int dslab = 0, int dt0 = 0) {
     constexpr int buf = decltype(bc)::value;
     afrag(nsc, nks, buf ^ 1);
     if constexpr (UMASK & 1) {
@@ -409,13 +488,16 @@ __device__ __forceinline__ void gemm_mfma16_body(const GemmArgs& p, char* lds) {
 #pragma unroll
       for (int mi = 0; mi < FM16; ++mi) mma(b16[ni], a16[buf][mi], acf[mi][ni], aci[mi][ni]);
       bfrag(nsc, nks, ni);
+      if constexpr (BROW) {
+        if (ni < ndma) issue(dst, dslab, dt0 + ni, dt0 + ni + 1);
+      }
     }
 #pragma unroll
     for (int i = 0; i < NMF16; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       if (i < FM16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (i % FM16 == FM16 - 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (ndma && i % (NMF16 / ndma) == 1 && i / (NMF16 / ndma) < ndma)
+      if (i % FM16 == FM16 - 1) __builtin_amdgcn_sched_group_barrier(0x100, BROW ? 2 : 1, 0);
+      if (!BROW && ndma && i % (NMF16 / ndma) == 1 && i / (NMF16 / ndma) < ndma)
         __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -438,12 +520,13 @@ __device__ __forceinline__ void gemm_mfma16_body(const GemmArgs& p, char* lds) {
     constexpr bool DMA = decltype(dc)::value;
     auto slab_iter = [&](auto cc, int kt) {
       constexpr int CUR = decltype(cc)::value, NXT = CUR ^ 1;
-      if constexpr (DMA) issue(NXT, min(kt + 1, last), H, GROUPS);
-      kstep(S0{}, cc, 1, DMA ? H : 0);
+      if constexpr (DMA && !BROW) issue(NXT, min(kt + 1, last), H, GROUPS);
+      kstep(S0{}, cc, 1, DMA ? H : 0, NXT, min(kt + 1, last), H);
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (DMA) issue(CUR, min(kt + 2, last), 0, H);
-      kstep(S1{}, std::integral_constant<int, NXT>{}, 0, DMA ? H : 0);  // (after the last slab: a stale stage, never used)
+      if constexpr (DMA && !BROW) issue(CUR, min(kt + 2, last), 0, H);
+      // (after the last slab: a stale stage, never used)
+      kstep(S1{}, std::integral_constant<int, NXT>{}, 0, DMA ? H : 0, CUR, min(kt + 2, last), 0);
     };
     int kt = 0;
     for (; kt + 1 < kslabs; kt += 2) {
@@ -734,6 +817,34 @@ __device__ __forceinline__ void transpose32_body(const GemmArgs& p) {
     if (n0 + n < p.N && k0 + k4 < p.K) {
       const u32x4 w = {t[k4][n], t[k4 + 1][n], t[k4 + 2][n], t[k4 + 3][n]};
       *(u32x4*)((uint32_t*)p.c + (long long)(n0 + n) * p.K + k0 + k4) = w;
+    }
+  }
+}
+
+// The same for bytes (int8 weights, N % 16 == 0, K % 16 == 0, 16-byte aligned
+// rows): 64 x 64 byte tiles, one 16-byte load (a k-row's 16 columns) and one
+// 16-byte store (an n-row's 16 k) per thread, bytes staged as 32-bit slots
+// with a 65-slot pitch.
+__device__ __forceinline__ void transpose8_body(const GemmArgs& p) {
+  __shared__ uint32_t t[64][65];
+  const int tiles_n = (p.N + 63) / 64;
+  const int k0 = (blockIdx.x / tiles_n) * 64, n0 = (blockIdx.x % tiles_n) * 64;
+  {
+    const int k = threadIdx.x >> 2, n16 = (threadIdx.x & 3) * 16;
+    if (k0 + k < p.K && n0 + n16 < p.N) {
+      const u32x4 w = *(const u32x4*)((const uint8_t*)p.b + (long long)(k0 + k) * p.b_s0 + n0 + n16);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) t[k][n16 + e] = (w[e >> 2] >> (8 * (e & 3))) & 0xFFu;
+    }
+  }
+  __syncthreads();
+  {
+    const int n = threadIdx.x >> 2, k16 = (threadIdx.x & 3) * 16;
+    if (n0 + n < p.N && k0 + k16 < p.K) {
+      u32x4 w = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) w[e >> 2] |= t[k16 + e][n] << (8 * (e & 3));
+      *(u32x4*)((uint8_t*)p.c + (long long)(n0 + n) * p.K + k0 + k16) = w;
     }
   }
 }
@@ -1166,6 +1277,14 @@ __device__ __forceinline__ void gemm_general_body(const GemmArgs& p) {
   extern "C" __global__ __launch_bounds__(WM * WN * 64) void NAME(const g950::GemmArgs p) {  \
     g950::gemm_mfma_body<MODE, WM, WN, UMASK, KT>(p);                                      \
   }
+// row-major B [K, N] read directly (M, N >= 256, whole 64-k slabs; host checks)
+#define G950_GEMM_MFMA_RB(NAME, MODE)                                                       \
+  extern "C" __global__ __launch_bounds__(512) void NAME(const g950::GemmArgs p) {         \
+    __shared__ __attribute__((aligned(1024))) char lds[4 * g950::BM * g950::SLAB];        \
+    g950::gemm_mfma16_body<MODE, 4, 2, 0, true>(p, lds);                                   \
+  }
+G950_GEMM_MFMA_RB(g950_gemm_bf16_256x256_rb, g950::GEMM_BF16)
+G950_GEMM_MFMA_RB(g950_gemm_f16_256x256_rb, g950::GEMM_F16)
 G950_GEMM_MFMA(g950_gemm_bf16_256x256, g950::GEMM_BF16, 4, 2, 0, false)
 G950_GEMM_MFMA(g950_gemm_f16_256x256, g950::GEMM_F16, 4, 2, 0, false)
 G950_GEMM_MFMA(g950_gemm_i8_256x256, g950::GEMM_I8, 4, 2, 0, false)
@@ -1178,6 +1297,9 @@ extern "C" __global__ __launch_bounds__(256) void g950_transpose_b16(const g950:
 }
 extern "C" __global__ __launch_bounds__(256) void g950_transpose_b32(const g950::GemmArgs p) {
   g950::transpose32_body(p);
+}
+extern "C" __global__ __launch_bounds__(256) void g950_transpose_b8(const g950::GemmArgs p) {
+  g950::transpose8_body(p);
 }
 // fp32 on v_mfma_f32_32x32x2_f32 (the matmul corpus's base dtype)
 G950_GEMM_MFMA(g950_gemm_f32_256x256, g950::GEMM_F32, 4, 2, 0, false)

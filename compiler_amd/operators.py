@@ -42,14 +42,15 @@ def softmax_kernel_inner(output_ptr, input_ptr, M, N, TILE_N=None, ONE_TILE_PER_
                          sync=False, prepare=False):
     """Row softmax over flat buffers (ops/suite/dev/softmax_kernel_inner.py:12-72):
     row m is the N contiguous elements at input_ptr + m*N, written to
-    output_ptr + m*N.  TILE_N / ONE_TILE_PER_CTA only shaped the reference's
-    tiles; the one-tile form covers a whole row only when TILE_N >= N, so a
-    call that asks for one tile narrower than the row is refused."""
-    if ONE_TILE_PER_CTA and TILE_N is not None and int(TILE_N) < int(N):
-        raise rt.G950Error(rt.USAGE, "softmax_kernel_inner: ONE_TILE_PER_CTA with TILE_N < N normalises only "
-                                     "the first TILE_N columns; not supported")
+    output_ptr + m*N.  With both constexprs given they travel as scalars: the
+    one-tile form (ONE_TILE_PER_CTA) with TILE_N < N normalises only the first
+    TILE_N elements of each row and leaves the rest of the output untouched,
+    as the reference's single masked tile does (:13-24)."""
+    scalars = {"M": M, "N": N}
+    if TILE_N is not None and ONE_TILE_PER_CTA is not None:
+        scalars.update(ONE_TILE_PER_CTA=bool(ONE_TILE_PER_CTA), TILE_N=int(TILE_N))
     return _launch(rt.OP_SOFTMAX_INNER, {"input_ptr": input_ptr, "output_ptr": output_ptr}, {"output_ptr"},
-                   {"M": M, "N": N}, stream, sync, prepare)
+                   scalars, stream, sync, prepare)
 
 
 def layer_norm_forward_row(Y_ptr, Y_row_stride, X_ptr, X_row_stride, W_ptr, B_ptr, Mean_ptr, Mean_row_stride,
@@ -174,8 +175,10 @@ def layernorm_kernel(X, Y, W, B, Mean, Rstd, stride, N, eps, *, stream=None, syn
 
 def matmul_kernel(a_ptr, b_ptr, y_ptr, M, N, K, *, stream=None, sync=False, prepare=False):
     """Y = A.B with fp32 accumulation (ops/suite/perf/matmul.py:21-37).
-    ``b_ptr`` is the logical [K, N] operand; a column-major (K-contiguous) b,
-    e.g. ``bt.t()`` of a row-major [N, K] tensor, takes the MFMA path."""
+    ``b_ptr`` is the logical [K, N] operand in either layout: column-major
+    (K-contiguous, e.g. ``bt.t()`` of a row-major [N, K] tensor) or the
+    reference's row-major [K, N], which the MFMA kernel reads as it lies
+    (transposing LDS reads) from one 256 tile each way."""
     return _launch(rt.OP_MATMUL, {"a_ptr": a_ptr, "b_ptr": b_ptr, "y_ptr": y_ptr}, {"y_ptr"},
                    {"M": M, "N": N, "K": K}, stream, sync, prepare)
 
@@ -284,7 +287,7 @@ def layernorm(x, w, b, eps, out=None, mean=None, rstd=None, **kw):
 
 
 def matmul(a, b, out=None, **kw):
-    """a [M,K] @ b [K,N] (pass ``bt.t()`` for a K-contiguous b)."""
+    """a [M,K] @ b [K,N] (row-major b, or ``bt.t()`` for a K-contiguous one)."""
     import torch
     m, k = a.shape
     n = b.shape[1]

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "lib" / "libg950rt.so"
 HSACO_PATH = PKG / "lib" / "g950.hsaco"
 
-OK, USAGE, REJECTED, RESOURCE, SYNC = 0, 2, 3, 4, 6
+OK, USAGE, REJECTED, RESOURCE, REPEAT_MISMATCH, SYNC = 0, 2, 3, 4, 5, 6
 
 # operator contracts (include/g950rt.h)
 OP_SOFTMAX = 1
@@ -41,7 +41,8 @@ OP_GQA = 16
 DT_BOOL, DT_INT8, DT_UINT8, DT_INT16, DT_UINT16, DT_INT32 = 1, 2, 3, 4, 5, 6
 DT_UINT32, DT_INT64, DT_UINT64, DT_F16, DT_BF16, DT_F32, DT_F64 = 7, 8, 9, 10, 11, 12, 13
 
-EXPORTS = ("g950_open", "g950_launch", "g950_launch_noalloc", "g950_validate", "g950_last_kernel", "g950_sync", "g950_strerror",
+EXPORTS = ("g950_open", "g950_launch", "g950_launch_noalloc", "g950_workspace_bytes", "g950_validate",
+           "g950_last_kernel", "g950_sync", "g950_strerror",
            "g950_last_error", "g950_close", "g950_bundle_open", "g950_bundle_check", "g950_bundle_reason",
            "g950_bundle_count", "g950_bundle_view", "g950_bundle_scalar", "g950_bundle_exec",
            "g950_bundle_close")
@@ -111,6 +112,8 @@ def load_library():
         lib.g950_launch.restype = ctypes.c_int
         lib.g950_launch_noalloc.argtypes = lib.g950_launch.argtypes
         lib.g950_launch_noalloc.restype = ctypes.c_int
+        lib.g950_workspace_bytes.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        lib.g950_workspace_bytes.restype = ctypes.c_size_t
         lib.g950_validate.argtypes = [ctypes.c_uint32, ctypes.POINTER(View), ctypes.c_uint32,
                                       ctypes.POINTER(Scalar), ctypes.c_uint32]
         lib.g950_validate.restype = ctypes.c_int
@@ -245,6 +248,15 @@ class Module:
             if rc != OK:
                 raise G950Error(rc, self._lib.g950_last_error().decode())
         return self.last_kernel
+
+    def workspace_bytes(self, stream=None) -> int:
+        """Device workspace bytes the library holds for ``stream`` (the
+        current stream by default); g950_launch_noalloc never changes it."""
+        import torch
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device)
+        handle = ctypes.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else stream)
+        return int(self._lib.g950_workspace_bytes(self._handle, handle))
 
     def prepare(self, op: int, tensors, outputs, scalars, stream=None):
         """Pack the call once; the returned object re-launches it with one C

@@ -41,6 +41,7 @@ extern "C" {
 #define G950_USAGE 2      /* operator contract / shape / scalar refused */
 #define G950_REJECTED 3   /* a view violates its storage or layout rules */
 #define G950_RESOURCE 4   /* HIP error: module load, launch, allocation */
+#define G950_REPEAT_MISMATCH 5 /* g950_exec: repeats produced different outputs */
 #define G950_SYNC 6       /* stream synchronisation failed */
 
 /* dtype codes (a100c/runtime/a100rt.h:58-72) */
@@ -153,7 +154,10 @@ typedef struct g950_scalar {
  *                      input_ptr + m*N, written to output_ptr + m*N
  *   views   input_ptr, output_ptr: flat (any rank, C-contiguous, >= M*N
  *           elements), one float dtype
- *   scalars M, N (TILE_N and ONE_TILE_PER_CTA only shape the reference's tiles)
+ *   scalars M, N; or M, N, ONE_TILE_PER_CTA, TILE_N (the constexprs): with
+ *           ONE_TILE_PER_CTA != 0 and TILE_N < N only the first TILE_N
+ *           elements of each row are normalised and written (:13-24); any
+ *           other pair covers the whole row
  * G950_OP_LAYERNORM_ROW  _layer_norm_forward_row (ops/suite/dev/layer_norm_forward_row.py:11-36):
  *                      mean = sum(x)/n, rstd = 1/sqrt(sum(x^2)/n - mean^2 + eps),
  *                      x_hat = (x - mean)*rstd rounded to X's dtype, Y = x_hat*W + B
@@ -215,13 +219,27 @@ int g950_launch(g950_module *module, uint32_t op, const g950_view *views, uint32
  * and results as g950_launch; workspace comes from the library's static
  * scratch array instead of hipMalloc, and no hipMalloc, hipFree or memset is
  * issued (no route needs memory cleared before it runs).  A call whose
- * workspace exceeds the scratch is refused with G950_USAGE; the W8A16 route
- * that copies B first takes the fused kernel instead when the copy does not
- * fit.  All calls on one GPU share its array and it keeps the last call's
- * contents: calls that overlap on one GPU (different streams or threads)
- * race and must be ordered by the caller. */
+ * workspace exceeds the scratch is refused with G950_USAGE, except the routes
+ * that copy B first, which have a workspace-free alternative taken when the
+ * copy does not fit: the widened W8A16 route (G950_OP_DEQUANT_MATMUL with
+ * K-contiguous int8 b) takes the fused W8A16 kernel, and the row-major-B
+ * routes that need a copy (G950_OP_MATMUL with row-major b the _rb kernels
+ * do not take: fp32, M or N under 256, K not a multiple of 64;
+ * G950_OP_DEQUANT_MATMUL with row-major int8 b) run g950_gemm_general, the
+ * scalar-FMA kernel: same results within the GEMM tolerance, much slower;
+ * g950_last_kernel names it.  All calls on one GPU share its array and it
+ * keeps the last call's contents: calls that overlap on one GPU (different
+ * streams or threads) race and must be ordered by the caller. */
 int g950_launch_noalloc(g950_module *module, uint32_t op, const g950_view *views, uint32_t nviews,
                         const g950_scalar *scalars, uint32_t nscalars, void *stream);
+
+/* Bytes of device workspace the module holds for launches on `stream` (0 if
+ * it holds none): what g950_launch allocated there for split rows, copies of
+ * B and int8 sums, grown on demand and freed by g950_close.  The runtime-side
+ * counterpart of the reference's workspace queries
+ * (operator_workspace_private/_shared, a100c/runtime/a100rt.h:180-181); it
+ * lets a caller see that g950_launch_noalloc left it untouched. */
+size_t g950_workspace_bytes(g950_module *module, void *stream);
 
 /* Run every contract check and the kernel choice of g950_launch without
  * touching a device (no module, no HIP call).  On success

@@ -183,12 +183,20 @@ def layernorm_row(x, w, b, eps):
     return y, mean, rstd
 
 
-def softmax_inner(flat, m, n) -> np.ndarray:
+def softmax_inner(flat, m, n, tile_n=None, one_tile=False, out=None) -> np.ndarray:
     """``softmax_kernel_inner`` (ops/suite/dev/softmax_kernel_inner.py, ref):
     the flat buffer's first m*n elements as m rows of n, row softmax in
-    float64, returned flat."""
+    float64, returned flat.  The one-tile form with ``tile_n < n`` loads
+    ``tl.arange(0, TILE_N)`` of each row (masked by ``< N``, so all of them)
+    and stores the same positions (:13-24): the first ``tile_n`` elements
+    of a row are normalised among themselves and the rest of the output row
+    keeps what ``out`` (the output buffer before the call, flat) held."""
     x = np.asarray(flat).reshape(-1)[: m * n].reshape(m, n)
-    return softmax(x).reshape(-1)
+    if not (one_tile and tile_n is not None and tile_n < n):
+        return softmax(x).reshape(-1)
+    res = np.array(np.asarray(out).reshape(-1)[: m * n], dtype=np.float64).reshape(m, n)
+    res[:, :tile_n] = softmax(x[:, :tile_n])
+    return res.reshape(-1)
 
 
 # -------------------------------------------------------------------- GEMM

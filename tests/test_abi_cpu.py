@@ -28,19 +28,6 @@ def test_library_exports_every_declared_function():
         assert hasattr(lib, name), name
 
 
-def test_probe_code_object_holds_every_probe_kernel():
-    # bench.py --hw-probe launches these by name from the probe code object
-    from compiler_amd import probes
-    data = Path(probes.PROBES).read_bytes()
-    names = [n for n, *_ in probes.RATE.values()] + [n for n, _ in probes.ISSUE.values()] + \
-        ["g950p_clock", "g950p_mfma_rate32", "g950p_mfma_rate16"]
-    for name in names:
-        assert (name + ".kd").encode() in data, name
-    # the phase-stamp probe swaps in the stamped attention kernels by name
-    stamped = Path(probes.STAMPS).read_bytes()
-    assert b"g950_attn_fwd_bf16_d128.kd" in stamped
-
-
 def test_record_layouts_match_reference_abi():
     # a100c/runtime/a100rt.h:186-199 pins these sizes and offsets
     assert ctypes.sizeof(rt.View) == 56
@@ -56,6 +43,8 @@ def test_strerror_codes():
     assert lib.g950_strerror(0) == b"ok"
     assert b"refused" in lib.g950_strerror(2)
     assert b"rejected" in lib.g950_strerror(3)
+    # a100c/runtime/a100rt.h:54: exit 5 = repeats produced different outputs
+    assert rt.REPEAT_MISMATCH == 5 and b"repeats" in lib.g950_strerror(5)
 
 
 class Args:
@@ -310,8 +299,22 @@ def test_dequant_matmul_contract():
     assert rc == 0 and name == "g950_gemm_bf16_256x256", err   # 160 tiles
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(4096, 4096, 208), [208, 4096, 4096])
     assert rc == 0 and name == "g950_gemm_w8a16_bf16_128x128", err   # K not a multiple of 64
+    # the reference's own weight layout, row-major int8 b [K, N]
+    # (dequantize_matmul.py:62-65): widened as it lies + the row-major-B MFMA
+    # kernel from one 256 tile each way (whole 64-k slabs), else transposed
+    # once to K-contiguous and the fused / decode kernels
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 64, col_b=False), [64, 64, 64])
-    assert rc == 0 and name == "g950_gemm_general", err
+    assert rc == 0 and name == "g950_gemm_w8a16_skinny64_bf16", err
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(2048, 4096, 4096, col_b=False), [4096, 2048, 4096])
+    assert rc == 0 and name == "g950_gemm_bf16_256x256_rb", err
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(300, 512, 256, rt.DT_F16, col_b=False), [256, 300, 512])
+    assert rc == 0 and name == "g950_gemm_f16_256x256_rb", err
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(100, 272, 96, col_b=False), [96, 100, 272])
+    assert rc == 0 and name == "g950_gemm_w8a16_bf16_128x128", err   # M < 256: transposed, fused kernel
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(1, 8192, 8192, col_b=False), [8192, 1, 8192])
+    assert rc == 0 and name == "g950_gemm_w8a16_skinny_c16_bf16", err
+    rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 72, 64, col_b=False), [64, 64, 72])
+    assert rc == 0 and name == "g950_gemm_general", err   # N not whole 16-byte int8 rows
     rc, name, err = validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 40), [40, 64, 64])
     assert rc == 0 and name == "g950_gemm_general", err
     assert validate(rt.OP_DEQUANT_MATMUL, args(64, 64, 64, sdt=rt.DT_F32), [64, 64, 64])[0] == rt.USAGE
@@ -389,7 +392,11 @@ def gemm_args(m, n, k, dtype, col_major_b=True, out=rt.DT_BF16):
 @pytest.mark.parametrize("m,n,k,colb,kernel", [
     (8192, 8192, 8192, True, "g950_gemm_bf16_256x256"),
     (4097, 11008, 4096, True, "g950_gemm_bf16_256x256"),
-    (8192, 8192, 8192, False, "g950_gemm_bf16_256x256"),  # row-major B (matmul.py:33): copied K-contiguous
+    (8192, 8192, 8192, False, "g950_gemm_bf16_256x256_rb"),  # row-major B (matmul.py:33), read as it lies
+    (4097, 11008, 4096, False, "g950_gemm_bf16_256x256_rb"),
+    (300, 264, 256, False, "g950_gemm_bf16_256x256_rb"),
+    (256, 256, 96, False, "g950_gemm_bf16_256x256_kt"),  # row-major B, K tail: copied K-contiguous
+    (255, 4096, 4096, False, "g950_gemm_bf16_256x256"),  # row-major B under one tile of rows: copied
     (128, 128, 128, False, "g950_gemm_bf16_256x256"),   # the corpus fixtures' layout
     (8, 24, 32, False, "g950_gemm_bf16_256x256_kt"),     # matmul-tail fixture shape [8,32,24]: K tail
     (64, 64, 96, True, "g950_gemm_bf16_256x256_kt"),    # K not a whole 64-element (128-byte) slab
@@ -552,6 +559,27 @@ def test_softmax_inner_contract():
     assert validate(rt.OP_SOFTMAX_INNER, a, [3])[0] == rt.USAGE
     # nothing to do
     assert validate(rt.OP_SOFTMAX_INNER, a, [0, 32])[0] == 0
+
+
+def test_softmax_inner_one_tile_contract():
+    # the constexprs as scalars (M, N, ONE_TILE_PER_CTA, TILE_N): one tile
+    # narrower than the row normalises the first TILE_N elements, read and
+    # written at row stride N -- 16 fp32 = whole 16-byte vectors of 32-element rows
+    a = Args().view([96], rt.DT_F32).view([96], rt.DT_F32, output=True)
+    rc, name, err = validate(rt.OP_SOFTMAX_INNER, a, [3, 32, True, 16])
+    assert rc == 0 and name.startswith("g950_rr_softmax_f32_v4"), err
+    # a tile as wide as the row, or the looped form, covers the row
+    for sc in ([3, 32, True, 32], [3, 32, True, 64], [3, 32, False, 16]):
+        rc, name, err = validate(rt.OP_SOFTMAX_INNER, a, sc)
+        assert rc == 0 and name == "g950_rr_softmax_f32_v4_i1_b64", (sc, err)
+    # bf16 rows of 3000 with a 2048-wide tile: 4096-byte tile rows at a 6000-byte stride
+    a = Args().view([8191 * 3000], rt.DT_BF16).view([8191 * 3000], rt.DT_BF16, output=True)
+    rc, name, err = validate(rt.OP_SOFTMAX_INNER, a, [8191, 3000, True, 2048])
+    assert rc == 0 and name.startswith("g950_r") and "softmax_bf16" in name, err
+    a = Args().view([96], rt.DT_F32).view([96], rt.DT_F32, output=True)
+    rc, _, err = validate(rt.OP_SOFTMAX_INNER, a, [3, 32, True, 0])
+    assert rc == rt.USAGE and "TILE_N" in err
+    assert validate(rt.OP_SOFTMAX_INNER, a, [3, 32, True])[0] == rt.USAGE
 
 
 def lnrow_args(rows, cols, dt, sdt=None, x2d=True):

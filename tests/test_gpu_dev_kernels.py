@@ -92,10 +92,24 @@ def test_softmax_kernel_inner_c2_scale_and_guard():
     assert np.allclose(got[: m * n].reshape(m, n).sum(axis=1), 1.0, atol=2e-2)
 
 
-def test_softmax_kernel_inner_refuses_narrow_one_tile():
-    x = torch.zeros(96, device=DEV)
-    with pytest.raises(rt.G950Error):
-        ops.softmax_kernel_inner(torch.empty_like(x), x, 3, 32, 16, True)
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("m,n,tile", [(3, 32, 16), (3, 32, 8), (5, 3000, 2048), (4, 100, 64)])
+def test_softmax_kernel_inner_one_narrow_tile(m, n, tile, dt):
+    """ONE_TILE_PER_CTA with TILE_N < N (softmax_kernel_inner.py:13-24): the
+    first TILE_N elements of each row are normalised among themselves and
+    the rest of the output (pre-filled with -7) stays as it was."""
+    x = rounded(np.random.default_rng(7).normal(0, 2.0, m * n), dt)
+    before = np.full(m * n + 16, -7.0)
+    out = torch.full((m * n + 16,), -7.0, dtype=TD[dt], device=DEV)
+    ops.softmax_kernel_inner(out, dev(x, dt), m, n, tile, True, sync=True)
+    got = host(out)
+    expect = ref.softmax_inner(x, m, n, tile, True, out=before)
+    rtol, atol = RED_BAR[dt]
+    if dt == "float32":
+        rel_close(got[: m * n], expect, rtol, 1e-30)
+    else:
+        close(got[: m * n], expect, rtol, atol)
+    assert np.all(got.reshape(-1)[m * n:] == -7.0)
 
 
 # ------------------------------------------------- _layer_norm_forward_row

@@ -492,9 +492,40 @@ def test_dequant_matmul_fused(m, n, k, dt):
     assert torch.equal(y, y2)
 
 
+@pytest.mark.parametrize("dt", ["bfloat16", "float16"])
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 4096), (300, 512, 256), (100, 272, 96), (16, 4096, 4096),
+                                   (1, 8192, 8192), (64, 1024, 2048)])
+def test_dequant_matmul_reference_weight_layout(m, n, k, dt):
+    """dequantize_matmul with the reference's own weight layout, int8 b
+    row-major [K, N] (stride_bk = N, ops/suite/perf/dequantize_matmul.py:62-65):
+    from one 256 tile each way the weights are widened as they lie and the
+    row-major-B MFMA kernel runs with the scale in its epilogue; smaller M
+    transposes the int8 weights once and takes the fused / decode kernels.
+    Bar 2e-2 against float64 a . (b * scale) on the rounded inputs."""
+    rng = np.random.default_rng(m + 3 * n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32) * 0.5
+    b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = (rng.random(n) / 64).astype(np.float32)
+    ad, sd = dev(a, dt), dev(s, dt)
+    y = ops.dequant_matmul(ad, torch.from_numpy(b).to(DEV), sd, sync=True)
+    short = "bf16" if dt == "bfloat16" else "f16"
+    kern = rt.module().last_kernel
+    if m >= 256 and n >= 256 and k % 64 == 0:
+        assert kern == f"g950_gemm_{short}_256x256_rb"
+    else:
+        assert kern.startswith("g950_gemm_w8a16_"), kern
+    rows = np.arange(m) if m <= 512 else np.unique(np.r_[0, 255, 256, m - 1,
+                                                        np.random.default_rng(5).integers(0, m, 24)])
+    expect = ref.matmul(host(ad)[rows], ref.dequantize(b, host(sd)))
+    close(host(y)[rows], expect, 2e-2, 2e-2)
+    # the K-contiguous layout of the same weights gives the same values (GEMM bar)
+    y2 = ops.dequant_matmul(ad, torch.from_numpy(np.ascontiguousarray(b.T)).to(DEV).t(), sd, sync=True)
+    close(host(y), host(y2), 2e-2, 2e-2)
+
+
 def test_dequant_matmul_general_layouts():
-    """Row-major int8 b, fp32 a and a ragged K take the general kernel, same bar
-    (fp32: 1e-4)."""
+    """Row-major int8 b with rows that are not whole 16-byte vectors, fp32 a
+    and a ragged K take the general kernel, same bar (fp32: 1e-4)."""
     rng = np.random.default_rng(12)
     a = rng.standard_normal((70, 40)).astype(np.float32)
     b = rng.integers(-128, 128, (40, 90)).astype(np.int8)
@@ -524,21 +555,51 @@ def test_gemm_f16_and_general_paths():
 
 @pytest.mark.parametrize("dt", ["bfloat16", "float16"])
 @pytest.mark.parametrize("m,n,k", [(256, 256, 64), (300, 264, 256), (513, 1000, 1024), (1, 8, 64), (8, 24, 32),
-                                   (257, 136, 200), (130, 72, 8), (4096, 4096, 4096)])
+                                   (257, 136, 200), (130, 72, 8), (4096, 4096, 4096), (4097, 11008, 4096),
+                                   (256, 520, 192), (777, 264, 128)])
 def test_gemm_row_major_b_on_mfma(m, n, k, dt):
     """The reference matmul's own layout (row-major B, ops/suite/perf/matmul.py:33):
-    B copied once K-contiguous, then the MFMA kernel (the _kt form when K is not
-    a whole 64-element slab: the last slab's tail multiplies zeros).  Bar 2e-2
-    (bf16) / 1e-2 (fp16) against float64; rows sampled at 4096^3."""
+    from one 256 tile each way with whole 64-k slabs the MFMA kernel reads B as
+    it lies (transposing LDS reads, _rb); smaller shapes and K tails copy B
+    once K-contiguous, then the MFMA kernel (the _kt form when K is not a
+    whole 64-element slab: the last slab's tail multiplies zeros).  Bar 2e-2
+    (bf16) / 1e-2 (fp16) against float64, every column of the rows checked
+    (one per 256-row tile at the large shapes, edges included); rows and
+    columns outside the output are guarded."""
     c = inputs.config3(m, n, k)
     a, b = dev(c["a"], dt), dev(np.ascontiguousarray(c["bt"].T), dt)   # b: [K, N] row-major
-    y = torch.zeros((m, n), dtype=TD[dt], device=DEV)
+    full = torch.full((m + 2, n + 8), 7.0, dtype=TD[dt], device=DEV)
+    y = full[1:m + 1, :n]
     ops.matmul_kernel(a, b, y, m, n, k, sync=True)
     short = "bf16" if dt == "bfloat16" else "f16"
-    assert rt.module().last_kernel == f"g950_gemm_{short}_256x256" + ("_kt" if k % 64 else "")
+    rb = m >= 256 and n >= 256 and k % 64 == 0
+    assert rt.module().last_kernel == f"g950_gemm_{short}_256x256" + ("_rb" if rb else "_kt" if k % 64 else "")
     rows = np.arange(m) if m <= 1024 else tile_rows(m, 3)
     bar = 2e-2 if dt == "bfloat16" else 1e-2
     close(host(y)[rows], ref.matmul(host(a)[rows], host(b)), bar, bar)
+    fh = host(full)
+    assert (fh[0] == 7).all() and (fh[-1] == 7).all() and (fh[:, n:] == 7).all()
+
+
+def test_gemm_row_major_b_config3_full_size():
+    """C3a in the reference matmul's layout (row-major B [8192, 8192]) through
+    the _rb kernel: one row of every 256-row tile plus the edges, all 8192
+    columns, against float64; and bit-identical to the column-major kernel
+    on the same values (same MFMA sequence per output: both sum the 64-k
+    slabs in order with the same fragment k layout)."""
+    c = inputs.config3(8192, 8192, 8192)
+    a = dev(c["a"], "bfloat16")
+    bt = dev(c["bt"], "bfloat16")
+    b = bt.t().contiguous()                                          # [K, N] row-major
+    y = torch.empty((8192, 8192), dtype=torch.bfloat16, device=DEV)
+    ops.matmul_kernel(a, b, y, 8192, 8192, 8192, sync=True)
+    assert rt.module().last_kernel == "g950_gemm_bf16_256x256_rb"
+    rows = tile_rows(8192, 4)
+    close(host(y)[rows], ref.matmul(host(a)[rows], host(b)), 2e-2, 2e-2)
+    y2 = torch.empty_like(y)
+    ops.matmul_kernel(a, bt.t(), y2, 8192, 8192, 8192, sync=True)
+    assert rt.module().last_kernel == "g950_gemm_bf16_256x256"
+    assert torch.equal(y, y2)
 
 
 @pytest.mark.parametrize("colb", [True, False])
@@ -760,6 +821,31 @@ def test_attention_fp32(z, h, hkv, s, d, causal):
     o, lse = ops.attention(q, k, v, causal=causal, sync=True)
     assert rt.module().last_kernel == f"g950_attn_fwd_f32mfma_d{d}"
     eo, el = ref.attention(c["q"], c["k"], c["v"], c["scale"], causal=causal)
+    close(o.cpu().numpy(), eo, 1e-4, 1e-5)
+    close(lse.cpu().numpy(), el, 1e-5, 1e-5)
+
+
+@pytest.mark.parametrize("shift,d", [(1, 64), (2, 128), (1, 32)])
+def test_attention_fp32_unaligned_kv(shift, d):
+    """fp32 K and V views that start one (two) elements into their buffers
+    and have row strides that are not whole 16-byte vectors: the fp32 MFMA
+    kernel stages them element by element (no 16-byte vector loads at
+    unaligned addresses) and still matches the oracle."""
+    c = inputs.config4(1, 4, 2, 150, d)
+    q = torch.from_numpy(c["q"]).to(DEV)
+
+    def shifted(a):
+        z, h, s_, dd = a.shape
+        row = dd + shift                     # padded rows: stride dd + shift elements
+        buf = torch.zeros(shift + z * h * s_ * row, device=DEV)
+        view = buf[shift:].view(z, h, s_, row)[..., :dd]
+        view.copy_(torch.from_numpy(a).to(DEV))
+        return view
+    k, v = shifted(c["k"]), shifted(c["v"])
+    assert k.data_ptr() % 16 != 0 and k.stride(2) % 4 != 0
+    o, lse = ops.attention(q, k, v, causal=True, sync=True)
+    assert rt.module().last_kernel == f"g950_attn_fwd_f32mfma_d{d}"
+    eo, el = ref.attention(c["q"], c["k"], c["v"], c["scale"], causal=True)
     close(o.cpu().numpy(), eo, 1e-4, 1e-5)
     close(lse.cpu().numpy(), el, 1e-5, 1e-5)
 

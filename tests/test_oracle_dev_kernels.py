@@ -71,6 +71,27 @@ def test_softmax_inner_rows_of_flat_buffer():
     assert not np.allclose(planted, got, atol=1e-3)
 
 
+def test_softmax_inner_one_narrow_tile():
+    # ONE_TILE_PER_CTA with TILE_N < N (softmax_kernel_inner.py:13-24): the
+    # first TILE_N elements of each row normalised among themselves, the
+    # rest of the output row as it was
+    rng = np.random.default_rng(14)
+    m, n, tile = 3, 32, 8
+    flat = rng.normal(0, 0.8, m * n)
+    before = rng.normal(0, 1.0, m * n)
+    got = ref.softmax_inner(flat, m, n, tile, True, out=before)
+    for r in range(m):
+        row = flat[r * n:r * n + tile]
+        bf = [math.exp(v) / sum(math.exp(u) for u in row) for v in row]
+        assert np.allclose(got[r * n:r * n + tile], bf, atol=1e-15)
+        assert np.array_equal(got[r * n + tile:(r + 1) * n], before[r * n + tile:(r + 1) * n])
+    # a whole-row normalisation (the looped form) gives other values on the tile
+    assert not np.allclose(got.reshape(m, n)[:, :tile], ref.softmax_inner(flat, m, n).reshape(m, n)[:, :tile])
+    # a tile as wide as the row, or the looped form, is the plain row softmax
+    for t, one in ((32, True), (64, True), (8, False)):
+        assert np.array_equal(ref.softmax_inner(flat, m, n, t, one, out=before), ref.softmax_inner(flat, m, n))
+
+
 # -------------------------------------------------------------- gqa_kernel
 def _gqa_brute(q, k, v, scale, group):
     z, hq, n, d = q.shape

@@ -16,15 +16,24 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def both(call):
-    """(regular result, no-alloc result, kernel the no-alloc call ran)."""
-    ref_out = call()
-    torch.cuda.synchronize()
-    with rt.no_alloc():
-        out = call()
-        kernel = rt.module().last_kernel
-    torch.cuda.synchronize()
-    return ref_out, out, kernel
+def both(call, kernels=False):
+    """(regular result, no-alloc result, kernel the no-alloc call ran[, kernel
+    the regular call ran]).  Both calls run on a fresh stream, the no-alloc
+    one first, so no workspace of the regular entry exists yet for it to
+    reuse, and the library must hold no workspace for that stream after it."""
+    mod = rt.module()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        assert mod.workspace_bytes(s) == 0
+        with rt.no_alloc():
+            out = call()
+            kernel = mod.last_kernel
+        s.synchronize()
+        assert mod.workspace_bytes(s) == 0, "g950_launch_noalloc allocated workspace"
+        ref_out = call()
+        ref_kernel = mod.last_kernel
+        s.synchronize()
+    return (ref_out, out, kernel, ref_kernel) if kernels else (ref_out, out, kernel)
 
 
 def split_rows_softmax(rows, cols, seed):
@@ -57,18 +66,58 @@ def test_w8a16_few_rows_two_calls():
 
 
 def test_w8a16_widened_copy_in_scratch_two_calls():
-    # many output tiles, B small enough for its bf16 copy to fit the scratch
+    # many output tiles (2 x 5 x 32 = 320 > 256 CUs), B small enough for its
+    # bf16 copy to fit the scratch
     for m, n, k, seed in ((1100, 8192, 128, 5), (1025, 8192, 64, 6)):
-        a, b, kernel = both(w8a16(m, n, k, seed))
-        assert kernel == "g950_gemm_bf16_256x256"
+        a, b, kernel, ref_kernel = both(w8a16(m, n, k, seed), kernels=True)
+        assert kernel == ref_kernel == "g950_gemm_bf16_256x256"
         assert torch.equal(a, b)
 
 
 def test_w8a16_widened_copy_too_large_takes_fused_kernel():
-    # the bf16 copy of B (32 MiB) does not fit: the fused kernel (no workspace)
-    # serves the no-alloc call; different kernels, so the GEMM bar (2e-2)
-    a, b, kernel = both(w8a16(1100, 4096, 4096, 7))
+    # 2048 x 8192 x 4096: 2 x 8 x 32 = 512 tiles > 256 CUs take the widened
+    # route, and its 64 MiB bf16 copy of B exceeds the 32 MiB scratch: the
+    # regular call widens into its workspace, the no-alloc call runs the fused
+    # kernel (no workspace); different kernels, so the GEMM bar (2e-2)
+    a, b, kernel, ref_kernel = both(w8a16(2048, 8192, 4096, 7), kernels=True)
+    assert ref_kernel == "g950_gemm_bf16_256x256"
     assert kernel == "g950_gemm_w8a16_bf16_128x128"
+    ok = torch.isclose(b.float(), a.float(), rtol=2e-2, atol=2e-2).all()
+    assert bool(ok)
+
+
+def rowmajor_gemm(m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    a = torch.from_numpy(rng.standard_normal((m, k), dtype=np.float32)).to(DEV).to(torch.bfloat16)
+    b = torch.from_numpy(rng.standard_normal((k, n), dtype=np.float32)).to(DEV).to(torch.bfloat16)
+    return lambda: ops.matmul(a, b, sync=True)   # b: the reference's row-major [K, N]
+
+
+def test_row_major_b_read_directly_two_calls():
+    # from one 256 tile each way the MFMA kernel reads row-major B as it lies:
+    # no workspace on either entry, the same kernel, the same bits
+    for m, n, k, seed in ((2048, 4096, 4096, 11), (300, 264, 256, 12)):
+        a, b, kernel, ref_kernel = both(rowmajor_gemm(m, n, k, seed), kernels=True)
+        assert kernel == ref_kernel == "g950_gemm_bf16_256x256_rb"
+        assert torch.equal(a, b)
+
+
+def test_row_major_b_copy_in_scratch_two_calls():
+    # fewer than 256 rows: B is copied K-contiguous first; a 2 MiB (then
+    # 0.5 MiB) copy fits the scratch, so both entries run the same kernels
+    for m, n, k, seed in ((128, 1024, 1024, 13), (100, 512, 512, 14)):
+        a, b, kernel, ref_kernel = both(rowmajor_gemm(m, n, k, seed), kernels=True)
+        assert kernel == ref_kernel == "g950_gemm_bf16_256x256"
+        assert torch.equal(a, b)
+
+
+def test_row_major_b_copy_too_large_takes_general_kernel():
+    # 128 x 8192 x 4096: the K-contiguous copy of B (64 MiB) exceeds the
+    # 32 MiB scratch, so the no-alloc call runs the general kernel (the
+    # documented fallback); the regular call copies into its workspace
+    a, b, kernel, ref_kernel = both(rowmajor_gemm(128, 8192, 4096, 15), kernels=True)
+    assert ref_kernel == "g950_gemm_bf16_256x256"
+    assert kernel == "g950_gemm_general"
     ok = torch.isclose(b.float(), a.float(), rtol=2e-2, atol=2e-2).all()
     assert bool(ok)
 
