@@ -309,7 +309,7 @@ def make_row(name, kernel, work, unit, scale, peak, bound, t):
 # suite sections (bench.py --only KEY[,KEY...] runs just these, without the
 # headline or the CPU legs: one rocprofv3 trace per config)
 SECTIONS = ("c1", "lse", "dequantize", "c3a", "c3b", "c3a_rowb", "gemm_f32", "c4", "attn_f32", "odd", "split",
-            "w8a16", "w8a16_16", "w8a16_1", "w8a16_rowb", "varlen", "c5")
+            "w8a16", "w8a16_16", "w8a16_1", "w8a16_rowb", "varlen", "varlen_paged", "c5")
 
 
 def suite(torch, ops, cpu=True, only=None):
@@ -546,8 +546,8 @@ def suite(torch, ops, cpu=True, only=None):
     # varlen attention (flash_varlen_fwd_kernel): 8 sequences of 4096 - 256 i
     # tokens (q = k lengths, causal), 32 query / 8 KV heads, d 128, bf16;
     # contiguous and paged (64-token pages, shuffled) K/V
-    if want("varlen"):
-        out.extend(varlen_rows(torch, ops))
+    if want("varlen") or want("varlen_paged"):
+        out.extend(varlen_rows(torch, ops, contiguous=want("varlen"), paged=want("varlen_paged")))
         torch.cuda.empty_cache()
 
     # C5: int8 GEMM 4096x8192x8192 + dequant
@@ -578,7 +578,7 @@ def suite(torch, ops, cpu=True, only=None):
     return out
 
 
-def varlen_rows(torch, ops):
+def varlen_rows(torch, ops, contiguous=True, paged=True):
     """flash_varlen_fwd_kernel at the C4 scale: 8 causal sequences of
     4096 - 256 i tokens, 32 query / 8 KV heads, d 128, bf16; contiguous and
     paged (64-token pages, shuffled) K/V."""
@@ -625,10 +625,12 @@ def varlen_rows(torch, ops):
                 page_table_ptr=table)
     flops = sum(4.0 * 32 * 128 * n * (n + 1) / 2 for n in lens)
     rows = []
-    for name, extra in (("F varlen causal GQA bf16 (8 seqs 4096..2304, 32/8, d128)", {}),
-                        ("F varlen paged(64) causal GQA bf16 (same)",
-                         dict(k_ptr=kp, v_ptr=vp, is_paged=True, is_cu_seqlens_k=False, is_seqused_k=True,
-                              page_table_batch_stride=max(pages), block_size=64, k_page_stride=64 * 8 * 128))):
+    for on, name, extra in ((contiguous, "F varlen causal GQA bf16 (8 seqs 4096..2304, 32/8, d128)", {}),
+                            (paged, "F varlen paged(64) causal GQA bf16 (same)",
+                             dict(k_ptr=kp, v_ptr=vp, is_paged=True, is_cu_seqlens_k=False, is_seqused_k=True,
+                                  page_table_batch_stride=max(pages), block_size=64, k_page_stride=64 * 8 * 128))):
+        if not on:
+            continue
         call = ops.flash_varlen_fwd_kernel(**{**ptrs, **scal, **extra}, prepare=True)
         t = timed(torch, lambda i: call(), 10, 2, warm_s=0.5)
         rows.append(make_row(name, call.kernel, flops, "TFLOP/s", 1e12, BF16_PEAK_TFS, "mfma", t))
@@ -639,7 +641,8 @@ def pmc_probe(torch, ops):
     """Counter-collection workload (run under rocprofv3 --pmc): the streaming
     copy kernel on exactly the bytes of one x (the calibration kernel: same
     nontemporal 16-byte loads/stores as the row kernels), then 8 launches of
-    each headline kernel on 6 rotating buffer sets, as in the timed region."""
+    each HBM-bound kernel on 6 rotating buffer sets, as in the timed region:
+    C2, C1, int8 dequantisation and the next-row kernels."""
     from oracle import inputs
     rows, cols = 8191, 3000
     dev = "cuda:0"
@@ -687,8 +690,46 @@ def pmc_probe(torch, ops):
     for i in range(8):
         dqc[i % ROTATE]()
     torch.cuda.synchronize()
+    del dq, dqc
+    # next-row kernels: row logsumexp bf16 [8191, 3000] -> fp32; odd rows
+    # bf16 [8191, 3001] LayerNorm and softmax; split rows bf16 [4, 2^22]
+    # softmax; W8A16 decode 16 x 8192 x 8192 and 1 x 8192 x 8192
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    lse = [(torch.randn((8191, 3000), device=dev, generator=gen).mul_(3.0).to(torch.bfloat16),
+            torch.empty(8191, device=dev)) for _ in range(ROTATE)]
+    lsec = [ops.logsumexp_kernel(x, y, 3000, prepare=True) for x, y in lse]
+    odd = [(torch.randn((8191, 3001), device=dev, generator=gen).mul_(3.0).to(torch.bfloat16),
+            torch.rand(3001, device=dev, generator=gen).add_(0.5).to(torch.bfloat16),
+            torch.randn(3001, device=dev, generator=gen).mul_(0.1).to(torch.bfloat16),
+            torch.empty((8191, 3001), dtype=torch.bfloat16, device=dev),
+            torch.empty(8191, device=dev), torch.empty(8191, device=dev)) for _ in range(ROTATE)]
+    lno = [ops.layernorm_kernel(x, y, g_, b_, m_, r_, 3001, 3001, 1e-5, prepare=True) for x, g_, b_, y, m_, r_ in odd]
+    smo = [ops.softmax_kernel(x, y, 3001, prepare=True) for x, g_, b_, y, m_, r_ in odd]
+    for calls in (lsec, lno, smo):
+        for i in range(8):
+            calls[i % ROTATE]()
+        torch.cuda.synchronize()
+    del lse, lsec, odd, lno, smo
+    xs = [torch.randn((4, 1 << 22), device=dev, generator=gen).to(torch.bfloat16) for _ in range(ROTATE)]
+    spc = [ops.softmax_kernel(x, torch.empty_like(x), 1 << 22, prepare=True) for x in xs]
+    for i in range(8):
+        spc[i % ROTATE]()
+    torch.cuda.synchronize()
+    del xs, spc
+    for m_ in (16, 1):
+        dec = [(torch.randn((m_, 8192), device=dev, generator=gen).to(torch.bfloat16),
+                torch.randint(-127, 127, (8192, 8192), device=dev, generator=gen, dtype=torch.int8),
+                torch.rand(8192, device=dev, generator=gen).to(torch.bfloat16),
+                torch.empty((m_, 8192), device=dev, dtype=torch.bfloat16)) for _ in range(ROTATE)]
+        decc = [ops.dequant_matmul_kernel(a_, b_.t(), s_, y_, m_, 8192, 8192, prepare=True) for a_, b_, s_, y_ in dec]
+        for i in range(8):
+            decc[i % ROTATE]()
+        torch.cuda.synchronize()
+        del dec, decc
     log(f"pmc probe: copy {src.numel() * 2} B read + write; C2 layernorm/softmax/layer_norm_forward_row, "
-        "C1 rmsnorm/softmax fp32, dequantize int8->bf16 8192^2: x8 each")
+        "C1 rmsnorm/softmax fp32, dequantize int8->bf16 8192^2, logsumexp bf16 [8191,3000], odd-row "
+        "layernorm/softmax [8191,3001], split-row softmax [4,2^22], W8A16 decode 16/1 x 8192 x 8192: x8 each")
 
 
 def mfma_probe(torch, ops):
@@ -715,6 +756,13 @@ def mfma_probe(torch, ops):
             for _ in range(4):
                 torch.matmul(a, bt.t())
             torch.cuda.synchronize()
+            # the reference layout, row-major B, read as it lies (_rb)
+            b = bt.t().contiguous()
+            rbg = ops.matmul_kernel(a, b, y, m, n, k, prepare=True)
+            for _ in range(4):
+                rbg()
+            torch.cuda.synchronize()
+            del b
         del a, bt, y
     c5 = inputs.config5()
     a8, b8 = torch.from_numpy(c5["a"]).to(dev), torch.from_numpy(c5["bt"]).to(dev)
@@ -735,7 +783,7 @@ def mfma_probe(torch, ops):
     for _ in range(4):
         attn()
     torch.cuda.synchronize()
-    log(f"mfma probe: {gemm.kernel} x4 (two shapes), {i8.kernel} x4, {attn.kernel} x4")
+    log(f"mfma probe: {gemm.kernel} x4 (two shapes), {rbg.kernel} x4, {i8.kernel} x4, {attn.kernel} x4")
 
 
 def traffic_for(kernel):
