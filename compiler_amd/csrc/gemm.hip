@@ -1128,6 +1128,12 @@ __device__ __forceinline__ void gemm_w8a16_skinny_body(const GemmArgs& p) {
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[r][t] = (f32x4){};
+  // Weights use plain (cacheable) loads: an instruction reads 64 bytes of
+  // each of its 16 columns, so every 128-byte line is requested in two halves
+  // by consecutive steps, and with nontemporal loads the line was fetched
+  // again for its second half (rocprofv3 FETCH_SIZE 1.20x the algorithmic
+  // bytes at 16 x 8192 x 8192; 16 x 8192 x 8192 25.4 -> 23.0 us and
+  // 32 x 8192 x 8192 32.8 -> 30.0 us with six rotating input sets).
   // STEPS 64-element K steps in flight per wave.  Over whole batches, step st
   // of the next batch is loaded into step st's registers as soon as their
   // MFMAs have issued, so the loads stream without a gap between batches (no
@@ -1138,7 +1144,7 @@ __device__ __forceinline__ void gemm_w8a16_skinny_body(const GemmArgs& p) {
   auto load = [&](int st, int k0) {
     const int kk = k0 + st * 64 + 16 * g;
 #pragma unroll
-    for (int t = 0; t < T; ++t) bw[st][t] = __builtin_nontemporal_load((const u32x4*)(bcol[t] + kk));
+    for (int t = 0; t < T; ++t) bw[st][t] = *(const u32x4*)(bcol[t] + kk);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       a0[st][r] = *(const u32x4*)(arow[r] + 2 * (long long)kk);

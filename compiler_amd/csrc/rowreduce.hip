@@ -735,9 +735,14 @@ __device__ __forceinline__ void rm_body(const RowArgs& a) {
 constexpr int RS_BLOCK = 256;
 constexpr int RS_ITEMS = 4;
 
+// cached: the partial pass's loads are cacheable, so the final pass's
+// re-read of the same chunk (one launch later) finds it in the MALL; the
+// final pass reads it for the last time, nontemporally.  Measured on MI355X
+// (six rotating input sets): bf16 [4, 2^22] softmax 18.7 -> 15.8 us,
+// [64, 2^20] 66.6 -> 63.5 us against nontemporal loads in both passes.
 template <int OP, typename T, int VEC>
 __device__ __forceinline__ void rs_load(const RowArgs& a, int row, int split, float (&v)[RS_ITEMS][VEC],
-                                        bool (&ok)[RS_ITEMS]) {
+                                        bool (&ok)[RS_ITEMS], bool cached) {
   using IO = RawIO<T, VEC>;
   const char* xrow = (const char*)a.x + (long long)row * a.x_row * (long long)sizeof(T);
   const int nvec = a.cols / VEC;
@@ -747,7 +752,7 @@ __device__ __forceinline__ void rs_load(const RowArgs& a, int row, int split, fl
   for (int i = 0; i < RS_ITEMS; ++i) {
     const int j = base + threadIdx.x + i * RS_BLOCK;
     ok[i] = j < nvec;
-    if (ok[i]) raw[i] = IO::load(xrow, (long long)j * VEC);
+    if (ok[i]) raw[i] = cached ? IO::load_cached(xrow, (long long)j * VEC) : IO::load(xrow, (long long)j * VEC);
   }
 #pragma unroll
   for (int i = 0; i < RS_ITEMS; ++i) {
@@ -767,7 +772,7 @@ __device__ __forceinline__ void rs_part_body(const RowArgs& a) {
   const int row = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
   float v[RS_ITEMS][VEC];
   bool ok[RS_ITEMS];
-  rs_load<OP, T, VEC>(a, row, split, v, ok);
+  rs_load<OP, T, VEC>(a, row, split, v, ok, true);
   f32x4 p = {0.0f, 0.0f, 0.0f, 0.0f};
   if constexpr (OP == ROW_SOFTMAX || OP == ROW_LOGSUMEXP) {
     float m = -__builtin_huge_valf(), nan = 0.0f;
@@ -899,7 +904,7 @@ __device__ __forceinline__ void rs_final_body(const RowArgs& a) {
     const int row = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
     float v[RS_ITEMS][VEC];
     bool ok[RS_ITEMS];
-    rs_load<OP, T, VEC>(a, row, split, v, ok);  // in flight during the merge
+    rs_load<OP, T, VEC>(a, row, split, v, ok, false);  // in flight during the merge
     const f32x4 r = rs_merge<OP>(a, row, scratch);
     void* yrow = (char*)a.y + (long long)row * a.y_row * (long long)sizeof(T);
     const int base = split * (RS_BLOCK * RS_ITEMS);
