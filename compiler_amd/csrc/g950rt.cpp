@@ -633,8 +633,10 @@ bool gemm_off32(const GemmArgs& g, int esz) {
 }
 
 // Row-major B[K,N] (N-contiguous, the reference matmul's layout,
-// ops/suite/perf/matmul.py:33) with A K-contiguous: B is copied once into a
-// K-contiguous Bt in the workspace (g950_transpose_b16) for the MFMA kernels.
+// ops/suite/perf/matmul.py:33) with A K-contiguous, 16-byte aligned rows: the
+// 16-bit shapes the `_rb` MFMA kernels take are read as they lie; the others
+// (fp32, a dimension under one tile, a K tail) copy B once into a
+// K-contiguous Bt in the workspace (g950_transpose_b16/_b32) first.
 bool gemm_rowb_ok(const View& a, const View& b, int K, int N, int esz) {
   const int per16 = 16 / esz;  // elements per 16-byte vector
   return (esz == 2 || esz == 4) && a.stride[1] == 1 && b.stride[1] == 1 && K % per16 == 0 && N % per16 == 0 &&

@@ -9,11 +9,15 @@
 // Y[m,n] = bf16(float(acc[m,n]) * sa[m] * sb[n]).
 //
 // MFMA kernel (g950_gemm_*_256x256): both operands K-contiguous (A row-major
-// [M,K]; B stored as Bt[N,K], i.e. column-major [K,N]).
+// [M,K]; B stored as Bt[N,K], i.e. column-major [K,N]).  The `_rb` variants
+// (16-bit) read the reference's row-major B[K,N] as it lies, with
+// transposing LDS reads (the BROW notes above gemm_mfma16_body).
 //   * workgroup tile 256x256, 8 waves (4 x 2, two per SIMD), wave tile
-//     64 x 128 = 2 x 4 fragments of v_mfma_f32_32x32x16_{bf16,f16} /
-//     v_mfma_i32_32x32x32_i8; the B tile feeds the MFMA A port so each lane
-//     ends with four consecutive output columns of one output row
+//     64 x 128: 4 x 8 fragments of v_mfma_f32_16x16x32_{bf16,f16} /
+//     v_mfma_i32_16x16x64_i8 for whole-slab 16-bit / int8 shapes with
+//     M, N >= 256 (gemm_mfma16_body), else 2 x 4 fragments of the 32x32
+//     forms; the B tile feeds the MFMA A port so each lane ends with four
+//     consecutive output columns of one output row
 //   * K in slabs of 128 bytes per row (64 bf16 / 128 int8); two LDS stages
 //     of 64 KiB (A rows then B rows, 128-byte rows), filled by direct
 //     global->LDS 16-byte DMA (global_load_lds_dwordx4) of whole 128-byte
@@ -39,7 +43,8 @@
 //
 // General kernel (g950_gemm_general): any strides, any K, fp32/fp16/bf16
 // inputs (fp32 FMA) or int8 (int32 exact); 64x64 tiles.  It serves the
-// reference's row-major-B fixtures and shapes the MFMA kernel refuses.
+// layouts no MFMA route takes (unaligned rows, non-unit inner strides) and
+// the no-alloc entry when a copy of B would not fit its scratch array.
 #include "g950_common.h"
 
 #include <utility>
