@@ -5,6 +5,8 @@ Bars (written per test): fp32 reductions <= 1e-5 relative; bf16 reductions
 <= 1e-2; bf16 GEMM / attention <= 2e-2 absolute+relative (np.isclose form of
 ops/harness/opslib/compare.py:107-140); int8 accumulators bit-exact.
 """
+import functools
+
 import numpy as np
 import pytest
 
@@ -753,6 +755,74 @@ def test_gemm_16x16_edge_windows(m, n, k):
         close(host(y), ref.matmul(ad, bd.T), *((2e-2, 2e-2) if dt == "bfloat16" else (1e-2, 1e-2)))
         fh = host(full)
         assert (fh[0] == 7).all() and (fh[-1] == 7).all() and (fh[:, n:] == 7).all()
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 512, 128), (300, 512, 256), (513, 768, 384), (4097, 1024, 128)])
+def test_gemm_staged_epilogue_matches_row_stores(m, n, k):
+    """Tiles of the 16x16 kernel that own all of their window's columns and
+    write a 16-bit output with 16-byte aligned rows stage the output tile
+    through LDS and store whole row pieces (a bottom-edge window stores only
+    its own rows); an output row stride that is not a multiple of 8 elements
+    takes the row-by-row stores.  The two must give the same bits: bf16 and
+    f16 GEMM, the int8 dequant epilogue in all four signedness pairs, and the
+    W8A16 column scale -- with the guard rows and columns around the output
+    untouched."""
+    rng = np.random.default_rng(m + 3 * n + k)
+    both = functools.partial(_staged_vs_row_stores, m, n)
+    c3 = inputs.config3(m, n, k)
+    for dt in ("bfloat16", "float16"):
+        a, bt = dev(c3["a"], dt), dev(c3["bt"], dt)
+        name = "g950_gemm_bf16_256x256" if dt == "bfloat16" else "g950_gemm_f16_256x256"
+        y = both(lambda out: ops.matmul_kernel(a, bt.t(), out, m, n, k), dt, name)
+        close(host(y), ref.matmul(host(a), host(bt).T), *((2e-2, 2e-2) if dt == "bfloat16" else (1e-2, 1e-2)))
+        brow = bt.t().contiguous()
+        both(lambda out: ops.matmul_kernel(a, brow, out, m, n, k), dt, name + "_rb")
+    sa = torch.from_numpy((rng.random(m) * 0.02 + 0.001).astype(np.float32)).to(DEV)
+    sb = torch.from_numpy((rng.random(n) * 0.02 + 0.001).astype(np.float32)).to(DEV)
+    for adt, bdt, name in ((np.int8, np.int8, "g950_gemm_i8_256x256"), (np.uint8, np.int8, "g950_gemm_u8s8_256x256"),
+                           (np.int8, np.uint8, "g950_gemm_s8u8_256x256"), (np.uint8, np.uint8, "g950_gemm_u8u8_256x256")):
+        lo_a, hi_a = (-128, 128) if adt is np.int8 else (0, 256)
+        lo_b, hi_b = (-128, 128) if bdt is np.int8 else (0, 256)
+        a8 = torch.from_numpy(rng.integers(lo_a, hi_a, (m, k)).astype(adt)).to(DEV)
+        b8 = torch.from_numpy(rng.integers(lo_b, hi_b, (n, k)).astype(bdt)).to(DEV)
+        both(lambda out: ops.matmul_i8_dequant_kernel(a8, b8.t(), sa, sb, out, m, n, k), "bfloat16", name)
+
+
+def test_w8a16_staged_epilogue_matches_row_stores():
+    """The widened W8A16 route (more 256x256 tiles than half the CUs: an
+    exact bf16 copy of the int8 weights, then the bf16 GEMM with the column
+    scale in its epilogue) stages its output like the plain GEMM; the same
+    bits as the row-by-row stores, on a shape with a bottom-edge window."""
+    m, n, k = 3000, 3072, 128
+    rng = np.random.default_rng(5)
+    a = dev((rng.standard_normal((m, k)) * 0.1).astype(np.float32), "bfloat16")
+    w8 = torch.from_numpy(rng.integers(-127, 128, (n, k)).astype(np.int8)).to(DEV)
+    scale = dev((rng.random(n) * 0.02 + 0.001).astype(np.float32), "bfloat16")
+    y = _staged_vs_row_stores(m, n, lambda out: ops.dequant_matmul_kernel(a, w8.t(), scale, out, m, n, k),
+                              "bfloat16", "g950_gemm_bf16_256x256")
+    deq = host(w8.t().float() * scale.float()[None, :])
+    close(host(y), ref.matmul(host(a), deq), 2e-2, 2e-2)
+
+
+def _staged_vs_row_stores(m, n, launch, dt, name):
+    """Run ``launch`` into an [m, n] output inside a guarded buffer twice:
+    row stride n + 8 (16-byte aligned rows: the staged epilogue) and n + 1
+    (the row-by-row stores), both starting 16 bytes (8 elements) into the
+    buffer; the same bits, the 8 leading and trailing guard elements and the
+    gap after each row untouched."""
+    outs = []
+    for extra in (8, 1):
+        flat = torch.full((16 + m * (n + extra),), 3.0, dtype=TD[dt], device=DEV)
+        y = torch.as_strided(flat, (m, n), (n + extra, 1), 8)
+        launch(y)
+        torch.cuda.synchronize()
+        assert rt.module().last_kernel == name
+        fh = host(flat)
+        rows = fh[8:8 + m * (n + extra)].reshape(m, n + extra)
+        assert (fh[:8] == 3).all() and (fh[-8:] == 3).all() and (rows[:, n:] == 3).all()
+        outs.append(y.clone())
+    assert torch.equal(outs[0], outs[1]), name
+    return outs[0]
 
 
 def test_int8_general_path_exact():
