@@ -865,6 +865,33 @@ def test_attention_every_mfma_instantiation(dt, d, causal):
     close(lse.cpu().numpy(), el, 1e-4, 1e-4)
 
 
+@pytest.mark.parametrize("dt", ["bfloat16", "float16"])
+@pytest.mark.parametrize("d,s,causal", [(128, 520, True), (64, 333, True), (128, 100, False), (64, 1, True)])
+def test_attention_staged_epilogue_matches_row_stores(dt, d, s, causal):
+    """With 16-byte aligned output rows the 16-bit kernels stage each wave's
+    output tile through LDS and store whole rows (queries past the sequence
+    end masked); an output row stride of d + 4 elements takes the per-lane
+    8-byte stores.  The two must give the same bits, with the padding after
+    each output row untouched, and match the oracle."""
+    c = inputs.config4(1, 4, 2, s, d)
+    q, k, v = (dev(c[n], dt) for n in ("q", "k", "v"))
+    outs = []
+    for pad in (8, 4):
+        full = torch.full((1, 4, s, d + pad), 5.0, dtype=TD[dt], device=DEV)
+        o = full[..., :d]
+        lse = torch.empty((1, 4, s), device=DEV)
+        ops.attn_fwd_causal_kernel(q, k, v, o, 1, 4, s, c["scale"], *q.stride(), *k.stride(), *v.stride(),
+                                   *o.stride(), CAUSAL=causal, lse_ptr=lse, sync=True)
+        assert rt.module().last_kernel == f"g950_attn_fwd_{'bf16' if dt == 'bfloat16' else 'f16'}_d{d}"
+        assert bool((full[..., d:] == 5.0).all())
+        outs.append((o.clone(), lse.clone()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    qh, kh, vh = (host(t) for t in (q, k, v))
+    eo, el = ref.attention(qh, kh, vh, c["scale"], causal=causal)
+    close(host(outs[0][0]), eo, 2e-2, 2e-2)
+    close(outs[0][1].cpu().numpy(), el, 1e-4, 1e-4)
+
+
 @pytest.mark.parametrize("scale", [-0.125, 0.0])
 def test_attention_non_positive_scale_takes_fp32_kernel(scale):
     """The 16-bit kernel's running maximum needs scale > 0; other scales run
