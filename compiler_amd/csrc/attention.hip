@@ -250,7 +250,13 @@ __device__ __forceinline__ long long paged_row(const VarlenArgs& vl, int z, int 
 // barrier; DMA of K(t+2) and V(t+1); then, in the order of the wave's half
 // of the ping-pong, the softmax of tile t and the MFMA phase (O^T += V^T.P^T
 // of tile t, S^T of tile t+1), or the MFMA phase and the softmax of tile t+1.
-template <int D, bool F16, int NW, bool VL>
+// PG (varlen only): how K/V rows are found -- 0 contiguous rows (no page
+// table), 1 pages holding whole 64-key tiles (one page-table read per tile),
+// 2 any page size (a page-table read per DMA lane).  A compile-time choice:
+// the unused paths cost the contiguous kernel 10% when they were run-time
+// branches inside the DMA loop (4 x 4096 tokens, 32/8 heads, d 128: 595 ->
+// 538 us; the fixed-shape kernel takes 516 us on the same tensors).
+template <int D, bool F16, int NW, bool VL, int PG = 0>
 __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* vl) {
   using C = AttnCfg<D, NW>;
   __shared__ __attribute__((aligned(1024))) char lds[C::LDS];
@@ -363,7 +369,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
   }
   // Pages of a multiple of 64 keys hold whole tiles: one uniform page-table
   // read per tile, issued one DMA round ahead so its latency is hidden.
-  const bool tile_pages = VL && vl->page_table && vl->tile_pages;
+  constexpr bool tile_pages = VL && PG == 1;
   auto tile_page = [&](int t) -> long long {
     if (!tile_pages || t >= ntiles) return 0;
     const long long e = (long long)z * vl->pt_stride + (kbeg + t * ATT_BK) / vl->block_size;
@@ -400,8 +406,8 @@ __device__ __forceinline__ void attn_body(const AttnArgs& p, const VarlenArgs* v
       const char* src = base + key * stride + dcol[u];
       if constexpr (VL) {
         // page rows use K's row stride for K and V (flash_varlen_fwd_kernel.py:101-104)
-        if (tile_pages) src = base + page_shift + key * kstride + dcol[u];
-        else if (vl->page_table) src = base + 2 * paged_row(*vl, z, key, p.k_ss) + dcol[u];
+        if constexpr (PG == 1) src = base + page_shift + key * kstride + dcol[u];
+        else if constexpr (PG == 2) src = base + 2 * paged_row(*vl, z, key, p.k_ss) + dcol[u];
       }
       // instruction d = wave + u * NW fills 1 KiB at d * 1024 of the K tile,
       // or (d - DMAS) * 1024 of the V tile (the V slot pointer is pre-shifted)
@@ -976,7 +982,13 @@ __device__ __forceinline__ void attn_varlen_general_body(const AttnVarArgs& g) {
     g950::attn_body<D, F16, NW, false>(p, nullptr);                                    \
   }                                                                                     \
   extern "C" __global__ __launch_bounds__(NW * 64) void NAME##_varlen(const g950::AttnVarArgs p) { \
-    g950::attn_body<D, F16, NW, true>(p.a, &p.v);                                      \
+    g950::attn_body<D, F16, NW, true, 0>(p.a, &p.v);                                   \
+  }                                                                                     \
+  extern "C" __global__ __launch_bounds__(NW * 64) void NAME##_varlen_pt(const g950::AttnVarArgs p) { \
+    g950::attn_body<D, F16, NW, true, 1>(p.a, &p.v);                                   \
+  }                                                                                     \
+  extern "C" __global__ __launch_bounds__(NW * 64) void NAME##_varlen_pl(const g950::AttnVarArgs p) { \
+    g950::attn_body<D, F16, NW, true, 2>(p.a, &p.v);                                   \
   }
 // waves per workgroup (32 queries each); the launcher reads the workgroup
 // size back from the kernel's launch bounds

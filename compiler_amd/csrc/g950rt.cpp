@@ -1411,8 +1411,11 @@ int op_flash_varlen(g950_module* m, const g950_view* views, uint32_t nviews, con
                     m8(a.k_sh) && m8(a.v_ss) && m8(a.v_sh) && a.o_ss % 4 == 0 && a.o_sh % 4 == 0 &&
                     m8(vl.q_bs) && m8(vl.k_bs) && m8(vl.v_bs) && vl.o_bs % 4 == 0 && (!paged || m8(vl.page_stride));
   if (mfma) {
+    // paging is compiled into the kernel: contiguous rows, pages of whole
+    // 64-key tiles, or a page-table read per DMA lane
     char name[64];
-    snprintf(name, sizeof name, "g950_attn_fwd_%s_d%lld_varlen", dt == G950_DTYPE_BFLOAT16 ? "bf16" : "f16", D);
+    snprintf(name, sizeof name, "g950_attn_fwd_%s_d%lld_varlen%s", dt == G950_DTYPE_BFLOAT16 ? "bf16" : "f16", D,
+             !paged ? "" : vl.tile_pages ? "_pt" : "_pl");
     const int threads = kernel_threads(m, name, 512);
     const int bq = threads / 2;
     va.a.nqb = (int)((SQ + bq - 1) / bq);

@@ -245,7 +245,11 @@ def test_flash_varlen_contract():
     a, meta = inputs.varlen_case(batches=3, max_q=64, max_k=200, h=4, hk=4, d=64, paged=True, block_size=16,
                                  causal=True, window_right=0)
     rc, name, err = varlen_validate(a, meta)
-    assert rc == 0 and name == "g950_attn_fwd_bf16_d64_varlen", err
+    assert rc == 0 and name == "g950_attn_fwd_bf16_d64_varlen_pl", err   # 16-key pages: per-lane lookups
+    a, meta = inputs.varlen_case(batches=3, max_q=64, max_k=200, h=4, hk=4, d=64, paged=True, block_size=64,
+                                 causal=True, window_right=0)
+    rc, name, err = varlen_validate(a, meta)
+    assert rc == 0 and name == "g950_attn_fwd_bf16_d64_varlen_pt", err   # whole-tile pages
     a, meta = inputs.varlen_case(strided=True, d=64)      # padded strides: not 16-byte multiples
     rc, name, err = varlen_validate(a, meta)
     assert rc == 0 and name == "g950_attn_varlen_general", err
