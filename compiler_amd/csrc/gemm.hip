@@ -84,10 +84,16 @@ __device__ __forceinline__ void dma16_asm(const char* sbase, uint32_t voff, uint
 }
 
 // Map the linear workgroup id to a (tile_m, tile_n): XCD-contiguous, then
-// grouped by 4 tile-rows.
+// grouped by 4 tile-rows.  The hardware deals workgroups round-robin over
+// the 8 XCDs, so XCD x runs ids x, x + 8, ...: it takes the contiguous run of
+// floor(total / 8) tiles (one more for x < total % 8) starting at
+// x * floor(total / 8) + min(x, total % 8).  Tile counts that are not a
+// multiple of 8 took ids in plain order before: 4097x11008x4096 (731 tiles)
+// 283 -> 268 us, the same bits.
 __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
-  if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+  const int x = pid & 7;
+  pid = x * (total >> 3) + min(x, total & 7) + (pid >> 3);
   const int group = 4;
   const int per_group = group * tiles_n;
   const int gid = pid / per_group;
