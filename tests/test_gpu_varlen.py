@@ -89,8 +89,15 @@ MFMA_CASES = {
 @pytest.mark.parametrize("dt", ["bfloat16", "float16"])
 @pytest.mark.parametrize("case", sorted(MFMA_CASES))
 def test_mfma_varlen_features(case, dt):
-    a, meta = inputs.varlen_case(**MFMA_CASES[case])
-    check(a, meta, dt, "g950_attn_fwd_")
+    """Every feature on the MFMA kernels; the paging mode is compiled into
+    the kernel: contiguous rows (`_varlen`), pages of whole 64-key tiles
+    (`_varlen_pt`), other page sizes (`_varlen_pl`)."""
+    c = MFMA_CASES[case]
+    a, meta = inputs.varlen_case(**c)
+    suffix = "" if not c.get("paged") else "_pt" if c["block_size"] % 64 == 0 else "_pl"
+    name = f"g950_attn_fwd_{'bf16' if dt == 'bfloat16' else 'f16'}_d{c['d']}_varlen{suffix}"
+    check(a, meta, dt, name)
+    assert rt.module().last_kernel == name
 
 
 def test_general_kernel_features_fp32():
