@@ -788,6 +788,23 @@ def test_gemm_staged_epilogue_matches_row_stores(m, n, k):
         both(lambda out: ops.matmul_i8_dequant_kernel(a8, b8.t(), sa, sb, out, m, n, k), "bfloat16", name)
 
 
+def test_gemm_random_shapes_sweep():
+    """Sixteen seeded shapes of the 16x16-fragment kernel (M, N in 256..1300,
+    K a multiple of 64): tile counts that are and are not multiples of 8
+    (the XCD-contiguous tile order), bottom/right edge windows, both output
+    paths (16-byte aligned rows: staged; stride n + 1: row stores) bit-equal,
+    and every element against float64."""
+    rng = np.random.default_rng(2026)
+    for _ in range(16):
+        m, n = (int(v) for v in rng.integers(256, 1301, 2))
+        k = 64 * int(rng.integers(1, 9))
+        c3 = inputs.config3(m, n, k)
+        a, bt = dev(c3["a"], "bfloat16"), dev(c3["bt"], "bfloat16")
+        y = _staged_vs_row_stores(m, n, lambda out: ops.matmul_kernel(a, bt.t(), out, m, n, k), "bfloat16",
+                                  "g950_gemm_bf16_256x256")
+        close(host(y), ref.matmul(host(a), host(bt).T), 2e-2, 2e-2)
+
+
 def test_w8a16_staged_epilogue_matches_row_stores():
     """The widened W8A16 route (more 256x256 tiles than half the CUs: an
     exact bf16 copy of the int8 weights, then the bf16 GEMM with the column
