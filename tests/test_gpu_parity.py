@@ -999,6 +999,39 @@ def test_attention_config4_sampled_heads():
     close(host(o[:, :, 0]), np.repeat(c["v"][:, :, 0], 4, axis=1), 0, 1e-6)
 
 
+def climbing_scores(s, d):
+    """Q/K whose scores climb by about 16 log2 units per 64-key tile: every
+    query has a constant component that meets a key component growing with
+    the key index, so each row's maximum passes its running reference by more
+    than 8 on every tile it reads.  The online softmax then rescales l and O
+    and the two half-waves holding a query combine their tile maxima on every
+    tile; N(0,1) inputs move the reference on a row's first tile only."""
+    c = inputs.config4(1, 4, 2, s, d, seed=31)
+    q, k = c["q"].copy(), c["k"].copy()
+    q[..., 0] = 4.0
+    k[..., 0] = 0.5 * np.arange(s, dtype=np.float32)
+    return {**c, "q": inputs.bf16_round(q), "k": inputs.bf16_round(k)}
+
+
+@pytest.mark.parametrize("dt", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_reference_max_moves_every_tile(dt, d, causal):
+    c = climbing_scores(520, d)
+    q, k, v = (dev(c[n], dt) for n in ("q", "k", "v"))
+    o, lse = ops.attention(q, k, v, causal=causal, sync=True)
+    name = {"bfloat16": f"g950_attn_fwd_bf16_d{d}", "float16": f"g950_attn_fwd_f16_d{d}",
+            "float32": f"g950_attn_fwd_f32mfma_d{d}"}[dt]
+    assert rt.module().last_kernel == name
+    eo, el = ref.attention(host(q), host(k), host(v), c["scale"], causal=causal)
+    # fp32: the dot products reach ~1040 before scaling, so fp32 rounding of
+    # their partial sums alone moves the probabilities by ~1e-4 relative; a
+    # wrong rescale would miss by O(1)
+    bar = (1e-3, 1e-4) if dt == "float32" else (2e-2, 2e-2)
+    close(host(o), eo, *bar)
+    close(lse.cpu().numpy(), el, 1e-5 if dt == "float32" else 1e-4, 1e-4)
+
+
 @pytest.mark.parametrize("case", golden_cases("attention"))
 def test_attention_reference_fixture(case):
     b = load(case)
