@@ -259,6 +259,35 @@ def test_softmax_special_rows(dt, cols):
     close(y[fin], e[fin], *((1e-5, 1e-6) if dt == "float32" else (1e-2, 1e-2)))
 
 
+@pytest.mark.parametrize("dt", ["float32", "bfloat16"])
+def test_split_rows_softmax_special_rows(dt):
+    """The rows of test_softmax_special_rows at 70000 columns, which take the
+    two-launch split (1024-vector chunks merged per row): whole chunks of
+    -inf (rows 3 and 4), maxima in three different chunks (row 5), the +inf
+    entry in a middle chunk (row 2), and huge rows whose chunk sums merge
+    with unit rescale factors."""
+    cols = 70000
+    rng = np.random.default_rng(cols + 1)
+    x = rng.standard_normal((8, cols)).astype(np.float32)
+    x[0, :] = 3.0e38
+    x[1, :] = -3.0e38
+    x[2, cols // 2] = np.inf
+    x[3, :] = -np.inf
+    x[4, : cols // 3] = -np.inf
+    x[5, [0, cols // 2, cols - 1]] = 2.5e38
+    x[6, :] = 1.5e38 + 0.0 * x[6, :]
+    x[7, :] = 1.6e7 + 4.0 * x[7, :]
+    if dt == "bfloat16":
+        x = ref.bf16_round(x)
+    y = host(ops.softmax(dev(x, dt), sync=True)).astype(np.float64)
+    assert rt.module().last_kernel.startswith("g950_rs_final_softmax_")
+    e = ref.softmax(x)
+    assert np.array_equal(np.isnan(y), np.isnan(e))
+    assert np.isnan(y[[2, 3]]).all()
+    fin = ~np.isnan(e)
+    close(y[fin], e[fin], *((1e-5, 1e-6) if dt == "float32" else (1e-2, 1e-2)))
+
+
 def _dq_expect(b, s, dt):
     p = ref.dequantize(b, s)
     if dt == "bfloat16":
