@@ -388,6 +388,25 @@ def test_split_rows_all_reductions(rows, cols, dt):
     assert rel_err(host(rstd), es, 1e-30) <= 1e-5
 
 
+@pytest.mark.parametrize("rows,cols,kernel", [(64, 3000, "g950_r"), (4, 100000, "g950_rs_final_layernorm_")])
+def test_layernorm_large_mean_rows(rows, cols, kernel):
+    """fp32 rows of mean 1000 and unit spread, in the one-pass register
+    kernels and the split path (chunk moments merged per row): the centered
+    variance holds (a one-pass E[x^2] - E[x]^2 form misses by 10-100% here),
+    and the split's merge keeps Mean and Rstd.  Bar 1e-2 on Y: fp32 sums of
+    values near 1000 move the mean by ~1e-3 of the spread."""
+    rng = np.random.default_rng(rows + cols)
+    x = (1000.0 + rng.standard_normal((rows, cols))).astype(np.float32)
+    w = (rng.standard_normal(cols) * 0.5 + 1.0).astype(np.float32)
+    b = (rng.standard_normal(cols) * 0.1).astype(np.float32)
+    y, mean, rstd = ops.layernorm(dev(x), dev(w), dev(b), 1e-5, sync=True)
+    assert rt.module().last_kernel.startswith(kernel)
+    ey, em, es = ref.layernorm(x, w, b, 1e-5)
+    close(host(y), ey, 1e-2, 1e-2)
+    close(host(mean), em, 1e-5, 1e-6)
+    close(host(rstd), es, 1e-2, 0.0)
+
+
 def test_split_rows_guard_and_special_values():
     """Split path: outputs stay inside padded rows; logsumexp keeps the NaN /
     +inf / all -inf rules across chunks (the special value in a later chunk)."""
