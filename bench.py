@@ -738,6 +738,56 @@ def pmc_probe(torch, ops):
         "layernorm/softmax [8191,3001], split-row softmax [4,2^22], W8A16 decode 16/1 x 8192 x 8192: x8 each")
 
 
+def load_probe(torch, ops, which, seconds):
+    """Power/clock workload: one config's kernel back to back for `seconds`
+    (C4 causal attention, the C3 GEMM at 8192^3, or C2 softmax on six
+    rotating sets), so `amd-smi metric --power` / `rocm-smi --showclocks`
+    can sample the chip under it from another process.  Prints the launch
+    count and the mean launch time."""
+    from oracle import inputs
+    dev = "cuda:0"
+    if which == "attn":
+        c = inputs.config4()
+        bf = lambda x: torch.from_numpy(x).to(dev).to(torch.bfloat16)  # noqa: E731
+        q, k, v = bf(c["q"]), bf(c["k"]), bf(c["v"])
+        del c
+        o = torch.empty_like(q)
+        lse = torch.empty((4, 32, 4096), dtype=torch.float32, device=dev)
+        call = ops.attn_fwd_causal_kernel(q, k, v, o, 4, 32, 4096, 1 / math.sqrt(128), *q.stride(), *k.stride(),
+                                          *v.stride(), *o.stride(), CAUSAL=True, lse_ptr=lse, prepare=True)
+        launch = lambda i: call()  # noqa: E731
+    elif which == "gemm":
+        c = inputs.config3(8192, 8192, 8192)
+        a = torch.from_numpy(c["a"]).to(dev).to(torch.bfloat16)
+        bt = torch.from_numpy(c["bt"]).to(dev).to(torch.bfloat16)
+        del c
+        y = torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)
+        call = ops.matmul_kernel(a, bt.t(), y, 8192, 8192, 8192, prepare=True)
+        launch = lambda i: call()  # noqa: E731
+    elif which == "softmax":
+        xs = [torch.from_numpy(inputs.config2(8191, 3000, seed=inputs.SEEDS["c2"] + s)["x"]).to(dev)
+              .to(torch.bfloat16) for s in range(ROTATE)]
+        ys = [torch.empty_like(x) for x in xs]
+        calls = [ops.softmax_kernel(x, y, 3000, prepare=True) for x, y in zip(xs, ys)]
+        launch = lambda i: calls[i % ROTATE]()  # noqa: E731
+    else:
+        sys.exit(f"bench.py: --load takes attn, gemm or softmax (not {which!r})")
+    torch.cuda.synchronize()
+    log(f"load {which}: started, {seconds} s")
+    n, t_end = 0, time.perf_counter() + seconds
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            launch(n)
+            n += 1
+        torch.cuda.synchronize()
+    end.record()
+    end.synchronize()
+    print(json.dumps({"load": which, "seconds": seconds, "launches": n,
+                      "mean_us": round(start.elapsed_time(end) / n * 1e3, 2)}), flush=True)
+
+
 def mfma_probe(torch, ops):
     """Counter-collection workload for the MFMA-bound kernels (run under
     rocprofv3 --pmc): C3 bf16 GEMM 8192^3 and 4097x11008x4096, C4 causal GQA
@@ -817,6 +867,9 @@ def main():
                     help="run only the counter-collection workload (for rocprofv3 --pmc)")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="run only the GEMM + attention counter workload (for rocprofv3 --pmc)")
+    ap.add_argument("--load", default=None, choices=("attn", "gemm", "softmax"),
+                    help="run one config's kernel back to back for --seconds (power/clock sampling beside it)")
+    ap.add_argument("--seconds", type=float, default=10.0)
     ap.add_argument("--only", default=None,
                     help="comma-separated suite sections (" + ",".join(SECTIONS) + ", or 'headline'): run just "
                          "these, without the CPU legs, and print their rows (one rocprofv3 trace per config)")
@@ -835,6 +888,9 @@ def main():
         return
     if args.mfma_probe:
         mfma_probe(torch, ops)
+        return
+    if args.load:
+        load_probe(torch, ops, args.load, args.seconds)
         return
     if args.only:
         only = set(args.only.split(","))
