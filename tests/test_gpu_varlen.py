@@ -100,6 +100,46 @@ def test_mfma_varlen_features(case, dt):
     assert rt.module().last_kernel == name
 
 
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("dt", ["bfloat16", "float16"])
+def test_mfma_varlen_empty_sequences(dt, paged):
+    """Whole sequences without keys or queries on the MFMA kernels, inside
+    the contract that seqlen_q bounds every sequence's rows (the reference's
+    grid has ceil(seqlen_q / BLOCK_M) q-blocks, flash_varlen_fwd_kernel.py:470):
+    sequence 1 gets seqused_k = 0 (no key tile at all: every row O = 0,
+    LSE = +inf, :309-312); sequence 2 gets no queries (equal cu_seqlens_q
+    entries); sequence 3 keeps its 294 queries over 100 keys, so under the
+    bottom-right causal alignment its first 194 rows see no key; the rows
+    after cu_seqlens_q[-1] belong to no sequence and keep their initial
+    values (O -0.875, LSE -inf)."""
+    extra = dict(paged=True, block_size=64) if paged else {}
+    a, meta = inputs.varlen_case(batches=4, max_q=300, max_k=400, h=8, hk=2, d=128, seqused_trim=5,
+                                 causal=True, window_right=0, **extra)
+    a = dict(a)
+    used = a["seqused_k_ptr"].copy()
+    used[1] = 0
+    used[3] = 100
+    a["seqused_k_ptr"] = used
+    cu = a["cu_seqlens_q_ptr"].copy()
+    q3 = cu[4] - cu[3]
+    cu[3] = cu[2]
+    cu[4] = cu[2] + q3
+    a["cu_seqlens_q_ptr"] = cu
+    o, lse, eo, el = run(a, meta, dt)
+    assert rt.module().last_kernel.endswith("_varlen_pt" if paged else "_varlen"), rt.module().last_kernel
+    o3, l2 = o.reshape(-1, 8, 128), lse.reshape(8, -1)
+    assert np.all(o3[cu[1]:cu[2]] == 0.0)
+    assert np.all(np.isposinf(l2[:, cu[1]:cu[2]]))
+    assert int(np.isposinf(l2[:, cu[3]:cu[4]]).sum()) == 8 * 194
+    assert np.all(o3[cu[4]:] == -0.875) and np.all(np.isneginf(l2[:, cu[4]:]))
+    bar = BAR[dt]
+    ok, err = ref.isclose_verdict(o, eo, bar, bar)
+    assert ok, f"O max err {err}"
+    ok, err = ref.isclose_verdict(lse, el, bar, bar)
+    assert ok, f"LSE max err {err}"
+    assert np.array_equal(np.isinf(lse), np.isinf(el))
+
+
 def test_general_kernel_features_fp32():
     """The same features through the fp32 one-thread-per-row kernel."""
     for kw in (dict(causal=True, window_right=0), dict(local=True, window_left=3, window_right=2),
