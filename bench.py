@@ -743,7 +743,8 @@ def load_probe(torch, ops, which, seconds):
     (C4 causal attention, the C3 GEMM at 8192^3, or C2 softmax on six
     rotating sets), so `amd-smi metric --power` / `rocm-smi --showclocks`
     can sample the chip under it from another process.  Prints the launch
-    count and the mean launch time."""
+    count and the mean time per launch (host waits between ~8 ms batches
+    included)."""
     from oracle import inputs
     dev = "cuda:0"
     if which == "attn":
@@ -773,12 +774,14 @@ def load_probe(torch, ops, which, seconds):
     else:
         sys.exit(f"bench.py: --load takes attn, gemm or softmax (not {which!r})")
     torch.cuda.synchronize()
+    # host waits once per ~8 ms of queued work, so the GPU never idles long
+    batch = 400 if which == "softmax" else 16
     log(f"load {which}: started, {seconds} s")
     n, t_end = 0, time.perf_counter() + seconds
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     while time.perf_counter() < t_end:
-        for _ in range(20):
+        for _ in range(batch):
             launch(n)
             n += 1
         torch.cuda.synchronize()
