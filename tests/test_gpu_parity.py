@@ -177,6 +177,68 @@ def test_masked_row_vectors(rows, cols, pad, dt):
     gaps_intact(y)
 
 
+def test_row_reductions_random_shapes_sweep():
+    """Thirty-six seeded shapes through the row dispatcher of every row op:
+    row lengths log-uniform over 1..200000 (one-wave rows, whole-workgroup
+    rows, the split-row pair), up to ~3M elements, the three dtypes in turn,
+    and four layouts in turn: whole 16-byte vectors (length a multiple of
+    8) packed or with an aligned gap of 8..32 elements between rows, any
+    length packed, any length with a gap of 1..9 (rows off a 16-byte
+    boundary: the masked kernels); softmax, logsumexp, RMSNorm and LayerNorm
+    against float64 at the dtype's bar, the gap elements untouched, and
+    every kernel family of the dispatcher reached."""
+    rng = np.random.default_rng(4242)
+    ran = set()
+    for case in range(36):
+        dt = ("float32", "bfloat16", "float16")[case % 3]
+        layout = case % 4
+        cols = int(np.exp(rng.uniform(0, np.log(200000))))
+        if layout < 2:
+            cols = max(8, cols // 8 * 8)
+        rows = int(rng.integers(1, max(2, min(9000, 3_000_000 // cols)) + 1))
+        pad = (0, 8 * int(rng.integers(1, 5)), 0, int(rng.integers(1, 10)))[layout]
+        stride = cols + pad
+        tag = f"case {case}: {dt} rows {rows} cols {cols} stride {stride}"
+        c = inputs.config2(rows, stride, seed=100 + case)
+        xd = dev(c["x"], dt)[:, :cols]
+        xr = host(xd)
+        g, b = dev(c["gamma"][:cols], dt), dev(c["beta"][:cols], dt)
+        gr, br = host(g), host(b)
+        bar = (1e-5, 1e-6) if dt == "float32" else (1e-2, 1e-2)
+
+        def out():
+            return torch.full((rows, stride), -7.0, dtype=TD[dt], device=DEV)[:, :cols]
+
+        def checked(what, actual, expected, rtol, atol, y=None):
+            ran.add(rt.module().last_kernel)
+            ok, err = ref.isclose_verdict(actual, expected, rtol, atol)
+            assert ok, f"{tag}: {what} ({rt.module().last_kernel}) max abs err {err}"
+            if y is not None and pad:
+                full = torch.as_strided(y, (rows, stride), (stride, 1))
+                assert bool((full[:, cols:] == -7.0).all()), f"{tag}: {what} wrote between rows"
+
+        y = out()
+        ops.softmax_kernel(xd, y, cols, sync=True)
+        checked("softmax", host(y), ref.softmax(xr), *bar, y=y)
+        lse = torch.empty(rows, device=DEV)
+        ops.logsumexp_kernel(xd, lse, cols, sync=True)
+        checked("logsumexp", host(lse), ref.logsumexp(xr), 3e-5, 3e-6)
+        y, r = out(), torch.empty(rows, device=DEV)
+        ops.rms_layernorm_forward_kernel(y, stride, xd, stride, g, 1, r, 1, cols, 1e-6, sync=True)
+        ey, er = ref.rms_layernorm(xr, gr, 1e-6)
+        checked("rmsnorm", host(y), ey, *bar, y=y)
+        checked("rmsnorm r", host(r), er, 1e-5, 1e-6)
+        y, mean, rstd = ops.layernorm(xd, g, b, 1e-5, out=out(), sync=True)
+        ey, em, es = ref.layernorm(xr, gr, br, 1e-5)
+        checked("layernorm", host(y), ey, *(bar if dt != "float32" else (1e-5, 1e-5)), y=y)
+        checked("layernorm mean", host(mean), em, 1e-5, 1e-6)
+        assert rel_err(host(rstd), es, 1e-30) <= 1e-5, f"{tag}: layernorm rstd"
+    for family in ("g950_rr_", "g950_rw_", "g950_rm_", "g950_rs_final_"):
+        assert any(k.startswith(family) for k in ran), (family, sorted(ran))
+    assert any(k.startswith("g950_rs_final_") and not k.endswith("_v1") for k in ran), sorted(ran)
+    assert any(k.startswith("g950_rr_") and k.endswith("_b256") for k in ran), sorted(ran)
+
+
 @pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
 @pytest.mark.parametrize("rows,cols", [(4, 16), (4, 97), (64, 1024), (8191, 3000), (2, 100000)])
 def test_logsumexp(rows, cols, dt):
@@ -913,6 +975,33 @@ def test_attention_small(z, h, hkv, s, d, causal):
     eo, el = ref.attention(c["q"], c["k"], c["v"], c["scale"], causal=causal)
     close(host(o), eo, 2e-2, 2e-2)
     close(lse.cpu().numpy(), el, 1e-4, 1e-4)
+
+
+def test_attention_random_shapes_sweep():
+    """Twelve seeded shapes of the 16-bit MFMA attention kernels: sequence
+    lengths 1..900 (one or several 256-query blocks, the last key tile cut
+    anywhere), 1-3 batches, 1-2 KV heads with GQA groups 1, 2 or 4, head
+    dim 64 or 128, causal or not, bf16 and fp16 in turn; O and LSE against
+    float64 on the 16-bit-rounded inputs."""
+    rng = np.random.default_rng(777)
+    for case in range(12):
+        dt = ("bfloat16", "float16")[case % 2]
+        d = (64, 128)[int(rng.integers(0, 2))]
+        hkv = int(rng.integers(1, 3))
+        h = hkv * (1, 2, 4)[int(rng.integers(0, 3))]
+        z = int(rng.integers(1, 4))
+        s = int(rng.integers(1, 901))
+        causal = bool(rng.random() < 0.5)
+        tag = f"case {case}: {dt} z {z} h {h}/{hkv} s {s} d {d} causal {causal}"
+        c = inputs.config4(z, h, hkv, s, d, seed=500 + case)
+        q, k, v = (dev(c[n], dt) for n in ("q", "k", "v"))
+        o, lse = ops.attention(q, k, v, causal=causal, sync=True)
+        assert rt.module().last_kernel == f"g950_attn_fwd_{'bf16' if dt == 'bfloat16' else 'f16'}_d{d}", tag
+        eo, el = ref.attention(host(q), host(k), host(v), c["scale"], causal=causal)
+        ok, err = ref.isclose_verdict(host(o), eo, 2e-2, 2e-2)
+        assert ok, f"{tag}: O max abs err {err}"
+        ok, err = ref.isclose_verdict(lse.cpu().numpy(), el, 1e-4, 1e-4)
+        assert ok, f"{tag}: LSE max abs err {err}"
 
 
 @pytest.mark.parametrize("dt", ["bfloat16", "float16"])
