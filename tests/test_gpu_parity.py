@@ -635,6 +635,39 @@ def test_dequant_matmul_reference_weight_layout(m, n, k, dt):
     close(host(y), host(y2), 2e-2, 2e-2)
 
 
+def test_dequant_matmul_random_shapes_sweep():
+    """Sixteen seeded dequantize_matmul shapes over the routes of both weight
+    layouts: decode rows (M 1..64) and larger M (65..1200), N and K
+    multiples of 16 (N up to 4096, K up to 2048), K-contiguous int8 weights
+    and the reference's row-major [K, N] weights, bf16 and fp16 in turn;
+    every row against float64 a . (b * scale) on the rounded inputs (2e-2),
+    and the decode, fused and widened row-major-B kernel families reached."""
+    rng = np.random.default_rng(31337)
+    ran = set()
+    for case in range(16):
+        dt = ("bfloat16", "float16")[case % 2]
+        route = (case // 2) % 4
+        m = int(rng.integers(1, 65)) if route < 2 else int(rng.integers(65 if route == 2 else 256, 1201))
+        n = 16 * int(rng.integers(1 if route < 3 else 16, 257))
+        k = 64 * int(rng.integers(1, 33)) if route == 3 else 16 * int(rng.integers(1, 129))
+        rowmajor = route in (1, 3)
+        tag = f"case {case}: {dt} m {m} n {n} k {k} {'row-major' if rowmajor else 'K-contiguous'} weights"
+        a = rng.standard_normal((m, k)).astype(np.float32) * 0.5
+        b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+        s = (rng.random(n) / 64).astype(np.float32)
+        ad, sd = dev(a, dt), dev(s, dt)
+        bw = torch.from_numpy(b).to(DEV) if rowmajor else torch.from_numpy(np.ascontiguousarray(b.T)).to(DEV).t()
+        y = ops.dequant_matmul(ad, bw, sd, sync=True)
+        kern = rt.module().last_kernel
+        ran.add(kern)
+        expect = ref.matmul(host(ad), ref.dequantize(b, host(sd)))
+        ok, err = ref.isclose_verdict(host(y), expect, 2e-2, 2e-2)
+        assert ok, f"{tag}: {kern} max abs err {err}"
+    assert any(k.startswith("g950_gemm_w8a16_skinny") for k in ran), sorted(ran)
+    assert any(k.startswith("g950_gemm_w8a16_") and k.endswith("_128x128") for k in ran), sorted(ran)
+    assert any(k.endswith("_256x256_rb") for k in ran), sorted(ran)
+
+
 def test_dequant_matmul_general_layouts():
     """Row-major int8 b with rows that are not whole 16-byte vectors, fp32 a
     and a ragged K take the general kernel, same bar (fp32: 1e-4)."""
