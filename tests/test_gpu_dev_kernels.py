@@ -306,6 +306,33 @@ def test_int8_signedness_general_path(adt, bdt):
     assert np.array_equal(acc.cpu().numpy(), ref.wrap_i32(ref.matmul_i8(a, b)))
 
 
+def test_int8_random_shapes_sweep():
+    """Sixteen seeded int8 GEMMs: a random signedness pair each, M and N in
+    1..1300, K a multiple of 16 in 16..2048 (whole 128-byte slabs or a K
+    tail), K-contiguous or row-major B; every int32 element bit-exact against
+    the integer product narrowed modulo 2^32, with both the MFMA kernels and
+    the general kernel reached."""
+    rng = np.random.default_rng(8128)
+    ran = set()
+    for case in range(16):
+        adt, bdt = PAIRS[case % 4]
+        m, n = (int(v) for v in rng.integers(1, 1301, 2))
+        k = 16 * int(rng.integers(1, 129))
+        colb = bool(rng.random() < 0.75)
+        a = draw(rng, adt, (m, k))
+        b = draw(rng, bdt, (k, n))
+        ad = torch.from_numpy(a).to(DEV)
+        bd = torch.from_numpy(np.ascontiguousarray(b.T)).to(DEV).t() if colb else torch.from_numpy(b).to(DEV)
+        acc = torch.full((m, n), -7, dtype=torch.int32, device=DEV)
+        ops.matmul_i8_kernel(ad, bd, acc, m, n, k, sync=True)
+        ran.add(rt.module().last_kernel)
+        tag = f"case {case}: {adt} x {bdt} m {m} n {n} k {k} {'K-contiguous' if colb else 'row-major'} B"
+        exact = ref.wrap_i32(ref.matmul_i8(a, b))
+        assert np.array_equal(acc.cpu().numpy(), exact), f"{tag}: {rt.module().last_kernel}"
+    assert any(k.endswith("_256x256") or k.endswith("_256x256_kt") for k in ran), sorted(ran)
+    assert "g950_gemm_general_i8" in ran, sorted(ran)
+
+
 # ------------------------------------------- W8A16 widened-route edge cases
 @pytest.mark.parametrize("n,ydt", [(8003, "bfloat16"), (8192, "float32")])
 def test_dequant_matmul_widened_ragged_n_and_fp32_out(n, ydt):
