@@ -140,6 +140,49 @@ def test_mfma_varlen_empty_sequences(dt, paged):
     assert np.array_equal(np.isinf(lse), np.isinf(el))
 
 
+def test_mfma_varlen_random_sweep():
+    """Sixteen seeded varlen cases on the MFMA kernels: 1-4 sequences of up
+    to 700 queries and 900 keys, GQA 1/2/4 over 1-2 KV heads, head dim 64 or
+    128, and a random mix of the features -- causal, a local window (random
+    left/right sizes, some of them negative), paged K/V with 16-, 64- or
+    128-key pages, seqused_k trimming, fixed-length rows -- bf16 and fp16
+    in turn; O and LSE against the oracle at the case's bar, and all three
+    paging forms of the kernel reached."""
+    rng = np.random.default_rng(90210)
+    ran = set()
+    for case in range(16):
+        dt = ("bfloat16", "float16")[case % 2]
+        batches = int(rng.integers(1, 5))
+        max_q = int(rng.integers(2 * batches + 1, 701))
+        max_k = int(rng.integers(3 * batches + 1, 901))
+        hk = int(rng.integers(1, 3))
+        kw = dict(batches=batches, max_q=max_q, max_k=max_k, hk=hk, h=hk * (1, 2, 4)[int(rng.integers(0, 3))],
+                  d=(64, 128)[int(rng.integers(0, 2))], seed=1000 + case)
+        feature = int(rng.integers(0, 4))
+        if feature == 1:
+            kw.update(causal=True, window_right=0)
+        elif feature == 2:
+            kw.update(local=True, window_left=int(rng.integers(-50, 300)), window_right=int(rng.integers(-50, 300)))
+        elif feature == 3:
+            kw.update(var_q=False, var_k=False)
+        if feature != 3 and rng.random() < 0.5:
+            kw.update(paged=True, block_size=(16, 64, 128)[int(rng.integers(0, 3))])
+        if rng.random() < 0.3:
+            kw.update(seqused_trim=int(rng.integers(1, 3 * batches + 1)))
+        a, meta = inputs.varlen_case(**kw)
+        o, lse, eo, el = run(a, meta, dt)
+        kern = rt.module().last_kernel
+        ran.add(kern.split("_varlen")[-1])
+        tag = f"case {case}: {dt} {kw} ({kern})"
+        bar = BAR[dt]
+        ok, err = ref.isclose_verdict(o, eo, bar, bar)
+        assert ok, f"{tag}: O max err {err}"
+        ok, err = ref.isclose_verdict(lse, el, bar, bar)
+        assert ok, f"{tag}: LSE max err {err}"
+        assert np.array_equal(np.isinf(lse), np.isinf(el)), tag
+    assert {"", "_pt", "_pl"} <= ran, sorted(ran)
+
+
 def test_general_kernel_features_fp32():
     """The same features through the fp32 one-thread-per-row kernel."""
     for kw in (dict(causal=True, window_right=0), dict(local=True, window_left=3, window_right=2),
