@@ -766,6 +766,47 @@ def test_gemm_fp32_mfma(m, n, k, colb):
     close(y.cpu().numpy()[rows], ref.matmul(a[rows], bt.T), 1e-5, 1e-5 * np.sqrt(k))
 
 
+def test_gemm_layouts_random_sweep():
+    """Eighteen seeded GEMMs across the dispatcher: bf16, fp16 and fp32 in
+    turn, K-contiguous or the reference's row-major B, M and N in 1..1300,
+    K in 1..2048 (16-bit: half whole 64-k slabs, most of the rest multiples
+    of 8 with a tail, now and then any K); every element against float64 (16-bit 2e-2, fp32
+    1e-5 with the sqrt(K) absolute term), and the column-major, row-major,
+    K-tail and general kernels all reached."""
+    rng = np.random.default_rng(6502)
+    ran = set()
+    for case in range(18):
+        dt = ("bfloat16", "float16", "float32")[case % 3]
+        m, n = (int(v) for v in rng.integers(1, 1301, 2))
+        draw = rng.random()
+        if dt != "float32" and draw < 0.5:
+            k = 64 * int(rng.integers(1, 33))
+        elif dt != "float32" and draw < 0.85:
+            k = 8 * int(rng.integers(1, 257))
+        else:
+            k = int(rng.integers(1, 2049))
+        colb = bool(rng.random() < 0.5)
+        if not colb and dt != "float32" and rng.random() < 0.7:
+            n = max(8, n // 8 * 8)  # 16-byte B rows: the row-major MFMA kernel can read them as they lie
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        bt = rng.standard_normal((n, k)).astype(np.float32)
+        ad = dev(a, dt)
+        bd = dev(bt, dt).t() if colb else dev(np.ascontiguousarray(bt.T), dt)
+        y = torch.empty((m, n), dtype=TD[dt], device=DEV)
+        ops.matmul_kernel(ad, bd, y, m, n, k, sync=True)
+        kern = rt.module().last_kernel
+        ran.add(kern)
+        tag = f"case {case}: {dt} m {m} n {n} k {k} {'K-contiguous' if colb else 'row-major'} B ({kern})"
+        expect = ref.matmul(host(ad), host(bd))
+        bar = (1e-5, 1e-5 * np.sqrt(k)) if dt == "float32" else (2e-2, 2e-2)
+        ok, err = ref.isclose_verdict(host(y), expect, *bar)
+        assert ok, f"{tag}: max abs err {err}"
+    assert any(k.endswith("_256x256") for k in ran), sorted(ran)
+    assert any(k.endswith("_rb") for k in ran), sorted(ran)
+    assert any(k.endswith("_kt") for k in ran), sorted(ran)
+    assert any("general" in k for k in ran), sorted(ran)
+
+
 def test_gemm_fp32_ieee_exact_grid():
     """The reference's IEEE check (a100c/tests/test_matrix_breadth.py:454):
     operands on a 1/16 grid make every product and partial sum exact in fp32,
