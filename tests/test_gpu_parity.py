@@ -350,6 +350,24 @@ def test_split_rows_softmax_special_rows(dt):
     close(y[fin], e[fin], *((1e-5, 1e-6) if dt == "float32" else (1e-2, 1e-2)))
 
 
+def test_dequantize_random_sweep():
+    """Twelve seeded dequantize shapes, K in 1..3000 and N in 1..3000 (half
+    of them N a multiple of 8: the vector kernels; the rest any N: the
+    general kernel), the three output dtypes in turn; every element
+    bit-exact against the float64 product rounded once."""
+    rng = np.random.default_rng(4711)
+    for case in range(12):
+        dt = ("float32", "bfloat16", "float16")[case % 3]
+        k, n = (int(v) for v in rng.integers(1, 3001, 2))
+        if case % 2 == 0:
+            n = max(8, n // 8 * 8)
+        b = rng.integers(-127, 128, (k, n)).astype(np.int8)
+        sd = dev(rng.random(n).astype(np.float32), dt)
+        y = ops.dequantize(torch.from_numpy(b).to(DEV), sd, sync=True)
+        assert np.array_equal(host(y), _dq_expect(b, host(sd), dt)), \
+            f"case {case}: {dt} k {k} n {n} ({rt.module().last_kernel})"
+
+
 def _dq_expect(b, s, dt):
     p = ref.dequantize(b, s)
     if dt == "bfloat16":
@@ -1148,6 +1166,34 @@ def test_attention_fp32(z, h, hkv, s, d, causal):
     eo, el = ref.attention(c["q"], c["k"], c["v"], c["scale"], causal=causal)
     close(o.cpu().numpy(), eo, 1e-4, 1e-5)
     close(lse.cpu().numpy(), el, 1e-5, 1e-5)
+
+
+def test_attention_fp32_kernel_random_sweep():
+    """Ten seeded shapes of the fp32 MFMA attention kernel: fp32 inputs at
+    head dim 32, 64 or 128, and (three of the ten) 16-bit inputs at head dim
+    32, which that kernel also serves; sequence lengths 1..700, 1-2 batches,
+    GQA groups 1/2/4, causal or not.  fp32: O within 1e-4 / 1e-5 and LSE
+    within 1e-5 of float64; 16-bit: the 16-bit attention bars."""
+    rng = np.random.default_rng(1729)
+    for case in range(10):
+        dt = ("float32", "float32", "bfloat16", "float32", "float16")[case % 5] if case < 8 else "float32"
+        d = 32 if dt != "float32" else (32, 64, 128)[int(rng.integers(0, 3))]
+        hkv = int(rng.integers(1, 3))
+        h = hkv * (1, 2, 4)[int(rng.integers(0, 3))]
+        z = int(rng.integers(1, 3))
+        s_len = int(rng.integers(1, 701))
+        causal = bool(rng.random() < 0.5)
+        tag = f"case {case}: {dt} z {z} h {h}/{hkv} s {s_len} d {d} causal {causal}"
+        c = inputs.config4(z, h, hkv, s_len, d, seed=900 + case)
+        q, k, v = (dev(c[n], dt) for n in ("q", "k", "v"))
+        o, lse = ops.attention(q, k, v, causal=causal, sync=True)
+        assert rt.module().last_kernel == f"g950_attn_fwd_f32mfma_d{d}", (tag, rt.module().last_kernel)
+        eo, el = ref.attention(host(q), host(k), host(v), c["scale"], causal=causal)
+        bars = ((1e-4, 1e-5), (1e-5, 1e-5)) if dt == "float32" else ((2e-2, 2e-2), (1e-4, 1e-4))
+        ok, err = ref.isclose_verdict(host(o), eo, *bars[0])
+        assert ok, f"{tag}: O max abs err {err}"
+        ok, err = ref.isclose_verdict(lse.cpu().numpy(), el, *bars[1])
+        assert ok, f"{tag}: LSE max abs err {err}"
 
 
 @pytest.mark.parametrize("shift,d", [(1, 64), (2, 128), (1, 32)])
