@@ -243,6 +243,77 @@ def test_gqa_kernel_c4_scale():
             close(host(out[z, h]), eo[0, 0], 2e-2, 2e-2)
 
 
+# ------------------------------------------------- dev contracts, random
+def test_dev_contracts_random_sweep():
+    """Twenty-four seeded cases over the three dev-suite signatures, the
+    three dtypes in turn: softmax_kernel_inner with M rows of N in 1..5000
+    elements, TILE_N a power of two and ONE_TILE_PER_CTA either way (a
+    narrow one-tile case leaves the tail of each output row as it was);
+    _layer_norm_forward_row with 1..300 rows of 1..5000 (any width, so
+    aligned and masked rows) and statistics in X's dtype; gqa_kernel with
+    1-2 batches, GROUP 1/2/4, N_CTX 1..300 and head dim 32/64/128.  Bars as
+    in the fixed-shape tests above."""
+    rng = np.random.default_rng(2718)
+    for case in range(24):
+        dt = DTYPES[case % 3]
+        kind = (case // 3) % 3
+        rtol, atol = RED_BAR[dt]
+        if kind == 0:
+            m, n = int(rng.integers(1, 51)), int(rng.integers(1, 5001))
+            tile = 1 << int(rng.integers(4, 13))
+            one = bool(rng.random() < 0.5)
+            tag = f"case {case}: softmax_kernel_inner {dt} M {m} N {n} TILE_N {tile} one_tile {one}"
+            x = rounded(rng.normal(0, 2.0, m * n), dt)
+            before = np.full(m * n + 16, -7.0)
+            out = torch.full((m * n + 16,), -7.0, dtype=TD[dt], device=DEV)
+            ops.softmax_kernel_inner(out, dev(x, dt), m, n, tile, one, sync=True)
+            got = host(out)
+            expect = ref.softmax_inner(x, m, n, tile, one, out=before)
+            ok, err = ref.isclose_verdict(got[: m * n], expect, rtol, atol)
+            assert ok, f"{tag}: max abs err {err}"
+            assert np.all(got[m * n:] == -7.0), tag
+        elif kind == 1:
+            rows, cols = int(rng.integers(1, 301)), int(rng.integers(1, 5001))
+            tag = f"case {case}: _layer_norm_forward_row {dt} rows {rows} cols {cols}"
+            x, w, b = lnrow_case(rows, cols, dt, seed=3000 + case)
+            yd = torch.full((rows * cols,), -7.0, dtype=TD[dt], device=DEV)
+            md = torch.full((rows,), -7.0, dtype=TD[dt], device=DEV)
+            sd = torch.full((rows,), -7.0, dtype=TD[dt], device=DEV)
+            ops._layer_norm_forward_row(yd, cols, dev(x, dt), cols, dev(w, dt), dev(b, dt), md, 1, sd, 1, rows,
+                                        cols, 1e-5, cols, sync=True)
+            tag += f" ({rt.module().last_kernel})"
+            y, mean, rstd = host(yd).reshape(rows, cols), host(md), host(sd)
+            ey, em, es = ref.layernorm_row(x, w, b, 1e-5)
+            if dt == "float32":
+                # y = (x - mean) * rstd * w + b: where the two terms nearly
+                # cancel, fp32 rounding of each (~3e-8 near 0.5) is all that
+                # is left, so y takes the isclose form with atol 1e-6 (an fp32
+                # emulation of the same arithmetic reaches 3.6e-5 relative at
+                # |y| = 4e-4 on case 3); the statistics stay relative
+                ok, err = ref.isclose_verdict(y, ey, 1e-5, 1e-6)
+                assert ok, f"{tag}: y max abs err {err}"
+                for what, got, want, floor in (("mean", mean, em, 1e-3), ("rstd", rstd, es, 1e-30)):
+                    a, e = np.asarray(got, np.float64), np.asarray(want, np.float64)
+                    err = float((np.abs(a - e) / np.maximum(np.abs(e), floor)).max())
+                    assert err <= 1e-5, f"{tag}: {what} relative error {err}"
+            else:
+                for what, got, want in (("y", y, ey), ("mean", mean, em), ("rstd", rstd, es)):
+                    ok, err = ref.isclose_verdict(got, want, rtol, atol)
+                    assert ok, f"{tag}: {what} max abs err {err}"
+        else:
+            z, hkv = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+            group = (1, 2, 4)[int(rng.integers(0, 3))]
+            n, d = int(rng.integers(1, 301)), (32, 64, 128)[int(rng.integers(0, 3))]
+            hq = hkv * group
+            tag = f"case {case}: gqa_kernel {dt} z {z} heads {hq}/{hkv} n {n} d {d}"
+            q = rounded(rng.standard_normal((z, hq, n, d)), dt)
+            k = rounded(rng.standard_normal((z, hkv, n, d)), dt)
+            v = rounded(rng.standard_normal((z, hkv, n, d)), dt)
+            out, (qh, kh, vh), scale = run_gqa(q, k, v, dt, group)
+            ok, err = ref.isclose_verdict(host(out), ref.gqa(qh, kh, vh, scale, group), 2e-2, 2e-2)
+            assert ok, f"{tag}: max abs err {err}"
+
+
 # ------------------------------------------------ int8 signedness variants
 PAIRS = [("int8", "int8"), ("uint8", "uint8"), ("uint8", "int8"), ("int8", "uint8")]
 SHORT = {("int8", "int8"): "i8", ("uint8", "int8"): "u8s8", ("int8", "uint8"): "s8u8", ("uint8", "uint8"): "u8u8"}
